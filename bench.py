@@ -1,0 +1,146 @@
+#!/usr/bin/env python3
+"""Throughput of the fused forward+adjoint Monte-Carlo replay on one MI355X.
+
+Workload: arithmetic-average Asian call under GBM, 252 daily fixings, ATM 1y
+(S0=K=100, sigma=0.20, r=0.03, T=1), value + 5 first-order Greeks from one
+reverse sweep, 2,000,000 scenarios per step, Philox seed 42; the headline is
+fp64 and the fp32 run is reported beside it. A step is one replay (one
+dispatch through the C ABI: replay kernel, deterministic finishing kernel,
+sums copied back) over a fresh range of 2,000,000 scenarios; inputs are
+resident on the device before timing starts.
+
+Prints one JSON line. `roofline` prices the replay kernel against the VALU
+peak with the NT-FLOP v1 algorithmic count (nablatensor_amd/flops.py), using
+the kernel's own HIP-event duration on its stream. `cpu_baseline` times the
+CPU oracle (a C restatement of the reference's scalar `cpu` engine, OpenMP
+over contiguous path ranges) on this host on a bounded sample; the
+reference's Java engines cannot run here (no JDK).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+WORKLOAD = "Asian call, GBM, 252 fixings, ATM 1y, value + 5 Greeks"
+# Reference rocm engine, same tape/seed/2M scenarios, fp64, on a Radeon 780M
+# (gfx1103): docs/examples/asian-greeks.md:43 in the reference repository.
+REFERENCE_ROCM_FP64 = 2.16e6
+
+
+def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg):
+    from nablatensor_amd import flops
+
+    with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg)) as x:
+        info = x.info()
+        for w in range(warmup):
+            x.replay(paths, w * paths, seed)
+        replay_ms, kernel_ms = [], []
+        t0 = time.perf_counter()
+        for k in range(steps):
+            _, tm = x.replay(paths, (warmup + k) * paths, seed)
+            replay_ms.append(tm["replay_ms"])
+            kernel_ms.append(tm["kernel_ms"])
+        wall = time.perf_counter() - t0
+    fl = flops.flops_per_scenario(flat, precision)
+    avg_replay_s = sum(replay_ms) / len(replay_ms) / 1e3
+    achieved = fl * paths / avg_replay_s / 1e12
+    peak = flops.PEAK_TFLOPS[precision]
+    return {
+        "value": paths * steps / wall,
+        "ms_per_step": wall / steps * 1e3,
+        "kernel_ms": sum(kernel_ms) / len(kernel_ms),
+        "replay_kernel_ms": avg_replay_s * 1e3,
+        "kernel_scenarios_per_s": paths / avg_replay_s,
+        "roofline": {"bound": "valu", "kernel": "nt_replay", "achieved": achieved, "peak": peak,
+                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": None,
+                     "flops_per_scenario": fl, "convention": "NT-FLOP v1"},
+        "kernel": {k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
+                                        "loop_iters", "seg_len", "checkpoint", "tape_slots", "grid_cap")},
+    }
+
+
+def cpu_baseline(flat, sample, seed):
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.replay_sums(flat, 4096, 0, seed, threads=threads)  # load + warm
+    t0 = time.perf_counter()
+    oracle.replay_sums(flat, sample, 0, seed, threads=threads)
+    secs = time.perf_counter() - t0
+    return {"value": sample / secs, "unit": "scenarios/s", "cores": threads, "kind": "port",
+            "sample": f"{WORKLOAD}, fp64, {sample:,} scenarios, seed {seed}: C restatement of the reference "
+                      f"scalar cpu engine (oracle/nt_oracle.c), OpenMP, {secs:.2f} s; reference cpu-jit/simd "
+                      "not run (no JDK on this host)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--paths", type=int, default=2_000_000)
+    ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--policy", type=int, default=0, help="checkpoint policy (0 auto, 1 recompute, 2 store draws, 3 store all)")
+    ap.add_argument("--seg", type=int, default=0, help="loop iterations per checkpoint segment (0 auto)")
+    ap.add_argument("--cpu-sample", type=int, default=1_000_000)
+    ap.add_argument("--no-fp32", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (scenarios shard by path "
+              "range with one reduction of raw sums per GPU, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import nablatensor_amd as nt
+    from nablatensor_amd import rocm
+
+    if rocm.probe() < 1:
+        print("no gfx950 device visible", file=sys.stderr)
+        return 1
+    flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()
+    print(f"[bench] {WORKLOAD}: {len(flat['op'])} nodes, {args.paths:,} scenarios/step", file=sys.stderr, flush=True)
+    f64 = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg)
+    print(f"[bench] fp64 {f64['value']:.3e} scen/s", file=sys.stderr, flush=True)
+    f32 = None
+    if not args.no_fp32:
+        f32 = measure(rocm, flat, "fp32", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg)
+        print(f"[bench] fp32 {f32['value']:.3e} scen/s", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(flat, args.cpu_sample, args.seed)
+    out = {
+        "metric": "scenarios/sec for value+all Greeks (fp64), % of VALU FP64 peak",
+        "value": f64["value"],
+        "unit": "scenarios/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": f64["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": f64["value"] / REFERENCE_ROCM_FP64,
+        "baseline": "reference rocm engine fp64 on Radeon 780M (gfx1103), docs/examples/asian-greeks.md:43",
+        "dtype": "f64",
+        "data": "synthetic (Philox2x32-10 normals, seed 42)",
+        "config": {"workload": WORKLOAD, "scenarios_per_step": args.paths, "seed": args.seed,
+                   "nodes": len(flat["op"]), "steps": 252, "greeks": 5},
+        "roofline": f64["roofline"],
+        "kernel_ms": f64["kernel_ms"],
+        "replay_kernel_ms": f64["replay_kernel_ms"],
+        "kernel": f64["kernel"],
+        "fp32": None if f32 is None else {k: f32[k] for k in ("value", "ms_per_step", "replay_kernel_ms",
+                                                               "roofline", "kernel")},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,168 @@
+/*
+ * nablatensor_rocm.h — C ABI of the MI355X (gfx950) fused forward+adjoint
+ * Monte-Carlo tape-replay engine.
+ *
+ * This is the drop-in boundary behind the reference's `rocm` AadEngine. A Java
+ * adapter binds these symbols with java.lang.foreign downcalls exactly where
+ * the reference binds libamdhip64/libhiprtc (nablatensor-engine-rocm/src/main/
+ * java/com/nablatensor/backend/rocm/HipRuntime.java:79-125); a C++ host (this
+ * repository's nablatensor_amd/host) binds them the same way.
+ *
+ * Conventions: every entry point returns int status, NT_OK (0) on success;
+ * negative values are engine errors (NT_E_*), positive values are hipError_t
+ * or hiprtcResult codes passed through. nt_last_error() returns the message of
+ * the calling thread's last failure. Only plain pointers and sizes cross the
+ * boundary; the caller owns every array it passes and the engine keeps none of
+ * them past the call. An nt_exec is not thread-safe; use one per thread.
+ */
+#ifndef NABLATENSOR_ROCM_H
+#define NABLATENSOR_ROCM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NT_ABI_VERSION 1
+
+enum {
+  NT_OK = 0,
+  NT_E_INVALID = -1,      /* bad argument (IllegalArgumentException in the reference) */
+  NT_E_UNSUPPORTED = -2,  /* tape the engine declines (UnsupportedOperationException) */
+  NT_E_NO_DEVICE = -3,    /* no usable gfx950 device (IllegalStateException) */
+  NT_E_COMPILE = -4,      /* hipRTC compile failure; nt_last_error() carries the log */
+  NT_E_CLOSED = -5,       /* executable already destroyed (IllegalStateException) */
+  NT_E_INTERNAL = -6
+};
+
+/* Opcodes: AadOpEnum ordinals (nablatensor-core/.../engine/AadOpEnum.java:19-50). */
+enum {
+  NT_OP_CONST = 0, NT_OP_INPUT, NT_OP_RANDN, NT_OP_RANDU, NT_OP_ADD, NT_OP_SUB, NT_OP_MUL,
+  NT_OP_DIV, NT_OP_NEG, NT_OP_EXP, NT_OP_LOG, NT_OP_SQRT, NT_OP_MAX, NT_OP_MIN, NT_OP_ABS
+};
+
+/* A recorded tape as the flat arrays of FlatTape
+ * (nablatensor-core/.../engine/FlatTape.java:37-79) plus the random-stream
+ * counts of AadTape (AadTape.java:116-196). */
+typedef struct nt_tape {
+  int32_t n_nodes;
+  const int32_t *op;        /* opcode per node */
+  const int32_t *arg_a;     /* node index; input index (INPUT); draw ordinal (RANDN/RANDU) */
+  const int32_t *arg_b;     /* node index; stream index (RANDN/RANDU); -1 when unused */
+  const double *constant;   /* literal for CONST nodes */
+  int32_t n_inputs;
+  const int32_t *input_node;
+  int32_t n_outputs;
+  const int32_t *output_node;
+  int32_t n_streams;        /* random streams; this engine supports 1 */
+  int32_t n_uniforms;       /* RANDU draws; this engine supports 0 */
+} nt_tape;
+
+enum { NT_FP64 = 0, NT_FP32 = 1 };
+
+/* Reverse-sweep storage policy for a rolled step loop. */
+enum {
+  NT_CKPT_AUTO = 0,       /* cost model picks one of the below */
+  NT_CKPT_RECOMPUTE = 1,  /* carries checkpointed per segment; the reverse recomputes each segment */
+  NT_CKPT_STORE_DRAWS = 2,/* draw-derived (inactive) values stored; active values recomputed */
+  NT_CKPT_STORE_ALL = 3   /* every value the reverse reads is stored; nothing recomputed */
+};
+
+/* Options (AadOptions.java:42-156 precision/adjoints, plus the engine's own
+ * knobs that the reference passes as engineOptions). Zero means default. */
+typedef struct nt_options {
+  int32_t precision;        /* NT_FP64 or NT_FP32 */
+  int32_t adjoints;         /* 1: value + every first-order Greek; 0: price only */
+  int32_t block;            /* threads per block; 0 = 256 */
+  int32_t max_blocks;       /* grid cap; 0 = sized from occupancy */
+  int32_t checkpoint;       /* NT_CKPT_* */
+  int32_t seg_len;          /* loop iterations per checkpoint segment; 0 = cost model */
+  int32_t roll;             /* 1 (default): roll the step loop when one is found; -1: never */
+  int32_t reserved[9];
+} nt_options;
+
+typedef struct nt_exec nt_exec;
+
+/* Static facts about a compiled executable (for tests, reports and profiles). */
+typedef struct nt_exec_info {
+  int32_t n_nodes, n_active, n_inputs, n_channels;  /* channels = 2 + n_inputs (value, value^2, grads) */
+  int32_t loop_start, loop_period, loop_iters;      /* period 0: no rolled loop */
+  int32_t loop_carries, seg_len, n_segments;
+  int32_t checkpoint;                               /* resolved NT_CKPT_* */
+  int32_t tape_slots;                               /* stored values per path per run (fp64/fp32 elements) */
+  int32_t vgprs, sgprs, agprs;                      /* from the code object */
+  int32_t scratch_bytes;                            /* private segment per lane; 0 means no spill */
+  int32_t lds_bytes;
+  int32_t block, grid_cap;
+  double compile_seconds;
+} nt_exec_info;
+
+/* --- device ------------------------------------------------------------- */
+
+/* Count usable gfx950 devices; never fails for their absence (*count = 0).
+ * Replaces HipRuntime.probe / HipCompute.reliable (HipCompute.java:57-71). */
+int nt_probe(int32_t *count);
+
+/* Name and arch of device 0 ("AMD Instinct MI355X", "gfx950").
+ * Replaces HipCompute.deviceName/arch (HipCompute.java:73-95). */
+int nt_device_name(char *name, int32_t name_len, char *arch, int32_t arch_len);
+
+/* --- lowering (no device needed) ----------------------------------------- */
+
+/* Lower a tape to its HIP source text. *len in: buffer size; out: bytes needed
+ * including the terminator. Replaces CudaAadCodegen.generate
+ * (nablatensor-core/.../engine/CudaAadCodegen.java:42-102). */
+int nt_lower(const nt_tape *tape, const nt_options *options, char *source, int64_t *len);
+
+/* Lower and compile for gfx950 with hipRTC, without a device; fills *info with
+ * the loop plan and the code object's register/scratch usage. Used by build
+ * checks and to prefill the code-object cache. */
+int nt_compile_check(const nt_tape *tape, const nt_options *options, nt_exec_info *info);
+
+/* --- executables ---------------------------------------------------------- */
+
+/* Validate, lower, compile (hipRTC, gfx950) and load a tape. Replaces
+ * RocmAadEngine.compile -> DeviceAadExecutable.compile
+ * (RocmAadEngine.java:76-86, DeviceAadExecutable.java:107-119). */
+int nt_exec_create(const nt_tape *tape, const nt_options *options, nt_exec **out);
+
+/* Bind input values (n == tape n_inputs, input order). Replaces setInput +
+ * uploadDoubles (DeviceAadExecutable.java:134-137,148-151). */
+int nt_exec_set_inputs(nt_exec *exec, const double *inputs, int32_t n);
+
+/* One dispatch over paths [offset, offset + paths) with Philox seed `seed`.
+ * sums[0] = sum of the output, sums[1] = sum of its square, sums[2 + j] = sum
+ * of the adjoint of input j (zero when built price-only); n_sums must be
+ * 2 + n_inputs. timing (nullable) receives {kernel_ms, wall_ms}: kernel_ms from
+ * HIP events around the replay and finishing kernels on the executable's
+ * stream, wall_ms from entry to sums on the host. Replaces
+ * DeviceAadExecutable.replay (DeviceAadExecutable.java:139-168), returning raw
+ * sums instead of means so callers can combine dispatches exactly. */
+int nt_exec_replay(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed,
+                   double *sums, int32_t n_sums, double *timing);
+
+/* Per-path value and adjoints for paths [offset, offset + paths):
+ * values[p] and grads[p * n_inputs + j]. A testing aid with no counterpart in
+ * the reference; it runs the same lowered sweep with a per-path store. */
+int nt_exec_replay_paths(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed,
+                         double *values, double *grads);
+
+int nt_exec_info_get(const nt_exec *exec, nt_exec_info *info);
+
+/* Copy of the generated source (same *len protocol as nt_lower). */
+int nt_exec_source(const nt_exec *exec, char *source, int64_t *len);
+
+/* Free device buffers, the module and the stream. Replaces close()
+ * (DeviceAadExecutable.java:203-221). Null is a no-op. */
+int nt_exec_destroy(nt_exec *exec);
+
+/* Thread-local message of the last failure on this thread ("" if none). */
+const char *nt_last_error(void);
+
+int nt_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,790 @@
+// Tape -> HIP lowering; see lower.hpp for the structure of the emitted kernel.
+#include "lower.hpp"
+
+#include <algorithm>
+#include <cinttypes>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <sstream>
+
+namespace ntl {
+
+namespace {
+
+int arity(int op) {
+  switch (op) {
+    case NT_OP_CONST: case NT_OP_INPUT: case NT_OP_RANDN: case NT_OP_RANDU: return 0;
+    case NT_OP_NEG: case NT_OP_EXP: case NT_OP_LOG: case NT_OP_SQRT: case NT_OP_ABS: return 1;
+    default: return 2;
+  }
+}
+
+uint64_t bits(double v) {
+  uint64_t u;
+  std::memcpy(&u, &v, sizeof u);
+  return u;
+}
+
+}  // namespace
+
+// ---- validation (AadEngine.requireSupportedTape, AadEngine.java:56-86) ---------
+
+int build_ir(const nt_tape* t, TapeIR& ir, std::string& err) {
+  if (!t) { err = "tape is null"; return NT_E_INVALID; }
+  if (t->n_nodes <= 0 || !t->op || !t->arg_a || !t->arg_b || !t->constant) {
+    err = "tape has no nodes";
+    return NT_E_INVALID;
+  }
+  if (t->n_outputs < 1 || !t->output_node) { err = "no output was recorded"; return NT_E_INVALID; }
+  if (t->n_outputs > 1) {
+    err = "engine 'rocm' does not yet support multi-output tapes; use cpu-jit or cpu for this tape";
+    return NT_E_UNSUPPORTED;
+  }
+  if (t->n_streams > 1 || t->n_uniforms > 0) {
+    err = "engine 'rocm' does not yet support rec.randu() or named random streams; use cpu-jit or cpu for this tape";
+    return NT_E_UNSUPPORTED;
+  }
+  if (t->n_inputs < 0 || (t->n_inputs > 0 && !t->input_node)) { err = "bad input list"; return NT_E_INVALID; }
+  const int n = t->n_nodes;
+  ir.n = n;
+  ir.n_in = t->n_inputs;
+  ir.op.assign(t->op, t->op + n);
+  ir.a.assign(t->arg_a, t->arg_a + n);
+  ir.b.assign(t->arg_b, t->arg_b + n);
+  ir.c.assign(t->constant, t->constant + n);
+  ir.input_node.assign(t->input_node, t->input_node + t->n_inputs);
+  ir.output = t->output_node[0];
+  for (int i = 0; i < n; ++i) {
+    const int op = ir.op[i], a = ir.a[i], b = ir.b[i];
+    char buf[160];
+    if (op < NT_OP_CONST || op > NT_OP_ABS) {
+      std::snprintf(buf, sizeof buf, "node %d has unknown opcode %d", i, op);
+      err = buf;
+      return NT_E_INVALID;
+    }
+    if (op == NT_OP_RANDU || (op == NT_OP_RANDN && b != 0)) {
+      err = "engine 'rocm' does not yet support rec.randu() or named random streams; use cpu-jit or cpu for this tape";
+      return NT_E_UNSUPPORTED;
+    }
+    if (op == NT_OP_RANDN && a < 0) {
+      std::snprintf(buf, sizeof buf, "draw node %d has negative ordinal %d", i, a);
+      err = buf;
+      return NT_E_INVALID;
+    }
+    if (op == NT_OP_INPUT && (a < 0 || a >= ir.n_in || ir.input_node[a] != i)) {
+      std::snprintf(buf, sizeof buf, "input node %d has bad input index %d", i, a);
+      err = buf;
+      return NT_E_INVALID;
+    }
+    const int ar = arity(op);
+    if ((ar >= 1 && (a < 0 || a >= i)) || (ar >= 2 && (b < 0 || b >= i))) {
+      std::snprintf(buf, sizeof buf, "node %d reads a node that is not before it (%d, %d)", i, a, b);
+      err = buf;
+      return NT_E_INVALID;
+    }
+  }
+  for (int j = 0; j < ir.n_in; ++j) {
+    const int node = ir.input_node[j];
+    if (node < 0 || node >= n || ir.op[node] != NT_OP_INPUT || ir.a[node] != j) {
+      err = "input list does not match the INPUT nodes";
+      return NT_E_INVALID;
+    }
+  }
+  if (ir.output < 0 || ir.output >= n) { err = "output node out of range"; return NT_E_INVALID; }
+  ir.active.assign(n, 0);
+  for (int i = 0; i < n; ++i) {
+    const int op = ir.op[i];
+    if (op == NT_OP_INPUT) ir.active[i] = 1;
+    else if (op == NT_OP_CONST || op == NT_OP_RANDN || op == NT_OP_RANDU) ir.active[i] = 0;
+    else if (arity(op) == 1) ir.active[i] = ir.active[ir.a[i]];
+    else ir.active[i] = static_cast<uint8_t>(ir.active[ir.a[i]] || ir.active[ir.b[i]]);
+  }
+  return NT_OK;
+}
+
+// ---- loop detection ----------------------------------------------------------
+
+namespace {
+
+// Node k = i + P repeats node i: same op and literal, draw ordinal advanced by D,
+// each operand either shifted by P (same iteration / carried) or unchanged (invariant).
+bool repeats(const TapeIR& t, int i, int k, int P, int D) {
+  const int op = t.op[i];
+  if (op != t.op[k] || op == NT_OP_INPUT) return false;
+  if (op == NT_OP_CONST) return bits(t.c[i]) == bits(t.c[k]);
+  if (op == NT_OP_RANDN) return t.b[i] == t.b[k] && t.a[k] - t.a[i] == D;
+  const int ar = arity(op);
+  if (ar >= 1 && !(t.a[k] == t.a[i] + P || t.a[k] == t.a[i])) return false;
+  if (ar >= 2 && !(t.b[k] == t.b[i] + P || t.b[k] == t.b[i])) return false;
+  return true;
+}
+
+// Iteration [s0, s0+P) followed by [s1 = s0+P, ...): like repeats(), except a
+// carried operand of the later iteration may come from any node before s0 (the
+// carry's initial value).
+bool extends(const TapeIR& t, int s0, int P, int D) {
+  const int s1 = s0 + P;
+  for (int j = 0; j < P; ++j) {
+    const int i = s0 + j, k = s1 + j;
+    const int op = t.op[i];
+    if (op != t.op[k] || op == NT_OP_INPUT) return false;
+    if (op == NT_OP_CONST) { if (bits(t.c[i]) != bits(t.c[k])) return false; continue; }
+    if (op == NT_OP_RANDN) { if (t.b[i] != t.b[k] || t.a[k] - t.a[i] != D) return false; continue; }
+    const int ar = arity(op);
+    for (int slot = 0; slot < ar; ++slot) {
+      const int xk = slot == 0 ? t.a[k] : t.b[k];
+      const int xi = slot == 0 ? t.a[i] : t.b[i];
+      if (xk >= s1) { if (xi != xk - P) return false; }
+      else if (xk >= s0) { if (xi >= s0) return false; }
+      else if (xi != xk) return false;
+    }
+  }
+  return true;
+}
+
+enum { V_OK = 0, V_ITER0 = 1, V_EPI = 2, V_FAIL = 3 };
+
+int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
+  const int e = s + P * iters;
+  L = LoopPlan();
+  L.start = s; L.period = P; L.iters = iters; L.draws = D;
+  L.kind_a.assign(P, ARG_NONE); L.ref_a.assign(P, -1);
+  L.kind_b.assign(P, ARG_NONE); L.ref_b.assign(P, -1);
+  L.rand_base.assign(P, -1);
+  L.carry_init.assign(P, -1);
+  L.is_carry.assign(P, 0);
+  L.is_liveout.assign(P, 0);
+  // classes from iteration 1
+  const int s1 = s + P;
+  for (int j = 0; j < P; ++j) {
+    const int k = s1 + j;
+    const int ar = arity(t.op[k]);
+    for (int slot = 0; slot < ar; ++slot) {
+      const int x = slot == 0 ? t.a[k] : t.b[k];
+      int kind, ref;
+      if (x >= s1) { kind = ARG_BODY; ref = x - s1; if (ref >= j) return V_FAIL; }
+      else if (x >= s) { kind = ARG_CARRY; ref = x - s; }
+      else { kind = ARG_INV; ref = x; }
+      (slot == 0 ? L.kind_a : L.kind_b)[j] = kind;
+      (slot == 0 ? L.ref_a : L.ref_b)[j] = ref;
+      if (kind == ARG_CARRY) L.is_carry[ref] = 1;
+    }
+    if (t.op[s + j] == NT_OP_RANDN) { L.rand_base[j] = t.a[s + j]; if (L.rand_base[j] < 0) return V_FAIL; }
+  }
+  for (int it = 0; it < iters; ++it) {
+    const int fail = it == 0 ? V_ITER0 : V_FAIL;
+    for (int j = 0; j < P; ++j) {
+      const int i = s + it * P + j;
+      const int op = t.op[i];
+      if (op != t.op[s1 + j]) return fail;
+      if (op == NT_OP_CONST && bits(t.c[i]) != bits(t.c[s + j])) return fail;
+      if (op == NT_OP_INPUT) return fail;
+      if (op == NT_OP_RANDN && (t.b[i] != 0 || t.a[i] != L.rand_base[j] + it * D)) return fail;
+      const int ar = arity(op);
+      for (int slot = 0; slot < ar; ++slot) {
+        const int x = slot == 0 ? t.a[i] : t.b[i];
+        const int kind = (slot == 0 ? L.kind_a : L.kind_b)[j];
+        const int ref = (slot == 0 ? L.ref_a : L.ref_b)[j];
+        if (kind == ARG_BODY) {
+          if (x != s + it * P + ref) return fail;
+        } else if (kind == ARG_CARRY) {
+          if (it > 0) {
+            if (x != s + (it - 1) * P + ref) return fail;
+          } else {
+            if (x >= s) return V_ITER0;
+            if (L.carry_init[ref] == -1) L.carry_init[ref] = x;
+            else if (L.carry_init[ref] != x) return V_ITER0;
+          }
+        } else if (x != ref) {
+          return fail;
+        }
+      }
+    }
+  }
+  const int last = s + (iters - 1) * P;
+  for (int i = e; i < t.n; ++i) {
+    const int ar = arity(t.op[i]);
+    for (int slot = 0; slot < ar; ++slot) {
+      const int x = slot == 0 ? t.a[i] : t.b[i];
+      if (x >= s && x < e) {
+        if (x < last) return V_EPI;
+        L.is_liveout[x - last] = 1;
+      }
+    }
+  }
+  if (t.output >= s && t.output < e) {
+    if (t.output < last) return V_EPI;
+    L.is_liveout[t.output - last] = 1;
+  }
+  L.found = true;
+  return V_OK;
+}
+
+}  // namespace
+
+LoopPlan detect_loop(const TapeIR& t) {
+  std::vector<int> rp;
+  for (int i = 0; i < t.n; ++i) {
+    if (t.op[i] == NT_OP_RANDN) rp.push_back(i);
+  }
+  LoopPlan none;
+  if (rp.size() < 8) return none;
+  const int mid = static_cast<int>(rp.size()) / 2;
+  std::vector<std::pair<int, int>> cands;  // (P, D)
+  for (int m = 1; m <= 256 && mid + m < static_cast<int>(rp.size()); ++m) {
+    const int P = rp[mid + m] - rp[mid];
+    if (P * 4 > t.n) break;
+    bool seen = false;
+    for (auto& c : cands) seen |= c.first == P;
+    if (!seen) cands.push_back({P, m});
+  }
+  int bestX = -1, bestY = -1, bestP = 0, bestD = 0;
+  long bestCover = 0;
+  for (auto& cd : cands) {
+    const int P = cd.first, D = cd.second;
+    int runStart = -1;
+    for (int i = 0; i + P <= t.n; ++i) {
+      const bool ok = i + P < t.n && repeats(t, i, i + P, P, D);
+      if (ok && runStart < 0) runStart = i;
+      if (!ok && runStart >= 0) {
+        const int x = runStart, y = i;
+        const long cover = static_cast<long>((y + P - x) / P) * P;
+        if (cover > bestCover) { bestCover = cover; bestX = x; bestY = y; bestP = P; bestD = D; }
+        runStart = -1;
+      }
+    }
+  }
+  if (bestP == 0) return none;
+  const int P = bestP, D = bestD;
+  int s = bestX;
+  for (int j = 0; j < P && bestX + j < t.n; ++j) {
+    if (t.op[bestX + j] == NT_OP_RANDN) { s = bestX + j; break; }
+  }
+  int iters = (bestY + P - s) / P;
+  while (s - P >= 0 && extends(t, s - P, P, D)) { s -= P; ++iters; }
+  LoopPlan L;
+  for (int attempt = 0; attempt < 8 && iters >= 4; ++attempt) {
+    const int r = verify(t, s, P, iters, D, L);
+    if (r == V_OK) break;
+    if (r == V_EPI) { --iters; continue; }
+    if (r == V_ITER0) { s += P; --iters; continue; }
+    return none;
+  }
+  if (!L.found || iters < 4 || static_cast<long>(iters) * P < 32) return none;
+  return L;
+}
+
+// ---- plan ----------------------------------------------------------------------
+
+int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err) {
+  nt_options o{};
+  if (opt) o = *opt;
+  p = Plan();
+  p.precision = o.precision == NT_FP32 ? NT_FP32 : NT_FP64;
+  if (o.precision != NT_FP32 && o.precision != NT_FP64) { err = "precision must be NT_FP64 or NT_FP32"; return NT_E_INVALID; }
+  p.adjoints = o.adjoints != 0;
+  p.block = o.block > 0 ? o.block : 256;
+  if (p.block % 64 != 0 || p.block > 1024) { err = "block must be a multiple of 64, at most 1024"; return NT_E_INVALID; }
+  p.n_channels = 2 + t.n_in;
+  if (o.checkpoint < NT_CKPT_AUTO || o.checkpoint > NT_CKPT_STORE_ALL) { err = "unknown checkpoint policy"; return NT_E_INVALID; }
+  if (o.seg_len < 0) { err = "seg_len must be >= 0"; return NT_E_INVALID; }
+  if (o.roll >= 0) p.loop = detect_loop(t);
+  if (!p.loop.found) return NT_OK;
+
+  LoopPlan& L = p.loop;
+  const int P = L.period, s = L.start;
+  p.taped.assign(P, 0);
+  p.stored.assign(P, 0);
+  p.store_index.assign(P, -1);
+  auto body_active = [&](int j) { return t.active[s + j] != 0; };
+  auto mark = [&](int kind, int ref) { if (kind == ARG_BODY || kind == ARG_CARRY) p.taped[ref] = 1; };
+  if (p.adjoints) {
+    for (int j = 0; j < P; ++j) {
+      if (!body_active(j)) continue;
+      const int op = t.op[s + j];
+      auto opActive = [&](int kind, int ref) {
+        if (kind == ARG_INV) return t.active[ref] != 0;
+        if (kind == ARG_BODY || kind == ARG_CARRY) return body_active(ref);
+        return false;
+      };
+      const bool aa = opActive(L.kind_a[j], L.ref_a[j]);
+      const bool ba = opActive(L.kind_b[j], L.ref_b[j]);
+      switch (op) {
+        case NT_OP_MUL:
+          if (aa) mark(L.kind_b[j], L.ref_b[j]);
+          if (ba) mark(L.kind_a[j], L.ref_a[j]);
+          break;
+        case NT_OP_DIV:
+          mark(L.kind_b[j], L.ref_b[j]);
+          if (ba) p.taped[j] = 1;
+          break;
+        case NT_OP_EXP: case NT_OP_SQRT: p.taped[j] = 1; break;
+        case NT_OP_LOG: case NT_OP_ABS: mark(L.kind_a[j], L.ref_a[j]); break;
+        case NT_OP_MAX: case NT_OP_MIN:
+          mark(L.kind_a[j], L.ref_a[j]);
+          mark(L.kind_b[j], L.ref_b[j]);
+          break;
+        default: break;
+      }
+    }
+  }
+  for (int j = 0; j < P; ++j) {
+    if (L.is_carry[j]) p.carries.push_back(j);
+  }
+  int ck = o.checkpoint;
+  // Inactive values that feed active body nodes (the draw-derived frontier).
+  std::vector<uint8_t> frontier(P, 0);
+  bool anyFrontier = false;
+  for (int j = 0; j < P && p.adjoints; ++j) {
+    if (!body_active(j)) continue;
+    for (int slot = 0; slot < arity(t.op[s + j]); ++slot) {
+      const int kind = slot == 0 ? L.kind_a[j] : L.kind_b[j];
+      const int ref = slot == 0 ? L.ref_a[j] : L.ref_b[j];
+      if ((kind == ARG_BODY || kind == ARG_CARRY) && !body_active(ref) && t.op[s + ref] != NT_OP_CONST) {
+        frontier[ref] = 1;
+        anyFrontier = true;
+      }
+    }
+  }
+  if (ck == NT_CKPT_AUTO) ck = anyFrontier ? NT_CKPT_STORE_DRAWS : NT_CKPT_RECOMPUTE;
+  if (!p.adjoints) ck = NT_CKPT_RECOMPUTE;
+  p.ckpt = ck;
+  if (p.adjoints && ck == NT_CKPT_STORE_DRAWS) {
+    p.stored = frontier;
+  } else if (p.adjoints && ck == NT_CKPT_STORE_ALL) {
+    for (int j = 0; j < P; ++j) p.stored[j] = p.taped[j] && t.op[s + j] != NT_OP_CONST;
+  }
+  for (int j = 0; j < P; ++j) {
+    if (p.stored[j]) p.store_index[j] = p.n_stored++;
+  }
+  // Iterations per segment: the recompute keeps every taped value of the
+  // segment in registers, so size it against a VGPR budget.
+  int taped = 0;
+  for (int j = 0; j < P; ++j) taped += p.taped[j];
+  const int w = p.precision == NT_FP64 ? 2 : 1;
+  int seg;
+  if (o.seg_len > 0) {
+    seg = o.seg_len;
+  } else if (!p.adjoints) {
+    seg = 4;
+  } else {
+    seg = std::max(1, 96 / std::max(1, taped * w));
+  }
+  seg = std::max(1, std::min({seg, L.iters, 64}));
+  if ((L.draws & 1) && (seg & 1)) seg = seg > 1 ? seg - 1 : 2;
+  seg = std::min(seg, L.iters);
+  if (o.seg_len <= 0) {
+    for (int cand = seg; cand >= std::max(1, seg / 2); --cand) {
+      if (L.iters % cand == 0 && (!(L.draws & 1) || !(cand & 1))) { seg = cand; break; }
+    }
+  }
+  if ((L.draws & 1) && (seg & 1)) {
+    err = "an odd seg_len needs an even number of draws per iteration";
+    return NT_E_INVALID;
+  }
+  p.seg = seg;
+  p.nseg_full = L.iters / seg;
+  p.tail = L.iters % seg;
+  const int segments = p.nseg_full + (p.tail ? 1 : 0);
+  p.ck_slots = p.adjoints ? segments * static_cast<int>(p.carries.size()) : 0;
+  p.tape_slots = p.ck_slots + L.iters * p.n_stored;
+  return NT_OK;
+}
+
+// ---- emission --------------------------------------------------------------------
+
+namespace {
+
+class Emitter {
+ public:
+  Emitter(const TapeIR& t, const Plan& p) : t_(t), p_(p), f32_(p.precision == NT_FP32), L_(p.loop) {}
+
+  std::string run();
+
+ private:
+  const TapeIR& t_;
+  const Plan& p_;
+  const bool f32_;
+  const LoopPlan& L_;
+  std::ostringstream o_;
+  std::map<int, std::string> pairs_;  // counter -> pair variable stem, per straight-line region
+
+  std::string lit(double v) const {
+    char buf[64];
+    if (f32_) {
+      float f = static_cast<float>(v);
+      if (std::isnan(f)) return "__builtin_nanf(\"\")";
+      if (std::isinf(f)) return f > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+      std::snprintf(buf, sizeof buf, "%af", static_cast<double>(f));
+    } else {
+      if (std::isnan(v)) return "__builtin_nan(\"\")";
+      if (std::isinf(v)) return v > 0 ? "__builtin_inf()" : "(-__builtin_inf())";
+      std::snprintf(buf, sizeof buf, "%a", v);
+    }
+    return std::string("(") + buf + ")";
+  }
+  std::string f(const char* name) const { return f32_ ? std::string(name) + "f" : std::string(name); }
+
+  std::string expr(int op, const std::string& x, const std::string& y, double c, int a) const {
+    switch (op) {
+      case NT_OP_CONST: return lit(c);
+      case NT_OP_INPUT: return "in" + std::to_string(a);
+      case NT_OP_ADD: return x + " + " + y;
+      case NT_OP_SUB: return x + " - " + y;
+      case NT_OP_MUL: return x + " * " + y;
+      case NT_OP_DIV: return x + " / " + y;
+      case NT_OP_NEG: return "-" + x;
+      case NT_OP_EXP: return f("exp") + "(" + x + ")";
+      case NT_OP_LOG: return f("log") + "(" + x + ")";
+      case NT_OP_SQRT: return f("sqrt") + "(" + x + ")";
+      case NT_OP_ABS: return f("fabs") + "(" + x + ")";
+      case NT_OP_MAX: return f("fmax") + "(" + x + ", " + y + ")";
+      case NT_OP_MIN: return f("fmin") + "(" + x + ", " + y + ")";
+      default: return "0";
+    }
+  }
+
+  // Reverse rule of one active node (CudaAadCodegen.java:386-448, ScalarReplay.java:129-166);
+  // Aa / Ab are empty when that operand is inactive.
+  void rev(const std::string& ind, int op, const std::string& Ai, const std::string& Vi, const std::string& Va,
+           const std::string& Vb, const std::string& Aa, const std::string& Ab) {
+    const std::string half = f32_ ? "0.5f" : "0.5";
+    const std::string zero = f32_ ? "0.0f" : "0.0";
+    switch (op) {
+      case NT_OP_ADD:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << ";\n";
+        if (!Ab.empty()) o_ << ind << Ab << " += " << Ai << ";\n";
+        break;
+      case NT_OP_SUB:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << ";\n";
+        if (!Ab.empty()) o_ << ind << Ab << " -= " << Ai << ";\n";
+        break;
+      case NT_OP_MUL:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << " * " << Vb << ";\n";
+        if (!Ab.empty()) o_ << ind << Ab << " += " << Ai << " * " << Va << ";\n";
+        break;
+      case NT_OP_DIV:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << " / " << Vb << ";\n";
+        if (!Ab.empty()) o_ << ind << Ab << " -= " << Ai << " * " << Vi << " / " << Vb << ";\n";
+        break;
+      case NT_OP_NEG:
+        if (!Aa.empty()) o_ << ind << Aa << " -= " << Ai << ";\n";
+        break;
+      case NT_OP_EXP:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << " * " << Vi << ";\n";
+        break;
+      case NT_OP_LOG:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << " / " << Va << ";\n";
+        break;
+      case NT_OP_SQRT:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Ai << " * " << half << " / " << Vi << ";\n";
+        break;
+      case NT_OP_ABS:
+        if (!Aa.empty()) o_ << ind << Aa << " += " << Va << " < " << zero << " ? -" << Ai << " : " << Ai << ";\n";
+        break;
+      case NT_OP_MAX:
+      case NT_OP_MIN: {
+        const std::string cmp = op == NT_OP_MAX ? " >= " : " <= ";
+        if (!Aa.empty()) o_ << ind << "if (" << Va << cmp << Vb << ") " << Aa << " += " << Ai << ";\n";
+        if (!Ab.empty()) o_ << ind << "if (!(" << Va << cmp << Vb << ")) " << Ab << " += " << Ai << ";\n";
+        break;
+      }
+      default: break;
+    }
+  }
+
+  // ---- straight-line regions ----
+  std::string vname(int node) const;        // forward value of a straight-line node or live-out
+  std::string dname(int node) const;        // adjoint of an active straight-line node or live-out
+  void line_forward(int lo, int hi);
+  void line_reverse(int lo, int hi);
+
+  // ---- loop ----
+  std::string body_value(int u, int kind, int ref, bool recompute) const;
+  void segment(int U, const std::string& sg, bool forward);
+  int draw_partner(int U, int rel, int& pu, int& pj) const;
+};
+
+std::string Emitter::vname(int node) const {
+  if (L_.found && node >= L_.start && node < L_.end()) {
+    return "st" + std::to_string(node - (L_.start + (L_.iters - 1) * L_.period));
+  }
+  return "v" + std::to_string(node);
+}
+
+std::string Emitter::dname(int node) const {
+  if (L_.found && node >= L_.start && node < L_.end()) {
+    return "gs" + std::to_string(node - (L_.start + (L_.iters - 1) * L_.period));
+  }
+  return "d" + std::to_string(node);
+}
+
+void Emitter::line_forward(int lo, int hi) {
+  pairs_.clear();
+  for (int i = lo; i < hi; ++i) {
+    const int op = t_.op[i];
+    if (op == NT_OP_RANDN) {
+      const int k = t_.a[i];
+      const int ctr = k >> 1;
+      auto it = pairs_.find(ctr);
+      std::string stem;
+      if (it == pairs_.end()) {
+        stem = "zl" + std::to_string(lo) + "_" + std::to_string(ctr);
+        o_ << "    real " << stem << "c, " << stem << "s;\n";
+        o_ << "    nt_normal_pair(rlo, rhi, " << ctr << "u, " << stem << "c, " << stem << "s);\n";
+        pairs_[ctr] = stem;
+      } else {
+        stem = it->second;
+      }
+      o_ << "    const real v" << i << " = " << stem << ((k & 1) ? "s" : "c") << ";\n";
+      continue;
+    }
+    const int ar = arity(op);
+    const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
+    const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
+    o_ << "    const real v" << i << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+  }
+}
+
+void Emitter::line_reverse(int lo, int hi) {
+  for (int i = hi - 1; i >= lo; --i) {
+    if (!t_.active[i]) continue;
+    const int op = t_.op[i];
+    const int ar = arity(op);
+    if (ar == 0) continue;
+    const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
+    const std::string Aa = t_.active[a] ? dname(a) : "";
+    const std::string Ab = (b >= 0 && t_.active[b]) ? dname(b) : "";
+    rev("    ", op, "d" + std::to_string(i), "v" + std::to_string(i), vname(a), b >= 0 ? vname(b) : "", Aa, Ab);
+  }
+}
+
+// Value of a body operand in iteration u of the current segment. Carried
+// operands of the first iteration come from the segment-start state (st* in
+// the forward pass, checkpoint k* in the recompute).
+std::string Emitter::body_value(int u, int kind, int ref, bool recompute) const {
+  if (kind == ARG_BODY) return "r" + std::to_string(u) + "_" + std::to_string(ref);
+  if (kind == ARG_CARRY) {
+    if (u > 0) return "r" + std::to_string(u - 1) + "_" + std::to_string(ref);
+    return (recompute ? "k" : "st") + std::to_string(ref);
+  }
+  return "v" + std::to_string(ref);
+}
+
+// Emits one segment of U iterations. `sg` is the segment index expression;
+// the iteration base is it0 = sg * SEG. forward: compute, store, advance the
+// state. !forward: recompute (reloading stored values), then reverse.
+void Emitter::segment(int U, const std::string& sg, bool forward) {
+  const int P = L_.period, s = L_.start, D = L_.draws;
+  const int NC = static_cast<int>(p_.carries.size());
+  const std::string ind = "      ";
+  o_ << "    {\n";
+  o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << p_.seg << "u;\n";
+  o_ << ind << "const nt_u32 kb = it0 * " << D << "u;\n";
+  const bool ckpt = p_.adjoints;
+  if (forward && ckpt) {
+    for (int ci = 0; ci < NC; ++ci) {
+      o_ << ind << "scratch[(nt_u64)((" << sg << ") * " << NC << "u + " << ci << "u) * T + tid] = st"
+         << p_.carries[ci] << ";\n";
+    }
+  }
+  if (!forward) {
+    for (int ci = 0; ci < NC; ++ci) {
+      o_ << ind << "const real k" << p_.carries[ci] << " = scratch[(nt_u64)((" << sg << ") * " << NC << "u + " << ci
+         << "u) * T + tid];\n";
+    }
+  }
+  // draws of this segment by relative ordinal, for pairing the two legs
+  std::map<int, std::string> pairs;
+  for (int u = 0; u < U; ++u) {
+    for (int j = 0; j < P; ++j) {
+      const int i = s + j;
+      const int op = t_.op[i];
+      const std::string name = "r" + std::to_string(u) + "_" + std::to_string(j);
+      const std::string slot = "(nt_u64)(" + std::to_string(p_.ck_slots) + "u + (it0 + " + std::to_string(u) + "u) * " +
+                               std::to_string(p_.n_stored) + "u + " + std::to_string(p_.store_index[j] < 0 ? 0 : p_.store_index[j]) +
+                               "u) * T + tid";
+      if (!forward && p_.stored[j]) {
+        o_ << ind << "const real " << name << " = scratch[" << slot << "];\n";
+        continue;
+      }
+      if (op == NT_OP_RANDN) {
+        const int rel = L_.rand_base[j] + u * D;
+        const int key = rel >> 1;
+        auto it = pairs.find(key);
+        std::string stem;
+        if (it == pairs.end()) {
+          stem = "zp" + std::to_string(key);
+          o_ << ind << "real " << stem << "c, " << stem << "s;\n";
+          o_ << ind << "nt_normal_pair(rlo, rhi, (kb >> 1) + " << key << "u, " << stem << "c, " << stem << "s);\n";
+          pairs[key] = stem;
+        } else {
+          stem = it->second;
+        }
+        o_ << ind << "const real " << name << " = " << stem << ((rel & 1) ? "s" : "c") << ";\n";
+      } else {
+        const int ar = arity(op);
+        const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], !forward) : "";
+        const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], !forward) : "";
+        o_ << ind << "const real " << name << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+      }
+      if (forward && p_.adjoints && p_.stored[j]) {
+        o_ << ind << "scratch[" << slot << "] = " << name << ";\n";
+      }
+    }
+  }
+  if (forward) {
+    for (int j = 0; j < P; ++j) {
+      if (L_.is_carry[j] || L_.is_liveout[j]) {
+        o_ << ind << "st" << j << " = r" << (U - 1) << "_" << j << ";\n";
+      }
+    }
+    o_ << "    }\n";
+    return;
+  }
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  for (int u = U - 1; u >= 0; --u) {
+    o_ << ind << "{\n";
+    const std::string in2 = ind + "  ";
+    for (int j = 0; j < P; ++j) {
+      if (!t_.active[s + j]) continue;
+      o_ << in2 << "real a" << j << " = " << ((L_.is_carry[j] || L_.is_liveout[j]) ? "gs" + std::to_string(j) : zero)
+         << ";\n";
+    }
+    for (int c : p_.carries) {
+      if (t_.active[s + c]) o_ << in2 << "real q" << c << " = " << zero << ";\n";
+    }
+    auto adj = [&](int kind, int ref) -> std::string {
+      if (kind == ARG_BODY) return t_.active[s + ref] ? "a" + std::to_string(ref) : "";
+      if (kind == ARG_CARRY) return t_.active[s + ref] ? "q" + std::to_string(ref) : "";
+      if (kind == ARG_INV) return t_.active[ref] ? "d" + std::to_string(ref) : "";
+      return "";
+    };
+    for (int j = P - 1; j >= 0; --j) {
+      if (!t_.active[s + j]) continue;
+      const int op = t_.op[s + j];
+      const int ar = arity(op);
+      if (ar == 0) continue;
+      const std::string Va = body_value(u, L_.kind_a[j], L_.ref_a[j], true);
+      const std::string Vb = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], true) : "";
+      rev(in2, op, "a" + std::to_string(j), "r" + std::to_string(u) + "_" + std::to_string(j), Va, Vb,
+          adj(L_.kind_a[j], L_.ref_a[j]), ar >= 2 ? adj(L_.kind_b[j], L_.ref_b[j]) : "");
+    }
+    for (int j = 0; j < P; ++j) {
+      if (!(L_.is_carry[j] || L_.is_liveout[j]) || !t_.active[s + j]) continue;
+      o_ << in2 << "gs" << j << " = " << (L_.is_carry[j] ? "q" + std::to_string(j) : zero) << ";\n";
+    }
+    o_ << ind << "}\n";
+  }
+  o_ << "    }\n";
+}
+
+std::string Emitter::run() {
+  const int n = t_.n;
+  const int nin = t_.n_in;
+  const int NCH = p_.n_channels;
+  const bool loop = L_.found;
+  const int ls = loop ? L_.start : n;
+  const int le = loop ? L_.end() : n;
+  o_ << "// generated by nablatensor_amd lowering: " << n << " nodes, " << nin << " inputs, "
+     << (loop ? "rolled loop" : "straight line") << "\n";
+  if (loop) {
+    o_ << "// loop: start " << L_.start << ", period " << L_.period << ", iterations " << L_.iters << ", draws/iter "
+       << L_.draws << ", segment " << p_.seg << " (" << p_.nseg_full << " full + tail " << p_.tail
+       << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
+  }
+  o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << "\n";
+  o_ << "#include \"nt_skeleton.h\"\n";
+  o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
+  o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block << ") void nt_replay(\n"
+     << "    const double* __restrict__ inputs, nt_u64 n_paths, nt_u64 path_offset, nt_u64 seed,\n"
+     << "    double* __restrict__ partials, real* __restrict__ scratch,\n"
+     << "    double* __restrict__ out_v, double* __restrict__ out_g) {\n";
+  o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
+  o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
+  o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
+  for (int j = 0; j < nin; ++j) o_ << "  const real in" << j << " = (real)inputs[" << j << "];\n";
+  o_ << "  double acc[" << NCH << "];\n";
+  o_ << "  for (int c = 0; c < " << NCH << "; ++c) acc[c] = 0.0;\n";
+  o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
+  o_ << "    const nt_u64 path = p + path_offset;\n";
+  o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
+  o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
+  // forward
+  line_forward(0, ls);
+  if (loop) {
+    for (int j = 0; j < L_.period; ++j) {
+      if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
+      o_ << "    real st" << j << " = "
+         << (L_.is_carry[j] ? "v" + std::to_string(L_.carry_init[j]) : std::string(f32_ ? "0.0f" : "0.0")) << ";\n";
+    }
+    if (p_.nseg_full > 0) {
+      o_ << "    for (nt_u32 sg = 0; sg < " << p_.nseg_full << "u; ++sg)\n";
+      segment(p_.seg, "sg", true);
+    }
+    if (p_.tail) segment(p_.tail, std::to_string(p_.nseg_full) + "u", true);
+    line_forward(le, n);
+  }
+  const std::string y = vname(t_.output);
+  o_ << "    const double y = (double)" << y << ";\n";
+  o_ << "    acc[0] += y;\n    acc[1] += y * y;\n";
+  if (p_.adjoints) {
+    const std::string zero = f32_ ? "0.0f" : "0.0";
+    const std::string one = f32_ ? "1.0f" : "1.0";
+    for (int i = 0; i < ls; ++i) {
+      if (t_.active[i]) o_ << "    real d" << i << " = " << zero << ";\n";
+    }
+    if (loop) {
+      for (int j = 0; j < L_.period; ++j) {
+        if ((L_.is_carry[j] || L_.is_liveout[j]) && t_.active[L_.start + j]) o_ << "    real gs" << j << " = " << zero << ";\n";
+      }
+      for (int i = le; i < n; ++i) {
+        if (t_.active[i]) o_ << "    real d" << i << " = " << zero << ";\n";
+      }
+    }
+    if (t_.active[t_.output]) {
+      o_ << "    " << dname(t_.output) << " = " << one << ";\n";
+      if (loop) line_reverse(le, n);
+      if (loop) {
+        if (p_.tail) segment(p_.tail, std::to_string(p_.nseg_full) + "u", false);
+        if (p_.nseg_full > 0) {
+          o_ << "    for (int sgi = " << (p_.nseg_full - 1) << "; sgi >= 0; --sgi)\n";
+          segment(p_.seg, "(nt_u32)sgi", false);
+        }
+        for (int c : p_.carries) {
+          const int init = L_.carry_init[c];
+          if (t_.active[L_.start + c] && init >= 0 && t_.active[init]) o_ << "    d" << init << " += gs" << c << ";\n";
+        }
+      }
+      line_reverse(0, ls);
+    }
+    for (int j = 0; j < nin; ++j) {
+      const int node = t_.input_node[j];
+      o_ << "    acc[" << 2 + j << "] += (double)" << (t_.active[t_.output] ? dname(node) : "0.0") << ";\n";
+    }
+  }
+  o_ << "#ifdef NT_DUMP_PATHS\n";
+  o_ << "    out_v[p] = y;\n";
+  for (int j = 0; j < nin; ++j) {
+    const int node = t_.input_node[j];
+    o_ << "    out_g[p * " << nin << "u + " << j << "u] = "
+       << (p_.adjoints && t_.active[t_.output] ? "(double)" + dname(node) : "0.0") << ";\n";
+  }
+  o_ << "#endif\n";
+  o_ << "  }\n";
+  o_ << "  __shared__ double nt_lds[" << NCH << " * (" << p_.block << " / 64)];\n";
+  o_ << "  nt_block_store<" << NCH << ">(acc, partials, nt_lds);\n";
+  o_ << "}\n";
+  return o_.str();
+}
+
+}  // namespace
+
+std::string emit_source(const TapeIR& ir, const Plan& plan) {
+  Emitter e(ir, plan);
+  return e.run();
+}
+
+}  // namespace ntl

@@ -1,0 +1,74 @@
+// Tape -> HIP lowering for the fused forward+adjoint replay kernel.
+//
+// Replaces the reference's CudaAadCodegen (nablatensor-core/.../engine/
+// CudaAadCodegen.java:42-448) and its opt-in AadCheckpointPlan
+// (AadCheckpointPlan.java:95-172). Instead of unrolling every node, the
+// lowering finds the per-step loop of a Monte-Carlo tape (the role of the
+// cpu-jit engine's detectLoop, nablatensor-engine-cpu/.../jit/
+// KernelGenerator.java:549-658) and emits the step body once per segment of
+// SEG unrolled iterations:
+//   forward:  prologue; NSEG segments (carries checkpointed at each segment
+//             start, optionally some body values stored); epilogue
+//   reverse:  epilogue adjoints; segments last to first, each recomputing its
+//             forward in registers (stored values are reloaded instead) and
+//             then sweeping its iterations backwards; prologue adjoints.
+// The adjoint accumulation order equals the oracle's node order, so fp64
+// paths agree to rounding (FMA contraction aside).
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "nablatensor_rocm.h"
+
+namespace ntl {
+
+// Validated copy of a tape with activity (AadTape.markActive, AadTape.java:70-81).
+struct TapeIR {
+  int n = 0, n_in = 0, output = -1;
+  std::vector<int32_t> op, a, b;
+  std::vector<double> c;
+  std::vector<int32_t> input_node;
+  std::vector<uint8_t> active;
+};
+
+// Operand classes of a body node, relative to its own iteration.
+enum { ARG_NONE = 0, ARG_BODY = 1, ARG_CARRY = 2, ARG_INV = 3 };
+
+struct LoopPlan {
+  bool found = false;
+  int start = 0, period = 0, iters = 0;
+  int draws = 0;                      // RANDN nodes per iteration
+  std::vector<int> kind_a, ref_a;     // per body position
+  std::vector<int> kind_b, ref_b;
+  std::vector<int> rand_base;         // RANDN ordinal in iteration 0, -1 otherwise
+  std::vector<int> carry_init;        // init node of a carried position, -1 otherwise
+  std::vector<uint8_t> is_carry;      // read as carry-in by the next iteration
+  std::vector<uint8_t> is_liveout;    // read by the epilogue from the last iteration
+  int end() const { return start + period * iters; }
+};
+
+struct Plan {
+  int precision = NT_FP64;
+  int adjoints = 1;
+  int block = 256;
+  LoopPlan loop;
+  int seg = 0, nseg_full = 0, tail = 0;   // iterations per segment, full segments, tail iterations
+  int ckpt = NT_CKPT_RECOMPUTE;           // resolved policy
+  std::vector<uint8_t> taped;             // body value read by the reverse (in-body or as carry-in)
+  std::vector<uint8_t> stored;            // body value stored per iteration
+  std::vector<int> store_index;           // position -> index among stored, -1 otherwise
+  std::vector<int> carries;               // carried positions (checkpointed)
+  int n_stored = 0;
+  int ck_slots = 0, tape_slots = 0;       // per-thread scratch slots
+  int n_channels = 0;                     // 2 + n_inputs
+};
+
+// Returns NT_OK or an NT_E_* code with a message in err.
+int build_ir(const nt_tape* tape, TapeIR& ir, std::string& err);
+LoopPlan detect_loop(const TapeIR& ir);
+int make_plan(const TapeIR& ir, const nt_options* opt, Plan& plan, std::string& err);
+std::string emit_source(const TapeIR& ir, const Plan& plan);
+
+}  // namespace ntl

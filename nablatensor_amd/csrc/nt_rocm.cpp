@@ -1,0 +1,502 @@
+// C-ABI implementation (include/nablatensor_rocm.h) over the HIP runtime and
+// hipRTC. Replaces the reference's FFM runtime surface (nablatensor-engine-rocm/
+// .../backend/rocm/HipRuntime.java:79-446, HipCompute.java:26-125) and the
+// device executable (nablatensor-core/.../engine/DeviceAadExecutable.java:43-222).
+#include "nablatensor_rocm.h"
+
+#include <amd_comgr/amd_comgr.h>
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "lower.hpp"
+#include "skeleton_src.inc"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  std::ostringstream s;
+  s << what << " failed: " << hipGetErrorString(e) << " (code " << static_cast<int>(e) << ")";
+  return fail(static_cast<int>(e), s.str());
+}
+
+#define NT_HIP(call, what)                       \
+  do {                                           \
+    hipError_t e_ = (call);                      \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+const char* kArch = "gfx950";
+
+// ---- code-object cache ---------------------------------------------------------
+
+uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
+  for (unsigned char ch : s) {
+    h ^= ch;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+std::string cache_dir() {
+  const char* env = std::getenv("NABLATENSOR_ROCM_CACHE");
+  if (env && std::strcmp(env, "off") == 0) return "";
+  if (env && *env) return env;
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&cache_dir), &info) && info.dli_fname) {
+    std::string path(info.dli_fname);
+    size_t slash = path.rfind('/');
+    if (slash != std::string::npos) return path.substr(0, slash) + "/_kcache";
+  }
+  return "";
+}
+
+bool read_file(const std::string& path, std::vector<char>& out) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) return false;
+  out.assign(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+  return !out.empty();
+}
+
+void write_file_atomic(const std::string& path, const std::vector<char>& data) {
+  const std::string tmp = path + ".tmp" + std::to_string(reinterpret_cast<uintptr_t>(&data));
+  {
+    std::ofstream f(tmp, std::ios::binary);
+    if (!f) return;
+    f.write(data.data(), static_cast<std::streamsize>(data.size()));
+  }
+  std::rename(tmp.c_str(), path.c_str());
+}
+
+std::vector<std::string> compile_options(bool dump) {
+  std::vector<std::string> o = {std::string("--offload-arch=") + kArch, "-O3", "-std=c++17",
+                                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  if (dump) o.push_back("-DNT_DUMP_PATHS=1");
+  return o;
+}
+
+int compile_hiprtc(const std::string& src, bool dump, std::vector<char>& code, double& seconds) {
+  const auto t0 = std::chrono::steady_clock::now();
+  const std::vector<std::string> opts = compile_options(dump);
+  int major = 0, minor = 0;
+  hiprtcVersion(&major, &minor);
+  std::string key = src + "\n#opts";
+  for (auto& o : opts) key += " " + o;
+  key += "\n#hiprtc " + std::to_string(major) + "." + std::to_string(minor) + "\n";
+  key += NT_SKELETON_SRC;
+  char hex[32];
+  std::snprintf(hex, sizeof hex, "%016llx", static_cast<unsigned long long>(fnv1a(key)));
+  const std::string dir = cache_dir();
+  const std::string path = dir.empty() ? "" : dir + "/" + hex + ".co";
+  if (!path.empty() && read_file(path, code)) {
+    seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    return NT_OK;
+  }
+  hiprtcProgram prog;
+  const char* hdr_src[] = {NT_SKELETON_SRC};
+  const char* hdr_name[] = {"nt_skeleton.h"};
+  hiprtcResult r = hiprtcCreateProgram(&prog, src.c_str(), "nt_replay.hip", 1, hdr_src, hdr_name);
+  if (r != HIPRTC_SUCCESS) return fail(static_cast<int>(r), std::string("hiprtcCreateProgram failed: ") + hiprtcGetErrorString(r));
+  std::vector<const char*> copts;
+  for (auto& o : opts) copts.push_back(o.c_str());
+  r = hiprtcCompileProgram(prog, static_cast<int>(copts.size()), copts.data());
+  if (r != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    return fail(NT_E_COMPILE, "hipRTC compile failed: " + std::string(hiprtcGetErrorString(r)) + "\n" + log);
+  }
+  size_t size = 0;
+  hiprtcGetCodeSize(prog, &size);
+  code.resize(size);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  if (!path.empty()) {
+    mkdir(dir.c_str(), 0755);
+    write_file_atomic(path, code);
+  }
+  seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  return NT_OK;
+}
+
+// ---- code-object metadata (register and scratch evidence, no device needed) ----
+
+bool meta_string(amd_comgr_metadata_node_t node, std::string& out) {
+  size_t n = 0;
+  if (amd_comgr_get_metadata_string(node, &n, nullptr) != AMD_COMGR_STATUS_SUCCESS) return false;
+  out.assign(n, '\0');
+  if (amd_comgr_get_metadata_string(node, &n, &out[0]) != AMD_COMGR_STATUS_SUCCESS) return false;
+  while (!out.empty() && out.back() == '\0') out.pop_back();
+  return true;
+}
+
+int meta_int(amd_comgr_metadata_node_t map, const char* key) {
+  amd_comgr_metadata_node_t v;
+  if (amd_comgr_metadata_lookup(map, key, &v) != AMD_COMGR_STATUS_SUCCESS) return -1;
+  std::string s;
+  bool ok = meta_string(v, s);
+  amd_comgr_destroy_metadata(v);
+  return ok ? std::atoi(s.c_str()) : -1;
+}
+
+void kernel_resources(const std::vector<char>& code, const char* kernel, nt_exec_info& info) {
+  info.vgprs = info.sgprs = info.agprs = info.scratch_bytes = info.lds_bytes = -1;
+  amd_comgr_data_t data;
+  if (amd_comgr_create_data(AMD_COMGR_DATA_KIND_EXECUTABLE, &data) != AMD_COMGR_STATUS_SUCCESS) return;
+  amd_comgr_set_data(data, code.size(), code.data());
+  amd_comgr_metadata_node_t meta;
+  if (amd_comgr_get_data_metadata(data, &meta) == AMD_COMGR_STATUS_SUCCESS) {
+    amd_comgr_metadata_node_t kernels;
+    if (amd_comgr_metadata_lookup(meta, "amdhsa.kernels", &kernels) == AMD_COMGR_STATUS_SUCCESS) {
+      size_t count = 0;
+      amd_comgr_get_metadata_list_size(kernels, &count);
+      for (size_t k = 0; k < count; ++k) {
+        amd_comgr_metadata_node_t km;
+        if (amd_comgr_index_list_metadata(kernels, k, &km) != AMD_COMGR_STATUS_SUCCESS) continue;
+        amd_comgr_metadata_node_t nm;
+        std::string name;
+        if (amd_comgr_metadata_lookup(km, ".name", &nm) == AMD_COMGR_STATUS_SUCCESS) {
+          meta_string(nm, name);
+          amd_comgr_destroy_metadata(nm);
+        }
+        if (name == kernel) {
+          info.vgprs = meta_int(km, ".vgpr_count");
+          info.sgprs = meta_int(km, ".sgpr_count");
+          info.agprs = meta_int(km, ".agpr_count");
+          info.scratch_bytes = meta_int(km, ".private_segment_fixed_size");
+          info.lds_bytes = meta_int(km, ".group_segment_fixed_size");
+        }
+        amd_comgr_destroy_metadata(km);
+      }
+      amd_comgr_destroy_metadata(kernels);
+    }
+    amd_comgr_destroy_metadata(meta);
+  }
+  amd_comgr_release_data(data);
+}
+
+// ---- lowering shared by nt_lower / nt_compile_check / nt_exec_create ------------
+
+struct Lowered {
+  ntl::TapeIR ir;
+  ntl::Plan plan;
+  std::string source;
+};
+
+int lower(const nt_tape* tape, const nt_options* opt, Lowered& out) {
+  std::string err;
+  int rc = ntl::build_ir(tape, out.ir, err);
+  if (rc != NT_OK) return fail(rc, err);
+  rc = ntl::make_plan(out.ir, opt, out.plan, err);
+  if (rc != NT_OK) return fail(rc, err);
+  out.source = ntl::emit_source(out.ir, out.plan);
+  return NT_OK;
+}
+
+void fill_static_info(const Lowered& l, nt_exec_info& info) {
+  int active = 0;
+  for (uint8_t a : l.ir.active) active += a;
+  info.n_nodes = l.ir.n;
+  info.n_active = active;
+  info.n_inputs = l.ir.n_in;
+  info.n_channels = l.plan.n_channels;
+  const auto& L = l.plan.loop;
+  info.loop_start = L.found ? L.start : 0;
+  info.loop_period = L.found ? L.period : 0;
+  info.loop_iters = L.found ? L.iters : 0;
+  info.loop_carries = static_cast<int32_t>(l.plan.carries.size());
+  info.seg_len = l.plan.seg;
+  info.n_segments = l.plan.nseg_full + (l.plan.tail ? 1 : 0);
+  info.checkpoint = L.found ? l.plan.ckpt : 0;
+  info.tape_slots = l.plan.tape_slots;
+  info.block = l.plan.block;
+}
+
+int copy_out(const std::string& s, char* buf, int64_t* len) {
+  if (!len) return fail(NT_E_INVALID, "len is null");
+  const int64_t need = static_cast<int64_t>(s.size()) + 1;
+  if (buf && *len >= need) std::memcpy(buf, s.c_str(), static_cast<size_t>(need));
+  const bool fits = buf && *len >= need;
+  *len = need;
+  return (buf && !fits) ? fail(NT_E_INVALID, "buffer too small") : NT_OK;
+}
+
+int device_index(int& dev) {
+  int count = 0;
+  if (nt_probe(&count) != NT_OK || count == 0) {
+    return fail(NT_E_NO_DEVICE, "no ROCm/HIP gfx950 device available for the AAD replay kernel");
+  }
+  NT_HIP(hipGetDevice(&dev), "hipGetDevice");
+  return NT_OK;
+}
+
+}  // namespace
+
+struct nt_exec {
+  Lowered low;
+  nt_exec_info info{};
+  std::vector<char> code;
+  hipModule_t mod = nullptr, mod_dump = nullptr;
+  hipFunction_t fn = nullptr, fn_finish = nullptr, fn_dump = nullptr;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  double* d_inputs = nullptr;
+  double* d_partials = nullptr;
+  double* d_sums = nullptr;
+  void* d_scratch = nullptr;
+  int dev = 0;
+  int grid_cap = 1;
+  std::vector<double> inputs;
+  bool dirty = true;
+};
+
+extern "C" {
+
+int nt_abi_version(void) { return NT_ABI_VERSION; }
+
+const char* nt_last_error(void) { return g_err.c_str(); }
+
+int nt_probe(int32_t* count) {
+  if (!count) return fail(NT_E_INVALID, "count is null");
+  *count = 0;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return NT_OK;
+  }
+  int usable = 0;
+  for (int d = 0; d < n; ++d) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, d) != hipSuccess) continue;
+    if (std::strncmp(prop.gcnArchName, kArch, std::strlen(kArch)) == 0) ++usable;
+  }
+  *count = usable;
+  return NT_OK;
+}
+
+int nt_device_name(char* name, int32_t name_len, char* arch, int32_t arch_len) {
+  int dev = 0;
+  int rc = device_index(dev);
+  if (rc != NT_OK) return rc;
+  hipDeviceProp_t prop;
+  NT_HIP(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+  if (name && name_len > 0) std::snprintf(name, static_cast<size_t>(name_len), "%s", prop.name);
+  if (arch && arch_len > 0) std::snprintf(arch, static_cast<size_t>(arch_len), "%s", prop.gcnArchName);
+  return NT_OK;
+}
+
+int nt_lower(const nt_tape* tape, const nt_options* options, char* source, int64_t* len) {
+  Lowered l;
+  int rc = lower(tape, options, l);
+  if (rc != NT_OK) return rc;
+  return copy_out(l.source, source, len);
+}
+
+int nt_compile_check(const nt_tape* tape, const nt_options* options, nt_exec_info* info) {
+  Lowered l;
+  int rc = lower(tape, options, l);
+  if (rc != NT_OK) return rc;
+  std::vector<char> code;
+  double secs = 0;
+  rc = compile_hiprtc(l.source, false, code, secs);
+  if (rc != NT_OK) return rc;
+  if (info) {
+    *info = nt_exec_info{};
+    fill_static_info(l, *info);
+    kernel_resources(code, "nt_replay", *info);
+    info->compile_seconds = secs;
+  }
+  return NT_OK;
+}
+
+int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out) {
+  if (!out) return fail(NT_E_INVALID, "out is null");
+  *out = nullptr;
+  std::unique_ptr<nt_exec> x(new nt_exec());
+  int rc = lower(tape, options, x->low);
+  if (rc != NT_OK) return rc;
+  rc = device_index(x->dev);
+  if (rc != NT_OK) return rc;
+  double secs = 0;
+  rc = compile_hiprtc(x->low.source, false, x->code, secs);
+  if (rc != NT_OK) return rc;
+  fill_static_info(x->low, x->info);
+  kernel_resources(x->code, "nt_replay", x->info);
+  x->info.compile_seconds = secs;
+  NT_HIP(hipModuleLoadData(&x->mod, x->code.data()), "hipModuleLoadData");
+  NT_HIP(hipModuleGetFunction(&x->fn, x->mod, "nt_replay"), "hipModuleGetFunction(nt_replay)");
+  NT_HIP(hipModuleGetFunction(&x->fn_finish, x->mod, "nt_finish"), "hipModuleGetFunction(nt_finish)");
+  int per_cu = 0, cus = 0;
+  NT_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, x->fn, x->low.plan.block, 0),
+         "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+  NT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, x->dev), "hipDeviceGetAttribute");
+  const nt_options o = options ? *options : nt_options{};
+  x->grid_cap = std::max(1, per_cu * cus);
+  if (o.max_blocks > 0) x->grid_cap = o.max_blocks;
+  x->info.grid_cap = x->grid_cap;
+  NT_HIP(hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  for (auto& e : x->ev) NT_HIP(hipEventCreate(&e), "hipEventCreate");
+  const int nch = x->low.plan.n_channels;
+  NT_HIP(hipMalloc(&x->d_inputs, sizeof(double) * std::max(1, x->low.ir.n_in)), "hipMalloc(inputs)");
+  NT_HIP(hipMalloc(&x->d_partials, sizeof(double) * static_cast<size_t>(x->grid_cap) * nch), "hipMalloc(partials)");
+  NT_HIP(hipMalloc(&x->d_sums, sizeof(double) * nch), "hipMalloc(sums)");
+  const size_t elem = x->low.plan.precision == NT_FP32 ? sizeof(float) : sizeof(double);
+  const size_t scratch = static_cast<size_t>(x->low.plan.tape_slots) * x->grid_cap * x->low.plan.block * elem;
+  if (scratch > 0) NT_HIP(hipMalloc(&x->d_scratch, scratch), "hipMalloc(scratch)");
+  // inputs default to zero until bound; the reference starts from the recorded values (Java side)
+  x->inputs.assign(static_cast<size_t>(x->low.ir.n_in), 0.0);
+  for (int j = 0; j < x->low.ir.n_in; ++j) x->inputs[j] = x->low.ir.c[x->low.ir.input_node[j]];
+  *out = x.release();
+  return NT_OK;
+}
+
+int nt_exec_set_inputs(nt_exec* x, const double* inputs, int32_t n) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  if (n != x->low.ir.n_in || (n > 0 && !inputs)) return fail(NT_E_INVALID, "expected one value per tape input");
+  x->inputs.assign(inputs, inputs + n);
+  x->dirty = true;
+  return NT_OK;
+}
+
+static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v,
+                         double* out_g, int& grid) {
+  const int block = x->low.plan.block;
+  const uint64_t need = (paths + static_cast<uint64_t>(block) - 1) / static_cast<uint64_t>(block);
+  grid = static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap)));
+  grid = std::max(grid, 1);
+  if (x->dirty) {
+    if (!x->inputs.empty()) {
+      NT_HIP(hipMemcpyAsync(x->d_inputs, x->inputs.data(), sizeof(double) * x->inputs.size(), hipMemcpyHostToDevice,
+                            x->stream),
+             "hipMemcpyAsync(inputs)");
+    }
+    x->dirty = false;
+  }
+  void* args[] = {&x->d_inputs, &paths, &offset, &seed, &x->d_partials, &x->d_scratch, &out_v, &out_g};
+  NT_HIP(hipModuleLaunchKernel(fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0, x->stream,
+                               args, nullptr),
+         "hipModuleLaunchKernel(nt_replay)");
+  return NT_OK;
+}
+
+int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, double* sums, int32_t n_sums,
+                   double* timing) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  if (paths == 0) return fail(NT_E_INVALID, "paths must be positive");
+  const int nch = x->low.plan.n_channels;
+  if (!sums || n_sums != nch) return fail(NT_E_INVALID, "sums must hold 2 + n_inputs doubles");
+  const auto t0 = std::chrono::steady_clock::now();
+  NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
+  NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");
+  int grid = 0;
+  int rc = launch_replay(x, x->fn, paths, offset, seed, nullptr, nullptr, grid);
+  if (rc != NT_OK) return rc;
+  NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
+  unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
+  void* fargs[] = {&x->d_partials, &blocks, &nchu, &x->d_sums};
+  NT_HIP(hipModuleLaunchKernel(x->fn_finish, 1, 1, 1, 256, 1, 1, 0, x->stream, fargs, nullptr),
+         "hipModuleLaunchKernel(nt_finish)");
+  NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
+  NT_HIP(hipMemcpyAsync(sums, x->d_sums, sizeof(double) * nch, hipMemcpyDeviceToHost, x->stream), "hipMemcpyAsync(sums)");
+  NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  if (timing) {
+    float all = 0, rep = 0;
+    NT_HIP(hipEventElapsedTime(&all, x->ev[0], x->ev[2]), "hipEventElapsedTime");
+    NT_HIP(hipEventElapsedTime(&rep, x->ev[0], x->ev[1]), "hipEventElapsedTime");
+    timing[0] = all;
+    timing[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    timing[2] = rep;
+  }
+  return NT_OK;
+}
+
+int nt_exec_replay_paths(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, double* values, double* grads) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  if (paths == 0) return fail(NT_E_INVALID, "paths must be positive");
+  if (!values) return fail(NT_E_INVALID, "values is null");
+  const int nin = x->low.ir.n_in;
+  if (nin > 0 && !grads) return fail(NT_E_INVALID, "grads is null");
+  NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
+  if (!x->mod_dump) {
+    std::vector<char> code;
+    double secs = 0;
+    int rc = compile_hiprtc(x->low.source, true, code, secs);
+    if (rc != NT_OK) return rc;
+    NT_HIP(hipModuleLoadData(&x->mod_dump, code.data()), "hipModuleLoadData(dump)");
+    NT_HIP(hipModuleGetFunction(&x->fn_dump, x->mod_dump, "nt_replay"), "hipModuleGetFunction(dump)");
+  }
+  double* d_v = nullptr;
+  double* d_g = nullptr;
+  NT_HIP(hipMalloc(&d_v, sizeof(double) * paths), "hipMalloc(values)");
+  hipError_t e = hipMalloc(&d_g, sizeof(double) * paths * static_cast<uint64_t>(std::max(1, nin)));
+  if (e != hipSuccess) {
+    (void)hipFree(d_v);
+    return hip_fail(e, "hipMalloc(grads)");
+  }
+  int grid = 0;
+  int rc = launch_replay(x, x->fn_dump, paths, offset, seed, d_v, d_g, grid);
+  if (rc == NT_OK) {
+    e = hipMemcpyAsync(values, d_v, sizeof(double) * paths, hipMemcpyDeviceToHost, x->stream);
+    if (e == hipSuccess && nin > 0) {
+      e = hipMemcpyAsync(grads, d_g, sizeof(double) * paths * nin, hipMemcpyDeviceToHost, x->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(x->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "replay_paths copy-back");
+  }
+  (void)hipFree(d_v);
+  (void)hipFree(d_g);
+  return rc;
+}
+
+int nt_exec_info_get(const nt_exec* x, nt_exec_info* info) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  if (!info) return fail(NT_E_INVALID, "info is null");
+  *info = x->info;
+  return NT_OK;
+}
+
+int nt_exec_source(const nt_exec* x, char* source, int64_t* len) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  return copy_out(x->low.source, source, len);
+}
+
+int nt_exec_destroy(nt_exec* x) {
+  if (!x) return NT_OK;
+  if (x->stream) (void)hipStreamSynchronize(x->stream);
+  for (auto& e : x->ev) {
+    if (e) (void)hipEventDestroy(e);
+  }
+  if (x->stream) (void)hipStreamDestroy(x->stream);
+  if (x->d_scratch) (void)hipFree(x->d_scratch);
+  if (x->d_sums) (void)hipFree(x->d_sums);
+  if (x->d_partials) (void)hipFree(x->d_partials);
+  if (x->d_inputs) (void)hipFree(x->d_inputs);
+  if (x->mod_dump) (void)hipModuleUnload(x->mod_dump);
+  if (x->mod) (void)hipModuleUnload(x->mod);
+  delete x;
+  return NT_OK;
+}
+
+}  // extern "C"

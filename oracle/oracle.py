@@ -1,0 +1,138 @@
+"""ctypes wrapper of the CPU oracle (libnt_oracle.so) — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module. It restates the reference's scalar `cpu` engine (see nt_oracle.h
+for the file:line each function follows) and is the checker for the HIP engine,
+never a fallback for it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libnt_oracle.so"
+
+
+class _Tape(C.Structure):
+    _fields_ = [("n", C.c_int32), ("op", C.POINTER(C.c_int32)), ("arg_a", C.POINTER(C.c_int32)),
+                ("arg_b", C.POINTER(C.c_int32)), ("constant", C.POINTER(C.c_double)), ("n_inputs", C.c_int32),
+                ("input_node", C.POINTER(C.c_int32)), ("n_outputs", C.c_int32),
+                ("output_node", C.POINTER(C.c_int32)), ("n_streams", C.c_int32)]
+
+
+class _Totals(C.Structure):
+    _fields_ = [("value", C.POINTER(C.c_double)), ("sumsq", C.POINTER(C.c_double)),
+                ("gradient", C.POINTER(C.c_double))]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+        L = C.CDLL(str(LIB_PATH))
+        L.nto_philox2x32_10.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint32)]
+        L.nto_normal.argtypes = [C.c_uint64, C.c_uint64, C.c_int32, C.c_int32]
+        L.nto_normal.restype = C.c_double
+        L.nto_uniform.argtypes = [C.c_uint64, C.c_uint64, C.c_int32, C.c_int32]
+        L.nto_uniform.restype = C.c_double
+        L.nto_mark_active.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_uint8)]
+        L.nto_replay.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64, C.c_uint64,
+                                 C.c_int, C.c_int, C.c_int, C.POINTER(_Totals)]
+        L.nto_replay_paths.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
+                                       C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                       C.POINTER(C.c_double)]
+        _lib = L
+    return _lib
+
+
+class Tape:
+    """A flat tape (the dict of AadTape.flat() or the same keys) pinned for C."""
+
+    def __init__(self, flat: dict):
+        self.op = np.ascontiguousarray(flat["op"], dtype=np.int32)
+        self.arg_a = np.ascontiguousarray(flat["arg_a"], dtype=np.int32)
+        self.arg_b = np.ascontiguousarray(flat["arg_b"], dtype=np.int32)
+        self.constant = np.ascontiguousarray(flat["constant"], dtype=np.float64)
+        self.input_node = np.ascontiguousarray(flat["input_node"], dtype=np.int32)
+        self.output_node = np.ascontiguousarray(flat["output_node"], dtype=np.int32)
+        self.n_streams = int(flat.get("n_streams", 1))
+        self.recorded = np.ascontiguousarray(flat.get("recorded_inputs", self.constant[self.input_node]),
+                                             dtype=np.float64)
+        p = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
+        self.s = _Tape(len(self.op), p(self.op), p(self.arg_a), p(self.arg_b),
+                       self.constant.ctypes.data_as(C.POINTER(C.c_double)), len(self.input_node),
+                       p(self.input_node), len(self.output_node), p(self.output_node), self.n_streams)
+
+    @property
+    def n_inputs(self) -> int:
+        return len(self.input_node)
+
+
+def philox(c0: int, c1: int, key: int) -> tuple[int, int]:
+    out = (C.c_uint32 * 2)()
+    lib().nto_philox2x32_10(c0, c1, key, out)
+    return out[0], out[1]
+
+
+def normal(path: int, seed: int, k: int, stream: int = 0) -> float:
+    return lib().nto_normal(path & (2**64 - 1), seed & (2**64 - 1), stream, k)
+
+
+def active(flat: dict) -> np.ndarray:
+    t = Tape(flat)
+    out = np.zeros(len(t.op), dtype=np.uint8)
+    lib().nto_mark_active(C.byref(t.s), out.ctypes.data_as(C.POINTER(C.c_uint8)))
+    return out
+
+
+def replay_sums(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, f32: bool = False,
+                adjoints: bool = True, threads: int = 0) -> np.ndarray:
+    """Raw sums [sum y, sum y^2, sum adjoint_j...] for output 0 (AadTotals fields)."""
+    t = Tape(flat)
+    x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
+    no = len(t.output_node)
+    val = np.zeros(no)
+    sq = np.zeros(no)
+    gr = np.zeros(no * max(1, t.n_inputs))
+    tot = _Totals(val.ctypes.data_as(C.POINTER(C.c_double)), sq.ctypes.data_as(C.POINTER(C.c_double)),
+                  gr.ctypes.data_as(C.POINTER(C.c_double)))
+    rc = lib().nto_replay(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
+                          offset & (2**64 - 1), seed & (2**64 - 1), int(f32), int(adjoints), threads, C.byref(tot))
+    if rc != 0:
+        raise ValueError(f"oracle rejected the tape ({rc})")
+    return np.concatenate([[val[0], sq[0]], gr[:t.n_inputs]])
+
+
+def replay_paths(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, f32: bool = False,
+                 threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    t = Tape(flat)
+    x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
+    values = np.zeros(paths)
+    grads = np.zeros((paths, max(1, t.n_inputs)))
+    rc = lib().nto_replay_paths(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
+                                offset & (2**64 - 1), seed & (2**64 - 1), int(f32), threads,
+                                values.ctypes.data_as(C.POINTER(C.c_double)),
+                                grads.ctypes.data_as(C.POINTER(C.c_double)))
+    if rc != 0:
+        raise ValueError(f"oracle rejected the tape ({rc})")
+    return values, grads[:, :t.n_inputs]
+
+
+def to_result(sums: np.ndarray, paths: int) -> dict:
+    """AadTotals.toResult (AadTotals.java:68-89): mean, stderr, mean gradient."""
+    n = float(paths)
+    mean = sums[0] / n
+    if paths > 1:
+        var = (sums[1] - n * mean * mean) / (n - 1.0)
+        se = float(np.sqrt(max(0.0, var) / n))
+    else:
+        se = float("nan")
+    return {"price": mean, "stderr": se, "gradient": np.asarray(sums[2:]) / n}

@@ -1,0 +1,85 @@
+"""Shared fixtures: the five workload tapes, recorded by the host layer.
+
+Tests marked `gpu` need an MI355X (gfx950) and the in-tree libnt_rocm.so;
+everything else runs on the CPU. The oracle (oracle/oracle.py) is the checker.
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "oracle"))
+sys.path.insert(0, str(ROOT / "tests"))
+
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device and the built HIP engine")
+
+
+@pytest.fixture(scope="session")
+def nt():
+    import nablatensor_amd
+    return nablatensor_amd
+
+
+def equity_tape(nt, product, market, steps):
+    return nt.record(product, market, nt.TimeGrid.uniform(steps))
+
+
+def worst_of_fixture() -> dict:
+    return json.loads((GOLDEN / "worst_of_16.json").read_text())
+
+
+def workload_tapes(nt, steps_c4: int = 504, steps_c5: int = 252) -> dict:
+    """Tapes of the five workloads (market inputs fixed, seeds as in the bench configs)."""
+    m = nt.EquityMarket.atmOneYear()
+    barrier = nt.ExoticProducts.barrier(nt.OptionTypeEnum.CALL, nt.ExoticProducts.BarrierEnum.DOWN_IN, 80.0, 1.0)
+    heston = nt.HestonMarket.create(spot=100, strike=100, rate=0.03, v0=0.04, kappa=2.0, theta=0.04, xi=0.5, rho=-0.7)
+    out = {
+        "C1": equity_tape(nt, nt.Products.europeanCall(), m, 1),
+        "C2": equity_tape(nt, nt.Products.asianCall(), m, 252),
+        "C3": equity_tape(nt, barrier, m.withVol(0.25), 252),
+        "C4": nt.record(nt.HestonModel.asian(nt.OptionTypeEnum.CALL, 2.0, steps_c4), heston),
+    }
+    fx = worst_of_fixture()
+    basket = nt.WorstOfBasket.market([100.0] * 16, fx["sigma"], 0.03)
+    out["C5"] = nt.record(nt.WorstOfBasket.call(fx["corr"], 100.0, 1.0, steps_c5), basket)
+    return out
+
+
+@pytest.fixture(scope="session")
+def tapes(nt):
+    return {k: v.flat() for k, v in workload_tapes(nt).items()}
+
+
+def tape_slots(source: str) -> int:
+    for line in source.splitlines():
+        if line.startswith("// nt-plan:"):
+            for kv in line.split()[2:]:
+                k, v = kv.split("=")
+                if k == "tape_slots":
+                    return int(v)
+    raise ValueError("no plan line in the generated source")
+
+
+def rel_err(a, b, floor: float = 1.0) -> float:
+    """max |a-b| / max(floor, |b|) elementwise (the reference's 1+|x| style scale)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.max(np.abs(a - b) / np.maximum(floor, np.abs(b)))) if a.size else 0.0
+
+
+def gpu_available() -> bool:
+    try:
+        from nablatensor_amd import rocm
+        return rocm.probe() > 0
+    except Exception:
+        return False

@@ -1,0 +1,52 @@
+"""Compile a generated replay kernel for the host (tests/host_emu) and run it.
+
+Used only by the CPU tests of the lowering: the emitted source is built with
+g++ -ffp-contract=off against glibc's libm, the same arithmetic as the oracle,
+so fp64 per-path results can be compared to rounding level.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+import subprocess
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+EMU = Path(__file__).resolve().parent / "host_emu"
+BUILD = Path(tempfile.gettempdir()) / "nt_host_emu"
+
+
+class EmulatedKernel:
+    def __init__(self, source: str, n_inputs: int, tape_slots: int, dump: bool = True):
+        BUILD.mkdir(exist_ok=True)
+        key = hashlib.sha1((source + str(dump)).encode()).hexdigest()[:16]
+        src = BUILD / f"k_{key}.hip.h"
+        so = BUILD / f"k_{key}.so"
+        if not so.exists():
+            src.write_text(source)
+            cmd = ["g++", "-O1", "-std=c++17", "-shared", "-fPIC", "-ffp-contract=off", "-w",
+                   f"-I{ROOT / 'nablatensor_amd' / 'csrc'}", f"-I{EMU}", f'-DNT_KERNEL_FILE="{src}"',
+                   str(EMU / "emu_main.cpp"), "-o", str(so) + ".tmp"]
+            if dump:
+                cmd.insert(1, "-DNT_DUMP_PATHS=1")
+            subprocess.run(cmd, check=True)
+            Path(str(so) + ".tmp").rename(so)
+        self.lib = C.CDLL(str(so))
+        self.lib.emu_run.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(C.c_double),
+                                     C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                     C.c_uint, C.c_uint, C.c_ulonglong]
+        self.n_inputs = n_inputs
+        self.slots = tape_slots
+
+    def run(self, inputs, paths: int, offset: int = 0, seed: int = 42, grid: int = 4, block: int = 64):
+        x = np.ascontiguousarray(inputs, dtype=np.float64)
+        sums = np.zeros(2 + self.n_inputs)
+        values = np.zeros(paths)
+        grads = np.zeros((paths, max(1, self.n_inputs)))
+        p = lambda a: a.ctypes.data_as(C.POINTER(C.c_double))
+        self.lib.emu_run(paths, offset & (2**64 - 1), seed & (2**64 - 1), p(x), p(sums), p(values), p(grads),
+                         grid, block, self.slots)
+        return sums, values, grads[:, :self.n_inputs]

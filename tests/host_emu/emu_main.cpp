@@ -1,0 +1,21 @@
+// Driver for an emulated replay kernel; NT_KERNEL_FILE names the generated source.
+#include "prelude.h"
+#include NT_KERNEL_FILE
+
+#include <cstddef>
+#include <vector>
+
+extern "C" int emu_run(nt_u64 n_paths, nt_u64 offset, nt_u64 seed, const double* inputs, double* sums,
+                       double* out_v, double* out_g, unsigned grid, unsigned block, unsigned long long slots) {
+  gridDim.x = grid;
+  blockDim.x = block;
+  std::vector<real> scratch(static_cast<size_t>(grid) * block * (slots ? slots : 1));
+  for (unsigned b = 0; b < grid; ++b) {
+    for (unsigned t = 0; t < block; ++t) {
+      blockIdx.x = b;
+      threadIdx.x = t;
+      nt_replay(inputs, n_paths, offset, seed, sums, scratch.data(), out_v, out_g);
+    }
+  }
+  return 0;
+}

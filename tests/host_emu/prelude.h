@@ -1,0 +1,33 @@
+// Host emulation of the HIP builtins a generated replay kernel uses, so the
+// lowering's output can be compiled with g++ and run on the CPU by the tests.
+// Threads of the emulated grid run one after another; every per-lane scratch
+// slot keeps the device indexing (slot * T + tid).
+#pragma once
+#include <math.h>
+
+#include <cmath>
+
+#define NT_HOST_EMU 1
+#define __global__
+#define __device__
+#define __forceinline__ inline
+#define __launch_bounds__(n)
+#define __shared__ static
+
+struct nt_emu_dim3 {
+  unsigned x = 0, y = 1, z = 1;
+};
+static nt_emu_dim3 gridDim, blockDim, blockIdx, threadIdx;
+
+inline void sincospif(float x, float* s, float* c) {
+  const double a = M_PI * static_cast<double>(x);
+  *s = static_cast<float>(::sin(a));
+  *c = static_cast<float>(::cos(a));
+}
+
+// Sequential stand-in for the block reduction: every emulated thread adds its
+// accumulators into partials[0 .. NCH).
+template <int NCH>
+inline void nt_block_store(const double (&acc)[NCH], double* partials, double*) {
+  for (int c = 0; c < NCH; ++c) partials[c] += acc[c];
+}

@@ -1,0 +1,106 @@
+"""The C ABI (include/nablatensor_rocm.h) without a GPU: exports, error codes,
+the lowering entry points and offline hipRTC compilation for gfx950."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, gpu_available
+
+
+@pytest.fixture(scope="module")
+def rocm():
+    from nablatensor_amd import rocm as r
+    return r
+
+
+def header_functions() -> list[str]:
+    text = (ROOT / "include" / "nablatensor_rocm.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(nt_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_function(rocm):
+    names = header_functions()
+    assert len(names) >= 12
+    lib = C.CDLL(str(rocm.LIB_PATH))
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(rocm.EXPORTS)
+    assert lib.nt_abi_version() == 1
+
+
+@pytest.mark.skipif(gpu_available(), reason="checks the no-device path")
+def test_no_device_paths(rocm, tapes):
+    assert rocm.probe() == 0
+    with pytest.raises(rocm.NtError) as e:
+        rocm.Executable(tapes["C1"])
+    assert e.value.status == rocm.NT_E_NO_DEVICE
+    assert "no ROCm/HIP gfx950 device" in str(e.value)
+
+
+def _mutated(flat, **kw):
+    out = {k: (np.array(v, copy=True) if isinstance(v, np.ndarray) else v) for k, v in flat.items()}
+    out.update(kw)
+    return out
+
+
+def test_unsupported_tapes_are_declined(rocm, tapes):
+    flat = tapes["C1"]
+    two_outputs = _mutated(flat, output_node=np.array([25, 24], dtype=np.int32))
+    with pytest.raises(rocm.NtError) as e:
+        rocm.lower(two_outputs)
+    assert e.value.status == rocm.NT_E_UNSUPPORTED and "multi-output" in str(e.value)
+    uniform = _mutated(flat)
+    uniform["op"][14] = 3  # RANDU
+    with pytest.raises(rocm.NtError) as e:
+        rocm.lower(uniform)
+    assert e.value.status == rocm.NT_E_UNSUPPORTED and "randu" in str(e.value)
+    streams = _mutated(flat, n_streams=2)
+    with pytest.raises(rocm.NtError) as e:
+        rocm.lower(streams)
+    assert e.value.status == rocm.NT_E_UNSUPPORTED
+
+
+def test_malformed_tapes_are_rejected(rocm, tapes):
+    flat = tapes["C1"]
+    forward_ref = _mutated(flat)
+    forward_ref["arg_a"][5] = 20
+    with pytest.raises(rocm.NtError) as e:
+        rocm.lower(forward_ref)
+    assert e.value.status == rocm.NT_E_INVALID
+    bad_op = _mutated(flat)
+    bad_op["op"][7] = 99
+    with pytest.raises(rocm.NtError) as e:
+        rocm.lower(bad_op)
+    assert e.value.status == rocm.NT_E_INVALID
+    bad_input = _mutated(flat, input_node=np.array([0, 1, 2, 3, 5], dtype=np.int32))
+    with pytest.raises(rocm.NtError):
+        rocm.lower(bad_input)
+    with pytest.raises(rocm.NtError) as e:
+        rocm.lower(flat, rocm.options(block=100))
+    assert e.value.status == rocm.NT_E_INVALID
+
+
+def test_lower_reports_needed_length(rocm, tapes):
+    from nablatensor_amd.rocm import NtOptions, TapeArrays, lib
+    arrays = TapeArrays(tapes["C2"])
+    t = arrays.struct()
+    o = rocm.options()
+    n = C.c_int64(0)
+    assert lib().nt_lower(C.byref(t), C.byref(o), None, C.byref(n)) == 0
+    small = C.create_string_buffer(16)
+    m = C.c_int64(16)
+    assert lib().nt_lower(C.byref(t), C.byref(o), small, C.byref(m)) == rocm.NT_E_INVALID
+    assert m.value == n.value
+
+
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+@pytest.mark.parametrize("precision", ["fp64", "fp32"])
+def test_offline_gfx950_compile_has_no_scratch(rocm, tapes, name, precision):
+    info = rocm.compile_check(tapes[name], rocm.options(precision))
+    assert info["scratch_bytes"] == 0
+    assert 0 < info["vgprs"] <= 512

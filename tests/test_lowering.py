@@ -1,0 +1,108 @@
+"""CPU tests of the tape lowering (nablatensor_amd/csrc/lower.cpp).
+
+The generated kernel source is compiled for the host (tests/host_emu) with the
+same IEEE arithmetic as the oracle (no FMA contraction, glibc libm) and run
+over an emulated grid with the device's scratch indexing. fp64 results must
+then equal the oracle bit for bit: any slip in loop detection, carry handling,
+segment checkpoints, stored values, draw pairing or the order of adjoint
+accumulation shows up as a difference.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import emu
+import oracle
+from conftest import equity_tape, rel_err, tape_slots
+
+OFFSET = 0x100000003
+
+
+def run_emulated(flat, opts, paths, offset=OFFSET, seed=42, grid=3, block=64, inputs=None, rocm=None):
+    src = rocm.lower(flat, opts)
+    k = emu.EmulatedKernel(src, len(flat["input_node"]), tape_slots(src))
+    x = flat["recorded_inputs"] if inputs is None else inputs
+    return k.run(x, paths, offset, seed, grid=grid, block=block)
+
+
+@pytest.fixture(scope="module")
+def rocm():
+    from nablatensor_amd import rocm as r
+    return r
+
+
+@pytest.mark.parametrize("ckpt", [1, 2, 3])
+@pytest.mark.parametrize("name,paths", [("C1", 700), ("C2", 400), ("C3", 300), ("C4", 150), ("C5", 40)])
+def test_emulated_fp64_is_bit_exact(rocm, tapes, name, paths, ckpt):
+    flat = tapes[name]
+    sums, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt), paths, rocm=rocm)
+    ov, og = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov)
+    assert np.array_equal(g, og)
+    ref = oracle.replay_sums(flat, paths, OFFSET, 42, threads=1)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-13
+
+
+@pytest.mark.parametrize("seg", [2, 4, 10, 50])
+def test_segment_lengths_with_tail(rocm, tapes, seg):
+    """Segment lengths that do not divide 252 leave a tail segment."""
+    flat = tapes["C2"]
+    _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=1, seg_len=seg), 200, rocm=rocm)
+    ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov) and np.array_equal(g, og)
+
+
+def test_unrolled_straight_line_matches(rocm, tapes):
+    flat = equity_tape_flat = tapes["C2"]
+    _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1), 64, rocm=rocm)
+    ov, og = oracle.replay_paths(flat, 64, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov) and np.array_equal(g, og)
+
+
+def test_price_only_and_moved_inputs(rocm, tapes):
+    flat = tapes["C3"]
+    x = [95.0, 101.0, 0.3, 0.01, 0.75]
+    sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False), 200, inputs=x, rocm=rocm)
+    ov, _ = oracle.replay_paths(flat, 200, OFFSET, 42, inputs=x, threads=1)
+    assert np.array_equal(v, ov)
+    assert np.all(sums[2:] == 0.0)
+
+
+@pytest.mark.parametrize("name", ["C2", "C3"])
+def test_emulated_fp32_tracks_fp32_oracle(rocm, tapes, name):
+    flat = tapes[name]
+    sums, v, g = run_emulated(flat, rocm.options("fp32"), 300, rocm=rocm)
+    ov, og = oracle.replay_paths(flat, 300, OFFSET, 42, f32=True, threads=1)
+    assert rel_err(v, ov) < 2e-4
+    assert rel_err(g, og) < 2e-3
+
+
+def test_lookback_and_digital_tapes(nt, rocm):
+    m = nt.EquityMarket.atmOneYear()
+    for product in (nt.Products.lookbackCall(), nt.Products.lookbackPut(),
+                    nt.ExoticProducts.digitalCash(nt.OptionTypeEnum.CALL, 1.0, 0.5),
+                    nt.ExoticProducts.barrier(nt.OptionTypeEnum.PUT, nt.ExoticProducts.BarrierEnum.UP_OUT, 120.0, 2.0)):
+        flat = equity_tape(nt, product, m, 24).flat()
+        for ckpt in (1, 2, 3):
+            _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt), 96, rocm=rocm)
+            ov, og = oracle.replay_paths(flat, 96, OFFSET, 42, threads=1)
+            assert np.array_equal(v, ov) and np.array_equal(g, og), (product.label, ckpt)
+
+
+def test_loop_plan_of_the_workloads(rocm, tapes):
+    def plan(name, **kw):
+        src = rocm.lower(tapes[name], rocm.options(**kw))
+        head = src.splitlines()[1]
+        return head
+    assert "start 15, period 6, iterations 252, draws/iter 1" in plan("C2")
+    assert "start 15, period 16, iterations 252, draws/iter 1" in plan("C3")
+    assert "period 30, iterations 504, draws/iter 2" in plan("C4")
+    assert "period 504, iterations 252, draws/iter 16" in plan("C5")
+    assert "straight line" in rocm.lower(tapes["C1"], rocm.options()).splitlines()[0]
+
+
+def test_draw_pairs_share_one_philox_block(rocm, tapes):
+    src = rocm.lower(tapes["C2"], rocm.options("fp64", checkpoint=1, seg_len=14))
+    fwd = src.split("for (nt_u32 sg = 0;")[1].split("const double y")[0]
+    assert fwd.count("nt_normal_pair(") == 7  # 14 draws per segment, two legs per block

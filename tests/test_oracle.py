@@ -1,0 +1,212 @@
+"""Pins of the CPU oracle (oracle/nt_oracle.c) against what fixes its answers.
+
+* Philox2x32-10 round function: the Random123 known-answer vectors.
+* Keying / Box-Muller leg mapping: the reference's formula restated
+  independently here in numpy, plus moments of the draws.
+* The whole chain (Philox + Box-Muller + recorded tape + reverse sweep + sums):
+  the Asian-call aggregates printed in the reference's evidence pack
+  (docs/validation.md:56-63, docs/compare/vs-bump-and-revalue.md:39).
+* Closed forms: Black-Scholes for the 1-step European (MvpPricingTest.java:40-53).
+* Invariants: knock-out + knock-in = vanilla (ExoticsTest.java:55-62), adjoint
+  price = price-only price (ModelsTest.java:67-68), additivity of path ranges,
+  thread-count independence.
+* Brute force: central differences with common random numbers on small tapes.
+A planted mistake in the oracle (sign of a reverse rule, a leg swap, an input
+order slip) fails at least one of these.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import equity_tape, rel_err, workload_tapes
+
+
+# ---- Philox ------------------------------------------------------------------
+
+def test_philox_random123_known_answers():
+    # philox2x32_10 KATs from Random123 (kat_vectors): (ctr, key) -> out
+    assert oracle.philox(0, 0, 0) == (0xFF1DAE59, 0x6CD10DF2)
+    assert oracle.philox(0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF) == (0x2C3F628B, 0xAB4FD7AD)
+    assert oracle.philox(0x243F6A88, 0x85A308D3, 0x13198A2E) == (0xDD7CE038, 0xF62A4C12)
+
+
+def _philox_np(c0, c1, key):
+    c0 = np.uint64(c0)
+    c1 = np.uint64(c1)
+    for _ in range(10):
+        p = np.uint64(0xD256D193) * c0
+        hi, lo = p >> np.uint64(32), p & np.uint64(0xFFFFFFFF)
+        c0, c1 = hi ^ np.uint64(key) ^ c1, lo
+        key = (key + 0x9E3779B9) & 0xFFFFFFFF
+    return int(c0), int(c1)
+
+
+@pytest.mark.parametrize("path,seed", [(0, 42), (12345, 42), (0x100000003, 0x12345678FEDCBA98), (2**40 + 5, 7)])
+def test_normal_keying_and_legs(path, seed):
+    """Draw k of path p: counter (lo, hi ^ (k>>1)), key 0x1BD11BDA; cos leg for even k, sin for odd k."""
+    lo = (path & 0xFFFFFFFF) ^ (seed & 0xFFFFFFFF)
+    hi = (path >> 32) ^ (seed >> 32)
+    for k in (0, 1, 2, 7, 250, 251):
+        c0, c1 = _philox_np(lo, hi ^ (k >> 1), 0x1BD11BDA)
+        u1 = (c0 + 0.5) * 2.0 ** -32
+        u2 = (c1 + 0.5) * 2.0 ** -32
+        r = math.sqrt(-2.0 * math.log(u1))
+        th = 6.283185307179586 * u2
+        want = r * (math.cos(th) if k % 2 == 0 else math.sin(th))
+        assert oracle.normal(path, seed, k) == pytest.approx(want, rel=1e-15, abs=1e-15)
+
+
+def test_normal_moments():
+    z = np.array([oracle.normal(p, 42, k) for p in range(4000) for k in range(4)])
+    assert abs(z.mean()) < 0.03
+    assert abs(z.var() - 1.0) < 0.04
+    a = np.array([oracle.normal(p, 42, 0) for p in range(8000)])
+    b = np.array([oracle.normal(p, 42, 1) for p in range(8000)])
+    assert abs(np.mean(a * b)) < 0.03  # the two legs of one block are uncorrelated
+
+
+# ---- tape structure ----------------------------------------------------------------
+
+def test_node_counts_match_reference(nt):
+    tapes = workload_tapes(nt)
+    assert tapes["C1"].size() == 26
+    assert tapes["C2"].size() == 1536   # README.md:73
+    assert tapes["C3"].size() == 4057   # docs/examples/asian-greeks.md:66-67
+    assert tapes["C4"].size() == 15144
+    assert tapes["C2"].randCount() == 252 and tapes["C4"].randCount() == 1008
+    assert tapes["C5"].inputCount() == 33 and tapes["C5"].randCount() == 16 * 252
+
+
+def test_activity_matches_reference_rule(nt, tapes):
+    for name in ("C1", "C2", "C3"):
+        assert np.array_equal(oracle.active(tapes[name]), tapes[name]["active"])
+    assert int(tapes["C2"]["active"].sum()) == 1279
+    assert int(tapes["C3"]["active"].sum()) == 2792
+
+
+# ---- whole chain: reference-held aggregates ------------------------------------------------
+
+def test_published_asian_aggregates_1m(tapes):
+    r = oracle.to_result(oracle.replay_sums(tapes["C2"], 1_000_000, 0, 42), 1_000_000)
+    g = r["gradient"]  # input order spot, strike, vol, rate, maturity
+    assert r["price"] == pytest.approx(5.3058639800, rel=5e-11)
+    assert g[0] == pytest.approx(0.56198939096, rel=5e-11)
+    assert g[1] == pytest.approx(-0.50893075116, rel=5e-11)
+    assert g[2] == pytest.approx(22.412432861, rel=5e-11)
+    assert g[3] == pytest.approx(23.603384920, rel=5e-11)
+    assert g[4] == pytest.approx(2.9493448337, rel=5e-11)
+
+
+def test_published_asian_aggregates_2m(tapes):
+    r = oracle.to_result(oracle.replay_sums(tapes["C2"], 2_000_000, 0, 42), 2_000_000)
+    assert r["price"] == pytest.approx(5.301676, abs=6e-7)
+    assert r["gradient"][0] == pytest.approx(0.561932, abs=6e-7)
+    assert r["gradient"][2] == pytest.approx(22.389375, abs=6e-7)
+    assert r["gradient"][3] == pytest.approx(23.603735, abs=6e-7)
+
+
+# ---- closed forms and invariants ---------------------------------------------------------------
+
+def _bs_call(s, k, vol, r, t):
+    d1 = (math.log(s / k) + (r + 0.5 * vol * vol) * t) / (vol * math.sqrt(t))
+    d2 = d1 - vol * math.sqrt(t)
+    n = lambda x: 0.5 * math.erfc(-x / math.sqrt(2.0))
+    disc = math.exp(-r * t)
+    pdf = math.exp(-0.5 * d1 * d1) / math.sqrt(2 * math.pi)
+    return {"price": s * n(d1) - k * disc * n(d2), "delta": n(d1), "dK": -disc * n(d2),
+            "vega": s * pdf * math.sqrt(t), "rho": k * t * disc * n(d2)}
+
+
+def test_european_matches_black_scholes(tapes):
+    n = 400_000
+    r = oracle.to_result(oracle.replay_sums(tapes["C1"], n, 0, 20260830), n)
+    bs = _bs_call(100.0, 100.0, 0.2, 0.03, 1.0)
+    g = r["gradient"]
+    # MvpPricingTest.java:47-51 tolerances
+    assert abs(r["price"] - bs["price"]) < 0.15
+    assert abs(g[0] - bs["delta"]) < 0.02
+    assert abs(g[1] - bs["dK"]) < 0.02
+    assert abs(g[2] - bs["vega"]) < 0.6
+    assert abs(g[3] - bs["rho"]) < 0.6
+    # and tighter: within 4 standard errors on the price
+    assert abs(r["price"] - bs["price"]) < 4 * r["stderr"]
+
+
+def test_european_per_path_by_hand(tapes):
+    """One path of the 1-step European evaluated from the formula."""
+    vals, grads = oracle.replay_paths(tapes["C1"], 3, 11, 42)
+    for i in range(3):
+        z = oracle.normal(11 + i, 42, 0)
+        s, k, v, r, t = 100.0, 100.0, 0.2, 0.03, 1.0
+        st = s * math.exp((r - 0.5 * v * v) * t + v * math.sqrt(t) * z)
+        disc = math.exp(-r * t)
+        assert vals[i] == pytest.approx(max(st - k, 0.0) * disc, rel=1e-13, abs=1e-13)
+        if st > k:
+            assert grads[i][0] == pytest.approx(st / s * disc, rel=1e-12)          # delta
+            assert grads[i][1] == pytest.approx(-disc, rel=1e-12)                  # dV/dK
+            assert grads[i][2] == pytest.approx(st * (-v * t + math.sqrt(t) * z) * disc, rel=1e-12)
+            assert grads[i][3] == pytest.approx(st * t * disc - t * (st - k) * disc, rel=1e-12)
+
+
+def test_knock_out_plus_knock_in_is_vanilla(nt):
+    m = nt.EquityMarket.atmOneYear()
+    B = nt.ExoticProducts.BarrierEnum
+    mk = lambda kind: equity_tape(nt, nt.ExoticProducts.barrier(nt.OptionTypeEnum.CALL, kind, 130.0, 1.0), m, 32).flat()
+    out = oracle.replay_sums(mk(B.UP_OUT), 50_000, 0, 42)
+    inn = oracle.replay_sums(mk(B.UP_IN), 50_000, 0, 42)
+    van = oracle.replay_sums(equity_tape(nt, nt.Products.europeanCall(), m, 32).flat(), 50_000, 0, 42)
+    assert abs(out[0] + inn[0] - van[0]) <= 1e-9 * (1 + abs(van[0]))
+    assert rel_err(out[2:] + inn[2:], van[2:], floor=1.0) <= 1e-9
+
+
+def test_adjoint_price_equals_price_only(tapes):
+    a = oracle.replay_sums(tapes["C4"], 2000, 0, 7, adjoints=True)
+    b = oracle.replay_sums(tapes["C4"], 2000, 0, 7, adjoints=False)
+    assert a[0] == b[0] and a[1] == b[1]
+
+
+def test_ranges_and_threads_are_consistent(tapes):
+    t = tapes["C2"]
+    whole = oracle.replay_sums(t, 6000, 100, 42, threads=1)
+    split = oracle.replay_sums(t, 2500, 100, 42, threads=1) + oracle.replay_sums(t, 3500, 2600, 42, threads=1)
+    assert rel_err(split, whole, floor=1e-300) <= 1e-13
+    many = oracle.replay_sums(t, 6000, 100, 42, threads=7)
+    assert rel_err(many, whole, floor=1e-300) <= 1e-13
+
+
+@pytest.mark.parametrize("name,idx,bump", [("C1", 0, 1e-3), ("C1", 2, 1e-5), ("C2s", 0, 1e-3), ("C2s", 3, 1e-5),
+                                            ("C4s", 4, 1e-5), ("C4s", 7, 1e-5)])
+def test_adjoint_matches_central_difference(nt, tapes, name, idx, bump):
+    """Per-path adjoints vs central differences with the same draws (fp64)."""
+    if name == "C2s":
+        flat = equity_tape(nt, nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), 8).flat()
+    elif name == "C4s":
+        h = nt.HestonMarket.create(spot=100, strike=100, rate=0.03, v0=0.04, kappa=2.0, theta=0.04, xi=0.5, rho=-0.7)
+        flat = nt.record(nt.HestonModel.asian(nt.OptionTypeEnum.CALL, 2.0, 6), h).flat()
+    else:
+        flat = tapes[name]
+    x0 = np.array(flat["recorded_inputs"])
+    vals, grads = oracle.replay_paths(flat, 64, 5, 42)
+    h = bump * max(1.0, abs(x0[idx]))
+    up, dn = x0.copy(), x0.copy()
+    up[idx] += h
+    dn[idx] -= h
+    vu, _ = oracle.replay_paths(flat, 64, 5, 42, inputs=up)
+    vd, _ = oracle.replay_paths(flat, 64, 5, 42, inputs=dn)
+    fd = (vu - vd) / (2 * h)
+    smooth = (np.abs(vals) > 1e-3) & (np.abs(vu - vd) < 0.5)  # away from the payoff kink
+    assert smooth.sum() > 10
+    assert np.max(np.abs(fd[smooth] - grads[smooth, idx]) / np.maximum(1.0, np.abs(grads[smooth, idx]))) < 1e-5
+
+
+def test_fp32_mode_rounds_every_node(tapes):
+    """fp32 replay stays within float rounding of the fp64 replay, per path."""
+    v64, g64 = oracle.replay_paths(tapes["C2"], 256, 0, 42)
+    v32, g32 = oracle.replay_paths(tapes["C2"], 256, 0, 42, f32=True)
+    assert rel_err(v32, v64) < 1e-4
+    assert not np.array_equal(v32, v64)
+    assert np.all(v32.astype(np.float32) == v32)  # stored values are floats
