@@ -285,6 +285,10 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   p.precision = o.precision == NT_FP32 ? NT_FP32 : NT_FP64;
   if (o.precision != NT_FP32 && o.precision != NT_FP64) { err = "precision must be NT_FP64 or NT_FP32"; return NT_E_INVALID; }
   p.adjoints = o.adjoints != 0;
+  // fp64 defaults to no contraction: the oracle rounds every product and sum
+  // separately, and over 500-step tapes fused rounding alone moves adjoints by
+  // ~5e-12 relative. fp32 is compared at aggregate level and keeps FMAs.
+  p.contract = o.contract > 0 || (o.contract == 0 && p.precision == NT_FP32);
   p.block = o.block > 0 ? o.block : 256;
   if (p.block % 64 != 0 || p.block > 1024) { err = "block must be a multiple of 64, at most 1024"; return NT_E_INVALID; }
   p.n_channels = 2 + t.n_in;
@@ -696,6 +700,7 @@ std::string Emitter::run() {
        << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
   }
   o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << "\n";
+  o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
   o_ << "#include \"nt_skeleton.h\"\n";
   o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
   o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block << ") void nt_replay(\n"

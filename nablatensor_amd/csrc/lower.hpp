@@ -53,6 +53,7 @@ struct Plan {
   int precision = NT_FP64;
   int adjoints = 1;
   int block = 256;
+  bool contract = false;                  // FMA contraction allowed in the generated code
   LoopPlan loop;
   int seg = 0, nseg_full = 0, tail = 0;   // iterations per segment, full segments, tail iterations
   int ckpt = NT_CKPT_RECOMPUTE;           // resolved policy

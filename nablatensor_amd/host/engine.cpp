@@ -407,6 +407,7 @@ std::unique_ptr<AadExecutable> RocmAadEngine::compile(TapePtr tape, const AadOpt
   o.checkpoint = optionInt(options, "checkpoint", 0);
   o.seg_len = optionInt(options, "segLen", 0);
   o.roll = optionInt(options, "roll", 1);
+  o.contract = optionInt(options, "contract", 0);
   const auto t0 = std::chrono::steady_clock::now();
   nt_exec* exec = nullptr;
   int rc = a.create(&ct, &o, &exec);
