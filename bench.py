@@ -34,6 +34,20 @@ WORKLOAD = "Asian call, GBM, 252 fixings, ATM 1y, value + 5 Greeks"
 REFERENCE_ROCM_FP64 = 2.16e6
 
 
+def measured_traffic(precision: str, info: dict) -> dict | None:
+    """HBM bytes per launch of this kernel configuration, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-calibrated), if one matches."""
+    path = ROOT / "profiles" / f"nt_replay_asian252_{precision}_counters.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic:"):
+            kv = dict(item.split("=") for item in line.split()[1:])
+            if int(kv["checkpoint"]) == info["checkpoint"] and int(kv["seg_len"]) == info["seg_len"]:
+                return {"bytes": float(kv["bytes"]), "source": str(path.relative_to(ROOT))}
+    return None
+
+
 def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg):
     from nablatensor_amd import flops
 
@@ -50,6 +64,7 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg):
         wall = time.perf_counter() - t0
     fl = flops.flops_per_scenario(flat, precision)
     avg_replay_s = sum(replay_ms) / len(replay_ms) / 1e3
+    traffic = measured_traffic(precision, info) if paths == 2_000_000 else None
     achieved = fl * paths / avg_replay_s / 1e12
     peak = flops.PEAK_TFLOPS[precision]
     return {
@@ -59,7 +74,10 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg):
         "replay_kernel_ms": avg_replay_s * 1e3,
         "kernel_scenarios_per_s": paths / avg_replay_s,
         "roofline": {"bound": "valu", "kernel": "nt_replay", "achieved": achieved, "peak": peak,
-                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / peak,
+                     "traffic": None if traffic is None else traffic["bytes"],
+                     "traffic_source": None if traffic is None else traffic["source"],
+                     "algorithmic_bytes": 8 * (len(flat["input_node"]) + info["grid_cap"] * (2 + len(flat["input_node"]))),
                      "flops_per_scenario": fl, "convention": "NT-FLOP v1"},
         "kernel": {k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
                                         "loop_iters", "seg_len", "checkpoint", "tape_slots", "grid_cap")},
@@ -81,6 +99,19 @@ def cpu_baseline(flat, sample, seed):
                       "not run (no JDK on this host)"}
 
 
+def copy_calibration(mib: int) -> int:
+    import torch
+
+    n = mib << 20
+    a = torch.ones(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "copies": 3}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -93,7 +124,12 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1_000_000)
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (scenarios shard by path "
               "range with one reduction of raw sums per GPU, see DESIGN.md)", file=sys.stderr)

@@ -105,10 +105,19 @@ def check_offline_hipcc(source: str, name: str = "check") -> Path:
     return out
 
 
+def build_mathbench() -> Path:
+    """hipcc build of the building-block microbenchmark (csrc/mathbench.hip)."""
+    out = PKG / "mathbench"
+    _run([str(ROCM / "bin" / "hipcc"), "--offload-arch=gfx950", "-O3", *PACKED_FP32_OFF, "-w",
+          str(CSRC / "mathbench.hip"), "-o", str(out)])
+    return out
+
+
 def build_all(force: bool = True) -> None:
     build_engine(force)
     build_host(force)
     build_oracle()
+    build_mathbench()
 
 
 if __name__ == "__main__":
