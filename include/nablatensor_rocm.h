@@ -80,7 +80,8 @@ typedef struct nt_options {
   int32_t seg_len;          /* loop iterations per checkpoint segment; 0 = cost model */
   int32_t roll;             /* 1 (default): roll the step loop when one is found; -1: never */
   int32_t contract;         /* FMA contraction: 0 default (off for fp64, on for fp32), 1 on, -1 off */
-  int32_t reserved[8];
+  int32_t libm;             /* fp64 Box-Muller: 0 the skeleton's own log/sqrt/sincos, 1 device libm, 2 own log/sqrt + libm sincos */
+  int32_t reserved[7];
 } nt_options;
 
 typedef struct nt_exec nt_exec;

@@ -41,9 +41,11 @@ def _newer(target: Path, sources: list[Path]) -> bool:
 
 def embed_skeleton() -> Path:
     src = (CSRC / "nt_skeleton.h").read_text()
+    tables = (CSRC / "nt_math_tables.h").read_text()
     out = CSRC / "skeleton_src.inc"
-    text = ("// generated from nt_skeleton.h by nablatensor_amd/build.py; do not edit\n"
-            f'static const char NT_SKELETON_SRC[] = R"NTSKEL({src})NTSKEL";\n')
+    text = ("// generated from nt_skeleton.h and nt_math_tables.h by nablatensor_amd/build.py; do not edit\n"
+            f'static const char NT_SKELETON_SRC[] = R"NTSKEL({src})NTSKEL";\n'
+            f'static const char NT_MATH_TABLES_SRC[] = R"NTSKEL({tables})NTSKEL";\n')
     if not out.exists() or out.read_text() != text:
         out.write_text(text)
     return out
@@ -53,7 +55,8 @@ def build_engine(force: bool = True) -> Path:
     inc = embed_skeleton()
     out = PKG / "libnt_rocm.so"
     srcs = [CSRC / "nt_rocm.cpp", CSRC / "lower.cpp"]
-    deps = srcs + [CSRC / "lower.hpp", inc, ROOT / "include" / "nablatensor_rocm.h"]
+    deps = srcs + [CSRC / "lower.hpp", CSRC / "nt_skeleton.h", CSRC / "nt_math_tables.h", inc,
+                   ROOT / "include" / "nablatensor_rocm.h"]
     if not force and _newer(out, deps):
         return out
     cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",

@@ -289,6 +289,7 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   // separately, and over 500-step tapes fused rounding alone moves adjoints by
   // ~5e-12 relative. fp32 is compared at aggregate level and keeps FMAs.
   p.contract = o.contract > 0 || (o.contract == 0 && p.precision == NT_FP32);
+  p.libm = (o.libm == 1 || o.libm == 2) ? o.libm : 0;
   p.block = o.block > 0 ? o.block : 256;
   if (p.block % 64 != 0 || p.block > 1024) { err = "block must be a multiple of 64, at most 1024"; return NT_E_INVALID; }
   p.n_channels = 2 + t.n_in;
@@ -701,6 +702,8 @@ std::string Emitter::run() {
   }
   o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << "\n";
   o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
+  if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
+  if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";
   o_ << "#include \"nt_skeleton.h\"\n";
   o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
   o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block << ") void nt_replay(\n"
@@ -710,6 +713,9 @@ std::string Emitter::run() {
   o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
   o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
   o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
+  bool draws = false;
+  for (int i = 0; i < n; ++i) draws |= t_.op[i] == NT_OP_RANDN;
+  if (draws && !f32_) o_ << "  nt_tables_load();\n";
   for (int j = 0; j < nin; ++j) o_ << "  const real in" << j << " = (real)inputs[" << j << "];\n";
   o_ << "  double acc[" << NCH << "];\n";
   o_ << "  for (int c = 0; c < " << NCH << "; ++c) acc[c] = 0.0;\n";

@@ -104,6 +104,7 @@ int compile_hiprtc(const std::string& src, bool dump, std::vector<char>& code, d
   for (auto& o : opts) key += " " + o;
   key += "\n#hiprtc " + std::to_string(major) + "." + std::to_string(minor) + "\n";
   key += NT_SKELETON_SRC;
+  key += NT_MATH_TABLES_SRC;
   char hex[32];
   std::snprintf(hex, sizeof hex, "%016llx", static_cast<unsigned long long>(fnv1a(key)));
   const std::string dir = cache_dir();
@@ -113,9 +114,9 @@ int compile_hiprtc(const std::string& src, bool dump, std::vector<char>& code, d
     return NT_OK;
   }
   hiprtcProgram prog;
-  const char* hdr_src[] = {NT_SKELETON_SRC};
-  const char* hdr_name[] = {"nt_skeleton.h"};
-  hiprtcResult r = hiprtcCreateProgram(&prog, src.c_str(), "nt_replay.hip", 1, hdr_src, hdr_name);
+  const char* hdr_src[] = {NT_SKELETON_SRC, NT_MATH_TABLES_SRC};
+  const char* hdr_name[] = {"nt_skeleton.h", "nt_math_tables.h"};
+  hiprtcResult r = hiprtcCreateProgram(&prog, src.c_str(), "nt_replay.hip", 2, hdr_src, hdr_name);
   if (r != HIPRTC_SUCCESS) return fail(static_cast<int>(r), std::string("hiprtcCreateProgram failed: ") + hiprtcGetErrorString(r));
   std::vector<const char*> copts;
   for (auto& o : opts) copts.push_back(o.c_str());

@@ -37,18 +37,134 @@ __device__ __forceinline__ void nt_philox(nt_u32 c0, nt_u32 c1, nt_u32& o0, nt_u
   o1 = c1;
 }
 
+#include "nt_math_tables.h"
+
+#if !defined(NT_HOST_EMU)
+__device__ __forceinline__ nt_u32 nt_hi(double x) { return static_cast<nt_u32>(__double2hiint(x)); }
+__device__ __forceinline__ nt_u32 nt_lo(double x) { return static_cast<nt_u32>(__double2loint(x)); }
+__device__ __forceinline__ double nt_mk(nt_u32 hi, nt_u32 lo) {
+  return __hiloint2double(static_cast<int>(hi), static_cast<int>(lo));
+}
+__device__ __forceinline__ double nt_rsq(double x) { return __builtin_amdgcn_rsq(x); }
+#endif
+
+#ifndef NT_DEVICE_LIBM
+// The log table lives in LDS; every block copies it once at kernel start.
+__constant__ NtLogTable nt_log_table_c = NT_LOG_TABLE_INIT;
+__shared__ NtLogTable nt_log_table;
+
+__device__ __forceinline__ void nt_tables_load() {
+  const double* src = &nt_log_table_c.inv[0];
+  double* dst = &nt_log_table.inv[0];
+  for (unsigned i = threadIdx.x; i < 3u * 129u; i += blockDim.x) dst[i] = src[i];
+  __syncthreads();
+}
+
+// -2 ln(u) for u = (c + 0.5) * 2^-32, by Tang's table-driven method: u = 2^e x
+// with x in [sqrt(1/2), sqrt(2)), F = x rounded to 7 fractional bits,
+// ln u = e ln2 + ln F + ln(1 + r), r = (x - F) / F, |r| <= 2^-8. x - F is
+// exact and F = 1 near u = 1, so ln u keeps full relative accuracy there.
+__device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
+  const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
+  nt_u32 hx = nt_hi(u) + (0x3FF00000u - 0x3FE6A09Eu);
+  const int e = static_cast<int>(hx >> 20) - 0x3FF;
+  hx = (hx & 0x000FFFFFu) + 0x3FE6A09Eu;
+  const double x = nt_mk(hx, nt_lo(u));
+  const nt_u32 j = (((hx >> 12) & 0xFFu) + 1u) >> 1;
+  const nt_u32 fhi = (hx & 0xFFF00000u) + (j << 13);
+  const nt_u32 idx = (fhi - 0x3FE6A000u) >> 13;
+  const double r = (x - nt_mk(fhi, 0u)) * nt_log_table.inv[idx];
+  double q = fma(r, 1.0 / 7.0, -1.0 / 6.0);
+  q = fma(r, q, 0.2);
+  q = fma(r, q, -0.25);
+  q = fma(r, q, 1.0 / 3.0);
+  q = fma(r, q, -0.5);
+  const double p = fma(r * r, q, r);
+  const double ed = static_cast<double>(e);
+  const double hi = fma(ed, NT_LN2_HI, nt_log_table.hi[idx]);  // exact by the table's layout
+  const double lo = fma(ed, NT_LN2_LO, nt_log_table.lo[idx]) + p;
+  return -2.0 * (hi + lo);
+}
+
+// sqrt(a) for a positive normal finite a: reciprocal square root seed and one
+// coupled Newton step on (sqrt, 1/(2 sqrt)), then a residual correction.
+__device__ __forceinline__ double nt_sqrt_pos(double a) {
+  const double y = nt_rsq(a);
+  double g = a * y;
+  double h = 0.5 * y;
+  const double r = fma(-g, h, 0.5);
+  g = fma(g, r, g);
+  h = fma(h, r, h);
+  const double d = fma(-g, g, a);
+  return fma(d, h, g);
+}
+
+// sin and cos of theta = fl(6.283185307179586 * u) for u = (c + 0.5) * 2^-32:
+// the reference rounds its angle once, and so does this (theta is that rounded
+// product). The quarter turn q and the remainder f = u - q/4 in [-1/8, 1/8]
+// come exactly from the integer c and the polynomials are in f; the rounding
+// of theta, eps = theta - 2 pi u, is known exactly (one FMA) and applied as
+// sin(2 pi u + eps) = S + eps C, cos = C - eps S.
+__device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& co) {
+  const nt_u32 q = (c >> 30) + ((c >> 29) & 1u);
+  const int d = static_cast<int>(c - (q << 30));
+  const double f = fma(static_cast<double>(d), 0x1p-32, 0x1p-33);
+  const double t = f * f;
+  double ps = fma(t, NT_SIN2PI_7, NT_SIN2PI_6);
+  ps = fma(t, ps, NT_SIN2PI_5);
+  ps = fma(t, ps, NT_SIN2PI_4);
+  ps = fma(t, ps, NT_SIN2PI_3);
+  ps = fma(t, ps, NT_SIN2PI_2);
+  ps = fma(t, ps, NT_SIN2PI_1);
+  ps = fma(t, ps, NT_SIN2PI_0);
+  const double sn = f * ps;
+  double pc = fma(t, NT_COS2PI_8, NT_COS2PI_7);
+  pc = fma(t, pc, NT_COS2PI_6);
+  pc = fma(t, pc, NT_COS2PI_5);
+  pc = fma(t, pc, NT_COS2PI_4);
+  pc = fma(t, pc, NT_COS2PI_3);
+  pc = fma(t, pc, NT_COS2PI_2);
+  pc = fma(t, pc, NT_COS2PI_1);
+  const double cs = fma(t, pc, NT_COS2PI_0);
+  const nt_u32 qq = q & 3u;
+  const double sv = (qq & 1u) ? cs : sn;
+  const double cv = (qq & 1u) ? sn : cs;
+  const double s2 = (qq & 2u) ? -sv : sv;
+  const double c2 = ((qq + 1u) & 2u) ? -cv : cv;
+  const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
+  const double theta = NT_TWO_PI_D * u;
+  const double eps = fma(NT_TWO_PI_D_ERR, u, -fma(NT_TWO_PI_D, u, -theta));
+  s = fma(eps, c2, s2);
+  co = fma(-eps, s2, c2);
+}
+#else
+__device__ __forceinline__ void nt_tables_load() {}
+#endif
+
 // Both legs of the Box-Muller pair for Philox counter `ctr` of a path whose
-// counter words are (lo, hi). fp64 follows the reference expression order:
-// u = (c + 0.5) * 2^-32 (exact), r = sqrt(-2 log u1), theta = 2pi * u2.
+// counter words are (lo, hi): u = (c + 0.5) * 2^-32, r = sqrt(-2 log u1),
+// z = r cos(2 pi u2) for even draws and r sin(2 pi u2) for odd ones. With
+// NT_DEVICE_LIBM the reference expression is evaluated with device libm.
 __device__ __forceinline__ void nt_normal_pair(nt_u32 lo, nt_u32 hi, nt_u32 ctr, double& zc, double& zs) {
   nt_u32 c0, c1;
   nt_philox(lo, hi ^ ctr, c0, c1);
+#ifdef NT_DEVICE_LIBM
   const double u1 = (static_cast<double>(c0) + 0.5) * NT_UINT_SCALE;
   const double u2 = (static_cast<double>(c1) + 0.5) * NT_UINT_SCALE;
   const double r = sqrt(-2.0 * log(u1));
   const double theta = 6.283185307179586 * u2;
   double s, c;
   sincos(theta, &s, &c);
+#elif defined(NT_LIBM_SINCOS)
+  const double r = nt_sqrt_pos(nt_neg2log_u32(c0));
+  const double u2 = (static_cast<double>(c1) + 0.5) * NT_UINT_SCALE;
+  double s, c;
+  sincos(6.283185307179586 * u2, &s, &c);
+#else
+  const double r = nt_sqrt_pos(nt_neg2log_u32(c0));
+  double s, c;
+  nt_sincos_2pi_u32(c1, s, c);
+#endif
   zc = r * c;
   zs = r * s;
 }

@@ -408,6 +408,7 @@ std::unique_ptr<AadExecutable> RocmAadEngine::compile(TapePtr tape, const AadOpt
   o.seg_len = optionInt(options, "segLen", 0);
   o.roll = optionInt(options, "roll", 1);
   o.contract = optionInt(options, "contract", 0);
+  o.libm = optionInt(options, "libm", 0);
   const auto t0 = std::chrono::steady_clock::now();
   nt_exec* exec = nullptr;
   int rc = a.create(&ct, &o, &exec);

@@ -331,3 +331,64 @@ void nto_to_result(const nto_totals *sums, int32_t n_outputs, int32_t n_inputs, 
     }
   }
 }
+
+/* Forward sweep only, tracking the distance of each path to the singular
+ * points of its active nodes (see nt_oracle.h). */
+int nto_replay_conditioning(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
+                            uint64_t seed, int f32, int threads, double *sing, double *tie) {
+  int rc = validate(t);
+  if (rc != 0) return rc;
+  uint8_t *active = (uint8_t *)malloc((size_t)t->n);
+  nto_mark_active(t, active);
+  const int T = resolve_threads(threads);
+#ifdef _OPENMP
+#pragma omp parallel num_threads(T)
+#endif
+  {
+    double *v = (double *)malloc(sizeof(double) * (size_t)t->n);
+    stream_state *rng = (stream_state *)malloc(sizeof(stream_state) * (size_t)t->n_streams);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+    for (long long pi = 0; pi < (long long)paths; pi++) {
+      const uint64_t path = offset + (uint64_t)pi;
+      for (int32_t s = 0; s < t->n_streams; s++) stream_init(&rng[s], path, seed, s);
+      double ms = INFINITY, mt = INFINITY;
+      for (int32_t i = 0; i < t->n; i++) {
+        int32_t a = t->arg_a[i], b = t->arg_b[i];
+        double x;
+        switch (t->op[i]) {
+          case NTO_CONST: x = t->constant[i]; break;
+          case NTO_INPUT: x = inputs[a]; break;
+          case NTO_RANDN: x = stream_normal(&rng[b]); break;
+          case NTO_RANDU: x = stream_uniform(&rng[b]); break;
+          case NTO_ADD: x = v[a] + v[b]; break;
+          case NTO_SUB: x = v[a] - v[b]; break;
+          case NTO_MUL: x = v[a] * v[b]; break;
+          case NTO_DIV: x = v[a] / v[b]; if (active[i]) ms = fmin(ms, fabs(v[b])); break;
+          case NTO_NEG: x = -v[a]; break;
+          case NTO_EXP: x = exp(v[a]); break;
+          case NTO_LOG: x = log(v[a]); if (active[i]) ms = fmin(ms, fabs(v[a])); break;
+          /* sqrt(0) is a kink that a MAX/MIN in front of it decides (counted in tie) */
+          case NTO_SQRT: x = sqrt(v[a]); if (active[i] && v[a] != 0.0) ms = fmin(ms, fabs(v[a])); break;
+          case NTO_ABS: x = fabs(v[a]); break;
+          case NTO_MAX:
+          case NTO_MIN: {
+            const double p = v[a], q = v[b];
+            if (active[i]) mt = fmin(mt, fabs(p - q) / fmax(1.0, fmax(fabs(p), fabs(q))));
+            x = t->op[i] == NTO_MAX ? (p >= q ? p : q) : (p <= q ? p : q);
+            break;
+          }
+          default: x = NAN; break;
+        }
+        v[i] = f32 ? (double)(float)x : x;
+      }
+      sing[pi] = ms;
+      tie[pi] = mt;
+    }
+    free(rng);
+    free(v);
+  }
+  free(active);
+  return 0;
+}

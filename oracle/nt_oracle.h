@@ -76,6 +76,15 @@ int nto_replay(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t
 int nto_replay_paths(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                      uint64_t seed, int f32, int threads, double *values, double *grads);
 
+/* Conditioning of each path of output 0 (no reference counterpart; used by the
+ * tests to tell ill-conditioned paths from engine error). sing[p] = smallest
+ * |argument| of an active SQRT (nonzero arguments), LOG or DIV-denominator
+ * node (their local derivatives grow without bound as it goes to 0); tie[p] = smallest
+ * |a - b| / max(1, |a|, |b|) over active MAX/MIN nodes (a branch within
+ * rounding of flipping). Either is +inf when the tape has no such node. */
+int nto_replay_conditioning(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
+                            uint64_t seed, int f32, int threads, double *sing, double *tie);
+
 /* mean, standard error and mean gradient from raw sums (AadTotals.toResult). */
 void nto_to_result(const nto_totals *sums, int32_t n_outputs, int32_t n_inputs, uint64_t paths,
                    double *mean, double *stderr_out, double *mean_gradient);

@@ -49,6 +49,9 @@ def lib() -> C.CDLL:
         L.nto_replay_paths.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
                                        C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
                                        C.POINTER(C.c_double)]
+        L.nto_replay_conditioning.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
+                                              C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                              C.POINTER(C.c_double)]
         _lib = L
     return _lib
 
@@ -136,3 +139,28 @@ def to_result(sums: np.ndarray, paths: int) -> dict:
     else:
         se = float("nan")
     return {"price": mean, "stderr": se, "gradient": np.asarray(sums[2:]) / n}
+
+
+def conditioning(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, threads: int = 0):
+    """Per path: (smallest |arg| of an active SQRT/LOG/DIV denominator, smallest
+    relative MAX/MIN gap) -- how close the path runs to a singular point."""
+    t = Tape(flat)
+    x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
+    sing = np.zeros(paths)
+    tie = np.zeros(paths)
+    rc = lib().nto_replay_conditioning(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
+                                       offset & (2**64 - 1), seed & (2**64 - 1), 0, threads,
+                                       sing.ctypes.data_as(C.POINTER(C.c_double)),
+                                       tie.ctypes.data_as(C.POINTER(C.c_double)))
+    if rc != 0:
+        raise ValueError(f"oracle rejected the tape ({rc})")
+    return sing, tie
+
+
+def path_errors(values, grads, ref_values, ref_grads):
+    """Per path: value error |dv| / max(1, |v|) and normwise gradient error
+    max_j |dg_j| / max(1, max_j |g_j|)."""
+    ev = np.abs(values - ref_values) / np.maximum(1.0, np.abs(ref_values))
+    scale = np.maximum(1.0, np.max(np.abs(ref_grads), axis=1)) if ref_grads.size else np.ones(len(values))
+    eg = np.max(np.abs(grads - ref_grads), axis=1) / scale if ref_grads.size else np.zeros(len(values))
+    return ev, eg

@@ -22,7 +22,10 @@ BUILD = Path(tempfile.gettempdir()) / "nt_host_emu"
 class EmulatedKernel:
     def __init__(self, source: str, n_inputs: int, tape_slots: int, dump: bool = True):
         BUILD.mkdir(exist_ok=True)
-        key = hashlib.sha1((source + str(dump)).encode()).hexdigest()[:16]
+        deps = "".join(p.read_text() for p in (EMU / "prelude.h", EMU / "emu_main.cpp",
+                                                  ROOT / "nablatensor_amd" / "csrc" / "nt_skeleton.h",
+                                                  ROOT / "nablatensor_amd" / "csrc" / "nt_math_tables.h"))
+        key = hashlib.sha1((source + str(dump) + deps).encode()).hexdigest()[:16]
         src = BUILD / f"k_{key}.hip.h"
         so = BUILD / f"k_{key}.so"
         if not so.exists():

@@ -8,6 +8,11 @@
 extern "C" int emu_run(nt_u64 n_paths, nt_u64 offset, nt_u64 seed, const double* inputs, double* sums,
                        double* out_v, double* out_g, unsigned grid, unsigned block, unsigned long long slots) {
   gridDim.x = grid;
+  // Threads run one after another here, so the block-cooperative table copy is
+  // done once, whole, before any of them reads it.
+  blockDim.x = 1;
+  threadIdx.x = 0;
+  nt_tables_load();
   blockDim.x = block;
   std::vector<real> scratch(static_cast<size_t>(grid) * block * (slots ? slots : 1));
   for (unsigned b = 0; b < grid; ++b) {

@@ -6,6 +6,7 @@
 #include <math.h>
 
 #include <cmath>
+#include <cstring>
 
 #define NT_HOST_EMU 1
 #define __global__
@@ -13,6 +14,19 @@
 #define __forceinline__ inline
 #define __launch_bounds__(n)
 #define __shared__ static
+#define __constant__ static
+inline void __syncthreads() {}
+
+inline unsigned nt_hi(double x) { unsigned long long u; std::memcpy(&u, &x, 8); return static_cast<unsigned>(u >> 32); }
+inline unsigned nt_lo(double x) { unsigned long long u; std::memcpy(&u, &x, 8); return static_cast<unsigned>(u); }
+inline double nt_mk(unsigned hi, unsigned lo) {
+  unsigned long long u = (static_cast<unsigned long long>(hi) << 32) | lo;
+  double x;
+  std::memcpy(&x, &u, 8);
+  return x;
+}
+// correctly rounded stand-in for the device's reciprocal-square-root seed
+inline double nt_rsq(double x) { return 1.0 / std::sqrt(x); }
 
 struct nt_emu_dim3 {
   unsigned x = 0, y = 1, z = 1;

@@ -14,7 +14,7 @@ import pytest
 
 import emu
 import oracle
-from conftest import equity_tape, rel_err, tape_slots
+from conftest import check_per_path, equity_tape, rel_err, tape_slots
 
 OFFSET = 0x100000003
 
@@ -35,8 +35,9 @@ def rocm():
 @pytest.mark.parametrize("ckpt", [1, 2, 3])
 @pytest.mark.parametrize("name,paths", [("C1", 700), ("C2", 400), ("C3", 300), ("C4", 150), ("C5", 40)])
 def test_emulated_fp64_is_bit_exact(rocm, tapes, name, paths, ckpt):
+    """With libm Box-Muller (NT_DEVICE_LIBM, glibc on the host) every fp64 bit matches."""
     flat = tapes[name]
-    sums, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt), paths, rocm=rocm)
+    sums, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1), paths, rocm=rocm)
     ov, og = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
     assert np.array_equal(v, ov)
     assert np.array_equal(g, og)
@@ -48,14 +49,14 @@ def test_emulated_fp64_is_bit_exact(rocm, tapes, name, paths, ckpt):
 def test_segment_lengths_with_tail(rocm, tapes, seg):
     """Segment lengths that do not divide 252 leave a tail segment."""
     flat = tapes["C2"]
-    _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=1, seg_len=seg), 200, rocm=rocm)
+    _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=1, seg_len=seg, libm=1), 200, rocm=rocm)
     ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, threads=1)
     assert np.array_equal(v, ov) and np.array_equal(g, og)
 
 
 def test_unrolled_straight_line_matches(rocm, tapes):
     flat = equity_tape_flat = tapes["C2"]
-    _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1), 64, rocm=rocm)
+    _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1, libm=1), 64, rocm=rocm)
     ov, og = oracle.replay_paths(flat, 64, OFFSET, 42, threads=1)
     assert np.array_equal(v, ov) and np.array_equal(g, og)
 
@@ -63,10 +64,18 @@ def test_unrolled_straight_line_matches(rocm, tapes):
 def test_price_only_and_moved_inputs(rocm, tapes):
     flat = tapes["C3"]
     x = [95.0, 101.0, 0.3, 0.01, 0.75]
-    sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False), 200, inputs=x, rocm=rocm)
+    sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False, libm=1), 200, inputs=x, rocm=rocm)
     ov, _ = oracle.replay_paths(flat, 200, OFFSET, 42, inputs=x, threads=1)
     assert np.array_equal(v, ov)
     assert np.all(sums[2:] == 0.0)
+
+
+@pytest.mark.parametrize("name,paths", [("C1", 700), ("C2", 300), ("C3", 200), ("C4", 100), ("C5", 30)])
+def test_emulated_own_math_within_1e12(rocm, tapes, name, paths):
+    """The skeleton's own log/sqrt/sincos keep paths within the per-path bar."""
+    flat = tapes[name]
+    _, v, g = run_emulated(flat, rocm.options("fp64"), paths, rocm=rocm)
+    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
 
 
 @pytest.mark.parametrize("name", ["C2", "C3"])
@@ -85,7 +94,7 @@ def test_lookback_and_digital_tapes(nt, rocm):
                     nt.ExoticProducts.barrier(nt.OptionTypeEnum.PUT, nt.ExoticProducts.BarrierEnum.UP_OUT, 120.0, 2.0)):
         flat = equity_tape(nt, product, m, 24).flat()
         for ckpt in (1, 2, 3):
-            _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt), 96, rocm=rocm)
+            _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1), 96, rocm=rocm)
             ov, og = oracle.replay_paths(flat, 96, OFFSET, 42, threads=1)
             assert np.array_equal(v, ov) and np.array_equal(g, og), (product.label, ckpt)
 

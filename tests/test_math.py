@@ -1,0 +1,112 @@
+"""Accuracy of the skeleton's own fp64 log / sqrt / sincos (nt_skeleton.h),
+built for the host, against mpmath at 40 digits; and of the Box-Muller pair
+against the oracle's glibc evaluation of the reference formula."""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+import tempfile
+from pathlib import Path
+
+import mpmath as mp
+import numpy as np
+import pytest
+
+import oracle
+from conftest import ROOT
+
+mp.mp.dps = 40
+EMU = ROOT / "tests" / "host_emu"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    out = Path(tempfile.gettempdir()) / "nt_math_emu.so"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-ffp-contract=off", "-w",
+                    f"-I{ROOT / 'nablatensor_amd' / 'csrc'}", f"-I{EMU}", str(EMU / "math_main.cpp"),
+                    "-o", str(out)], check=True)
+    L = C.CDLL(str(out))
+    P = C.POINTER
+    L.emu_neg2log.argtypes = [P(C.c_uint32), P(C.c_double), C.c_long]
+    L.emu_sincos.argtypes = [P(C.c_uint32), P(C.c_double), P(C.c_double), C.c_long]
+    L.emu_sqrt.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
+    L.emu_normal_pair.argtypes = [P(C.c_uint32)] * 3 + [P(C.c_double)] * 2 + [C.c_long]
+    return L
+
+
+def _u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def _ptr(a, t):
+    return a.ctypes.data_as(C.POINTER(t))
+
+
+def ulp_err(got: float, want) -> float:
+    w = float(want)
+    if w == 0.0:
+        return abs(got) / 5e-324
+    return float(abs(mp.mpf(got) - want) / mp.mpf(np.spacing(abs(w))))
+
+
+def sample_u32(n: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    edges = [0, 1, 2, 3, 2**29 - 1, 2**29, 2**29 + 1, 2**30 - 1, 2**30, 2**31 - 1, 2**31, 3 * 2**30 - 1,
+             3 * 2**30, 2**32 - 2**29 - 1, 2**32 - 2**29, 2**32 - 3, 2**32 - 2, 2**32 - 1]
+    return _u32(np.concatenate([edges, rng.integers(0, 2**32, n, dtype=np.uint64)]))
+
+
+def test_neg2log_within_two_ulp(lib):
+    c = sample_u32(3000, 1)
+    near_one = _u32(2**32 - 1 - np.arange(0, 200000, 997))
+    c = _u32(np.concatenate([c, near_one]))
+    out = np.zeros(len(c))
+    lib.emu_neg2log(_ptr(c, C.c_uint32), _ptr(out, C.c_double), len(c))
+    worst = 0.0
+    for ci, oi in zip(c, out):
+        u = (mp.mpf(int(ci)) + mp.mpf(0.5)) / mp.mpf(2) ** 32
+        worst = max(worst, ulp_err(oi, -2 * mp.log(u)))
+    assert worst <= 2.0, worst
+
+
+def test_sincos_within_two_ulp(lib):
+    c = sample_u32(3000, 2)
+    s = np.zeros(len(c))
+    co = np.zeros(len(c))
+    lib.emu_sincos(_ptr(c, C.c_uint32), _ptr(s, C.c_double), _ptr(co, C.c_double), len(c))
+    worst = 0.0
+    for ci, si, cj in zip(c, s, co):
+        u = (int(ci) + 0.5) * 2.0**-32
+        th = mp.mpf(6.283185307179586 * u)  # the reference's rounded angle
+        # error relative to the unit circle scale: sin near 0 is judged in absolute terms
+        worst = max(worst, float(abs(mp.mpf(si) - mp.sin(th)) / mp.mpf(2.0**-53)),
+                    float(abs(mp.mpf(cj) - mp.cos(th)) / mp.mpf(2.0**-53)))
+    assert worst <= 2.0, worst
+
+
+def test_sqrt_within_one_ulp(lib):
+    rng = np.random.default_rng(3)
+    a = np.ascontiguousarray(np.concatenate([np.exp(rng.uniform(np.log(2e-10), np.log(46.0), 20000)),
+                                             [2.3283064365386963e-10, 45.75, 1.0, 2.0, 0.5]]))
+    out = np.zeros(len(a))
+    lib.emu_sqrt(_ptr(a, C.c_double), _ptr(out, C.c_double), len(a))
+    err = np.abs(out - np.sqrt(a)) / np.spacing(np.sqrt(a))
+    assert err.max() <= 1.0
+
+
+def test_normal_pairs_track_the_reference_formula(lib):
+    """The pair equals the oracle's draws (glibc log/sqrt/sin/cos of the
+    rounded 2 pi u2) to within 4e-15 absolute, for draws 0 and 1 of many paths."""
+    paths = np.arange(0, 4000, dtype=np.uint64) * 7919 + 0x100000003
+    seed = 42
+    lo = _u32((paths & 0xFFFFFFFF) ^ (seed & 0xFFFFFFFF))
+    hi = _u32((paths >> 32) ^ (seed >> 32))
+    ctr = _u32(np.zeros(len(paths)))
+    zc = np.zeros(len(paths))
+    zs = np.zeros(len(paths))
+    lib.emu_normal_pair(_ptr(lo, C.c_uint32), _ptr(hi, C.c_uint32), _ptr(ctr, C.c_uint32),
+                        _ptr(zc, C.c_double), _ptr(zs, C.c_double), len(paths))
+    ref_c = np.array([oracle.normal(int(p), seed, 0) for p in paths])
+    ref_s = np.array([oracle.normal(int(p), seed, 1) for p in paths])
+    assert np.max(np.abs(zc - ref_c)) <= 4e-15
+    assert np.max(np.abs(zs - ref_s)) <= 4e-15
