@@ -29,9 +29,12 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 WORKLOAD = "Asian call, GBM, 252 fixings, ATM 1y, value + 5 Greeks"
-# Reference rocm engine, same tape/seed/2M scenarios, fp64, on a Radeon 780M
-# (gfx1103): docs/examples/asian-greeks.md:43 in the reference repository.
-REFERENCE_ROCM_FP64 = 2.16e6
+
+
+def workload_tape(name: str):
+    from nablatensor_amd import workloads
+
+    return workloads.workload_tapes()[name].flat()
 
 
 def measured_traffic(precision: str, info: dict) -> dict | None:
@@ -112,6 +115,30 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def other_workload(rocm, args) -> int:
+    from nablatensor_amd import workloads
+
+    desc, paths, seed, prec = workloads.DESCRIPTIONS[args.workload]
+    prec = args.precision or prec
+    paths = args.paths if args.paths != 2_000_000 else paths
+    flat = workload_tape(args.workload)
+    print(f"[bench] {args.workload} {desc}: {len(flat['op'])} nodes, {paths:,} scenarios/step, {prec}",
+          file=sys.stderr, flush=True)
+    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg)
+    out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f64" if prec == "fp64" else "f32", "data": f"synthetic (Philox2x32-10 normals, seed {seed})",
+           "config": {"workload": f"{args.workload}: {desc}", "scenarios_per_step": paths, "seed": seed,
+                      "nodes": len(flat["op"]), "inputs": len(flat["input_node"])},
+           "roofline": m["roofline"], "kernel_ms": m["kernel_ms"], "replay_kernel_ms": m["replay_kernel_ms"],
+           "kernel": m["kernel"]}
+    if args.workload == "C5":
+        out["projection_1e10_seconds"] = 1e10 / m["value"]
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,6 +151,10 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1_000_000)
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
+                    help="C2 (default) prints the headline line; the others print the same fields for that workload")
+    ap.add_argument("--precision", choices=["fp64", "fp32"], default=None,
+                    help="precision of a non-default workload (default: the workload's own)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -141,6 +172,8 @@ def main() -> int:
     if rocm.probe() < 1:
         print("no gfx950 device visible", file=sys.stderr)
         return 1
+    if args.workload != "C2":
+        return other_workload(rocm, args)
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()
     print(f"[bench] {WORKLOAD}: {len(flat['op'])} nodes, {args.paths:,} scenarios/step", file=sys.stderr, flush=True)
     f64 = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg)

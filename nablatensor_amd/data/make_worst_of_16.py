@@ -5,6 +5,7 @@ PCG64 seeded with 42, made positive definite by flooring its eigenvalues at
 1e-3 and rescaling to a unit diagonal. Vols: uniform in [0.15, 0.40] from the
 same generator. The Cholesky factor is included for reference; the host layer
 recomputes it (CorrelatedNormals.of) from `corr`.
+Run: python nablatensor_amd/data/make_worst_of_16.py
 """
 import json
 from pathlib import Path

@@ -1,0 +1,50 @@
+"""The five benchmark workloads as recorded tapes.
+
+C1 European call (1 exact GBM step), C2 arithmetic Asian call (252 fixings),
+C3 down-and-in barrier call (252 smoothed daily monitors, barrier 80,
+width 1.0), C4 Heston-Asian call (504 full-truncation Euler steps, rho -0.7),
+C5 worst-of call on 16 correlated GBM assets (252 steps). C1-C3 are the
+reference's own products (Products.europeanCall/asianCall,
+ExoticProducts.BarrierOption); C4 and C5 have no reference product and are
+recorded from its building blocks (HestonModel.step, CorrelatedNormals,
+GbmPath) by HestonModel::asian and WorstOfBasket::call. The C5 correlation
+and vols are the fixed inputs in data/worst_of_16.json.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+DATA = Path(__file__).resolve().parent / "data"
+
+DESCRIPTIONS = {
+    "C1": ("European call, GBM, 1 exact step, ATM 1y, value + 4 Greeks", 1_000_000, 42, "fp64"),
+    "C2": ("Asian call, GBM, 252 fixings, ATM 1y, value + 5 Greeks", 2_000_000, 42, "fp64"),
+    "C3": ("Down-and-in barrier call, GBM, 252 daily monitors, barrier 80, width 1.0, value + 5 Greeks",
+           20_000_000, 42, "fp32"),
+    "C4": ("Heston-Asian call, 504 full-truncation Euler steps, value + 8 adjoints", 10_000_000, 7, "fp64"),
+    "C5": ("Worst-of call on 16 correlated GBM assets, 252 steps, value + 33 adjoints, 1e6 scenarios per launch",
+           1_000_000, 42, "fp32"),
+}
+
+
+def worst_of_inputs() -> dict:
+    return json.loads((DATA / "worst_of_16.json").read_text())
+
+
+def workload_tapes(steps_c4: int = 504, steps_c5: int = 252) -> dict:
+    from . import _host as nt
+
+    m = nt.EquityMarket.atmOneYear()
+    barrier = nt.ExoticProducts.barrier(nt.OptionTypeEnum.CALL, nt.ExoticProducts.BarrierEnum.DOWN_IN, 80.0, 1.0)
+    heston = nt.HestonMarket.create(spot=100, strike=100, rate=0.03, v0=0.04, kappa=2.0, theta=0.04, xi=0.5, rho=-0.7)
+    out = {
+        "C1": nt.record(nt.Products.europeanCall(), m, nt.TimeGrid.uniform(1)),
+        "C2": nt.record(nt.Products.asianCall(), m, nt.TimeGrid.uniform(252)),
+        "C3": nt.record(barrier, m.withVol(0.25), nt.TimeGrid.uniform(252)),
+        "C4": nt.record(nt.HestonModel.asian(nt.OptionTypeEnum.CALL, 2.0, steps_c4), heston),
+    }
+    fx = worst_of_inputs()
+    basket = nt.WorstOfBasket.market([100.0] * 16, fx["sigma"], 0.03)
+    out["C5"] = nt.record(nt.WorstOfBasket.call(fx["corr"], 100.0, 1.0, steps_c5), basket)
+    return out

@@ -20,6 +20,11 @@ sys.path.insert(0, str(ROOT / "tests"))
 GOLDEN = ROOT / "tests" / "golden"
 
 
+def reference_values() -> dict:
+    """Values held by the reference repository (tests/golden/reference_values.json)."""
+    return json.loads((GOLDEN / "reference_values.json").read_text())
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device and the built HIP engine")
 
@@ -34,25 +39,10 @@ def equity_tape(nt, product, market, steps):
     return nt.record(product, market, nt.TimeGrid.uniform(steps))
 
 
-def worst_of_fixture() -> dict:
-    return json.loads((GOLDEN / "worst_of_16.json").read_text())
-
-
 def workload_tapes(nt, steps_c4: int = 504, steps_c5: int = 252) -> dict:
-    """Tapes of the five workloads (market inputs fixed, seeds as in the bench configs)."""
-    m = nt.EquityMarket.atmOneYear()
-    barrier = nt.ExoticProducts.barrier(nt.OptionTypeEnum.CALL, nt.ExoticProducts.BarrierEnum.DOWN_IN, 80.0, 1.0)
-    heston = nt.HestonMarket.create(spot=100, strike=100, rate=0.03, v0=0.04, kappa=2.0, theta=0.04, xi=0.5, rho=-0.7)
-    out = {
-        "C1": equity_tape(nt, nt.Products.europeanCall(), m, 1),
-        "C2": equity_tape(nt, nt.Products.asianCall(), m, 252),
-        "C3": equity_tape(nt, barrier, m.withVol(0.25), 252),
-        "C4": nt.record(nt.HestonModel.asian(nt.OptionTypeEnum.CALL, 2.0, steps_c4), heston),
-    }
-    fx = worst_of_fixture()
-    basket = nt.WorstOfBasket.market([100.0] * 16, fx["sigma"], 0.03)
-    out["C5"] = nt.record(nt.WorstOfBasket.call(fx["corr"], 100.0, 1.0, steps_c5), basket)
-    return out
+    """Tapes of the five workloads (nablatensor_amd/workloads.py)."""
+    from nablatensor_amd import workloads
+    return workloads.workload_tapes(steps_c4, steps_c5)
 
 
 @pytest.fixture(scope="session")
