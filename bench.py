@@ -2,9 +2,11 @@
 """Throughput of the fused forward+adjoint Monte-Carlo replay on one MI355X.
 
 Workload: arithmetic-average Asian call under GBM, 252 daily fixings, ATM 1y
-(S0=K=100, sigma=0.20, r=0.03, T=1), value + 5 first-order Greeks from one
-reverse sweep, 2,000,000 scenarios per step, Philox seed 42; the headline is
-fp64 and the fp32 run is reported beside it. A step is one replay (one
+(S0=K=100, sigma=0.20, r=0.03, T=1), value + 5 first-order Greeks, 2,000,000
+scenarios per step, Philox seed 42; the headline is fp64 and the fp32 run is
+reported beside it. The engine's default derivative mode (the lowering's cost
+model: tangent for this tape) is the headline; the reverse-sweep kernel of the
+same tape is timed beside it under "reverse". A step is one replay (one
 dispatch through the C ABI: replay kernel, deterministic finishing kernel,
 sums copied back) over a fresh range of 2,000,000 scenarios; inputs are
 resident on the device before timing starts.
@@ -29,6 +31,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 WORKLOAD = "Asian call, GBM, 252 fixings, ATM 1y, value + 5 Greeks"
+MODES = {1: "reverse", 2: "tangent"}
+# The reference's rocm engine, fp64, same tape, 2,000,000 scenarios, seed 42, on a
+# Radeon 780M (gfx1103): docs/examples/asian-greeks.md:43.
+REFERENCE_ROCM_FP64 = 2.16e6
 
 
 def workload_tape(name: str):
@@ -46,15 +52,16 @@ def measured_traffic(precision: str, info: dict) -> dict | None:
     for line in path.read_text().splitlines():
         if line.startswith("traffic:"):
             kv = dict(item.split("=") for item in line.split()[1:])
-            if int(kv["checkpoint"]) == info["checkpoint"] and int(kv["seg_len"]) == info["seg_len"]:
+            if (int(kv.get("mode", 1)) == info["mode"] and int(kv["checkpoint"]) == info["checkpoint"]
+                    and int(kv["seg_len"]) == info["seg_len"]):
                 return {"bytes": float(kv["bytes"]), "source": str(path.relative_to(ROOT))}
     return None
 
 
-def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg):
+def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0):
     from nablatensor_amd import flops
 
-    with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg)) as x:
+    with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode)) as x:
         info = x.info()
         for w in range(warmup):
             x.replay(paths, w * paths, seed)
@@ -82,8 +89,9 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg):
                      "traffic_source": None if traffic is None else traffic["source"],
                      "algorithmic_bytes": 8 * (len(flat["input_node"]) + info["grid_cap"] * (2 + len(flat["input_node"]))),
                      "flops_per_scenario": fl, "convention": "NT-FLOP v1"},
-        "kernel": {k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
-                                        "loop_iters", "seg_len", "checkpoint", "tape_slots", "grid_cap")},
+        "kernel": {**{k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
+                                           "loop_iters", "seg_len", "checkpoint", "tape_slots", "grid_cap")},
+                   "mode": MODES[info["mode"]]},
     }
 
 
@@ -124,7 +132,7 @@ def other_workload(rocm, args) -> int:
     flat = workload_tape(args.workload)
     print(f"[bench] {args.workload} {desc}: {len(flat['op'])} nodes, {paths:,} scenarios/step, {prec}",
           file=sys.stderr, flush=True)
-    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg)
+    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -148,6 +156,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--policy", type=int, default=0, help="checkpoint policy (0 auto, 1 recompute, 2 store draws, 3 store all)")
     ap.add_argument("--seg", type=int, default=0, help="loop iterations per checkpoint segment (0 auto)")
+    ap.add_argument("--mode", type=int, default=0, help="derivative mode (0 cost model, 1 reverse sweep, 2 tangent)")
+    ap.add_argument("--no-reverse", action="store_true", help="skip the reverse-sweep comparison run")
     ap.add_argument("--cpu-sample", type=int, default=1_000_000)
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -176,12 +186,18 @@ def main() -> int:
         return other_workload(rocm, args)
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()
     print(f"[bench] {WORKLOAD}: {len(flat['op'])} nodes, {args.paths:,} scenarios/step", file=sys.stderr, flush=True)
-    f64 = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg)
-    print(f"[bench] fp64 {f64['value']:.3e} scen/s", file=sys.stderr, flush=True)
+    f64 = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg,
+                  args.mode)
+    print(f"[bench] fp64 {f64['kernel']['mode']} {f64['value']:.3e} scen/s", file=sys.stderr, flush=True)
+    rev = None
+    if not args.no_reverse and f64["kernel"]["mode"] != "reverse":
+        rev = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg, 1)
+        print(f"[bench] fp64 reverse {rev['value']:.3e} scen/s", file=sys.stderr, flush=True)
     f32 = None
     if not args.no_fp32:
-        f32 = measure(rocm, flat, "fp32", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg)
-        print(f"[bench] fp32 {f32['value']:.3e} scen/s", file=sys.stderr, flush=True)
+        f32 = measure(rocm, flat, "fp32", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg,
+                      args.mode)
+        print(f"[bench] fp32 {f32['kernel']['mode']} {f32['value']:.3e} scen/s", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(flat, args.cpu_sample, args.seed)
     out = {
         "metric": "scenarios/sec for value+all Greeks (fp64), % of VALU FP64 peak",
@@ -203,6 +219,8 @@ def main() -> int:
         "kernel_ms": f64["kernel_ms"],
         "replay_kernel_ms": f64["replay_kernel_ms"],
         "kernel": f64["kernel"],
+        "reverse": None if rev is None else {k: rev[k] for k in ("value", "ms_per_step", "replay_kernel_ms",
+                                                                  "roofline", "kernel")},
         "fp32": None if f32 is None else {k: f32[k] for k in ("value", "ms_per_step", "replay_kernel_ms",
                                                                "roofline", "kernel")},
         "cpu_baseline": cpu,

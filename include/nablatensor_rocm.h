@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NT_ABI_VERSION 1
+#define NT_ABI_VERSION 2
 
 enum {
   NT_OK = 0,
@@ -69,6 +69,14 @@ enum {
   NT_CKPT_STORE_ALL = 3   /* every value the reverse reads is stored; nothing recomputed */
 };
 
+/* How the first-order Greeks are propagated. Both give the same derivatives
+ * (the pathwise gradient of the output); they differ in cost and rounding. */
+enum {
+  NT_MODE_AUTO = 0,       /* cost model picks one of the below per tape */
+  NT_MODE_REVERSE = 1,    /* adjoint sweep after the forward pass (ScalarReplay.java:129-183) */
+  NT_MODE_TANGENT = 2     /* sparse forward tangents carried with the values, one per input the node depends on */
+};
+
 /* Options (AadOptions.java:42-156 precision/adjoints, plus the engine's own
  * knobs that the reference passes as engineOptions). Zero means default. */
 typedef struct nt_options {
@@ -81,7 +89,8 @@ typedef struct nt_options {
   int32_t roll;             /* 1 (default): roll the step loop when one is found; -1: never */
   int32_t contract;         /* FMA contraction: 0 default (off for fp64, on for fp32), 1 on, -1 off */
   int32_t libm;             /* fp64 Box-Muller: 0 the skeleton's own log/sqrt/sincos, 1 device libm, 2 own log/sqrt + libm sincos */
-  int32_t reserved[7];
+  int32_t mode;             /* NT_MODE_* */
+  int32_t reserved[6];
 } nt_options;
 
 typedef struct nt_exec nt_exec;
@@ -97,6 +106,7 @@ typedef struct nt_exec_info {
   int32_t scratch_bytes;                            /* private segment per lane; 0 means no spill */
   int32_t lds_bytes;
   int32_t block, grid_cap;
+  int32_t mode;                                     /* resolved NT_MODE_REVERSE or NT_MODE_TANGENT */
   double compile_seconds;
 } nt_exec_info;
 

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <sstream>
 
@@ -182,6 +183,8 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
       if (op == NT_OP_CONST && bits(t.c[i]) != bits(t.c[s + j])) return fail;
       if (op == NT_OP_INPUT) return fail;
       if (op == NT_OP_RANDN && (t.b[i] != 0 || t.a[i] != L.rand_base[j] + it * D)) return fail;
+      // one body serves every iteration, so activity must not change along the loop
+      if (t.active[i] != t.active[s1 + j]) return fail;
       const int ar = arity(op);
       for (int slot = 0; slot < ar; ++slot) {
         const int x = slot == 0 ? t.a[i] : t.b[i];
@@ -278,6 +281,11 @@ LoopPlan detect_loop(const TapeIR& t) {
 
 // ---- plan ----------------------------------------------------------------------
 
+namespace {
+int plan_reverse_loop(const TapeIR& t, const nt_options& o, Plan& p, std::string& err);
+void choose_mode(const TapeIR& t, const nt_options& o, Plan& p);
+}  // namespace
+
 int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err) {
   nt_options o{};
   if (opt) o = *opt;
@@ -295,9 +303,19 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   p.n_channels = 2 + t.n_in;
   if (o.checkpoint < NT_CKPT_AUTO || o.checkpoint > NT_CKPT_STORE_ALL) { err = "unknown checkpoint policy"; return NT_E_INVALID; }
   if (o.seg_len < 0) { err = "seg_len must be >= 0"; return NT_E_INVALID; }
+  if (o.mode < NT_MODE_AUTO || o.mode > NT_MODE_TANGENT) { err = "unknown derivative mode"; return NT_E_INVALID; }
   if (o.roll >= 0) p.loop = detect_loop(t);
-  if (!p.loop.found) return NT_OK;
+  if (p.loop.found) {
+    const int rc = plan_reverse_loop(t, o, p, err);
+    if (rc != NT_OK) return rc;
+  }
+  choose_mode(t, o, p);
+  return NT_OK;
+}
 
+namespace {
+
+int plan_reverse_loop(const TapeIR& t, const nt_options& o, Plan& p, std::string& err) {
   LoopPlan& L = p.loop;
   const int P = L.period, s = L.start;
   p.taped.assign(P, 0);
@@ -397,6 +415,153 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   p.tape_slots = p.ck_slots + L.iters * p.n_stored;
   return NT_OK;
 }
+
+// Input dependency sets: INPUT j -> {j}; CONST and draws -> {}; otherwise the
+// union over the operands. A node is active exactly when its set is non-empty.
+void compute_deps(const TapeIR& t, Plan& p) {
+  const int W = std::max(1, (t.n_in + 63) / 64);
+  p.n_words = W;
+  p.deps.assign(static_cast<size_t>(t.n) * W, 0);
+  for (int i = 0; i < t.n; ++i) {
+    uint64_t* d = &p.deps[static_cast<size_t>(i) * W];
+    const int op = t.op[i];
+    if (op == NT_OP_INPUT) {
+      d[t.a[i] >> 6] |= uint64_t{1} << (t.a[i] & 63);
+      continue;
+    }
+    const int ar = arity(op);
+    for (int slot = 0; slot < ar; ++slot) {
+      const uint64_t* x = &p.deps[static_cast<size_t>(slot == 0 ? t.a[i] : t.b[i]) * W];
+      for (int w = 0; w < W; ++w) d[w] |= x[w];
+    }
+  }
+  p.posdeps.clear();
+  if (!p.loop.found) return;
+  const LoopPlan& L = p.loop;
+  p.posdeps.assign(static_cast<size_t>(L.period) * W, 0);
+  for (int it = 0; it < L.iters; ++it) {
+    for (int j = 0; j < L.period; ++j) {
+      const uint64_t* x = &p.deps[static_cast<size_t>(L.start + it * L.period + j) * W];
+      for (int w = 0; w < W; ++w) p.posdeps[static_cast<size_t>(j) * W + w] |= x[w];
+    }
+  }
+}
+
+int popcount(const uint64_t* x, int W) {
+  int n = 0;
+  for (int w = 0; w < W; ++w) n += __builtin_popcountll(x[w]);
+  return n;
+}
+
+// Estimated VALU instructions per lane (fp64 weights; fp32 scales them alike).
+double fwd_cost(int op) {
+  switch (op) {
+    case NT_OP_ADD: case NT_OP_SUB: case NT_OP_MUL: return 1;
+    case NT_OP_MAX: case NT_OP_MIN: return 1;
+    case NT_OP_DIV: return 10;
+    case NT_OP_EXP: case NT_OP_LOG: return 20;
+    case NT_OP_SQRT: return 8;
+    case NT_OP_RANDN: return 45;  // half a Box-Muller pair with its Philox block
+    default: return 0;
+  }
+}
+
+double rev_cost(int op, bool aa, bool ba) {
+  const double A = aa ? 1 : 0, B = ba ? 1 : 0;
+  switch (op) {
+    case NT_OP_ADD: case NT_OP_SUB: return A + B;
+    case NT_OP_MUL: return 2 * (A + B);
+    case NT_OP_DIV: return 11 * A + 13 * B;
+    case NT_OP_NEG: return A;
+    case NT_OP_EXP: return 2 * A;
+    case NT_OP_LOG: return 11 * A;
+    case NT_OP_SQRT: return 12 * A;
+    case NT_OP_ABS: return 3 * A;
+    case NT_OP_MAX: case NT_OP_MIN: return 3 * (A + B);
+    default: return 0;
+  }
+}
+
+// Extra work of one active node in tangent mode: per dependency j, the local
+// rule; once per node, the factor it shares across j (a reciprocal, a sign, a
+// branch condition).
+double tan_cost(const TapeIR& t, const Plan& p, int i) {
+  const int W = p.n_words;
+  const int op = t.op[i];
+  const int ar = arity(op);
+  if (ar == 0) return 0;
+  const uint64_t* da = &p.deps[static_cast<size_t>(t.a[i]) * W];
+  const uint64_t* db = ar >= 2 ? &p.deps[static_cast<size_t>(t.b[i]) * W] : nullptr;
+  double c = 0;
+  for (int w = 0; w < W; ++w) {
+    const uint64_t a = da[w], b = db ? db[w] : 0;
+    const double both = __builtin_popcountll(a & b), any = __builtin_popcountll(a | b);
+    switch (op) {
+      case NT_OP_ADD: case NT_OP_SUB: c += both; break;
+      case NT_OP_MUL: c += any + both; break;
+      case NT_OP_DIV: c += any + both; break;
+      case NT_OP_NEG: break;
+      case NT_OP_MAX: case NT_OP_MIN: c += 2 * any; break;
+      default: c += any; break;
+    }
+  }
+  switch (op) {
+    case NT_OP_DIV: c += 11; break;
+    case NT_OP_LOG: case NT_OP_SQRT: c += 10; break;
+    case NT_OP_ABS: case NT_OP_MAX: case NT_OP_MIN: c += 1; break;
+    default: break;
+  }
+  return c;
+}
+
+void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
+  p.mode = NT_MODE_REVERSE;
+  if (!p.adjoints) return;
+  compute_deps(t, p);
+  const LoopPlan& L = p.loop;
+  const int le = L.found ? L.end() : 0;
+  double rev = 0, tan = 0;
+  for (int i = 0; i < t.n; ++i) {
+    const int ar = arity(t.op[i]);
+    const bool inLoop = L.found && i >= L.start && i < le;
+    if (inLoop && p.ckpt == NT_CKPT_RECOMPUTE && !t.active[i]) rev += fwd_cost(t.op[i]);
+    if (!t.active[i] || ar == 0) continue;
+    const bool aa = t.active[t.a[i]] != 0;
+    const bool ba = ar >= 2 && t.active[t.b[i]] != 0;
+    rev += rev_cost(t.op[i], aa, ba);
+    if (inLoop && p.ckpt != NT_CKPT_STORE_ALL) rev += fwd_cost(t.op[i]);  // the reverse recomputes it
+    tan += tan_cost(t, p, i);
+  }
+  if (L.found) rev += 8.0 * L.iters * p.n_stored;  // store, reload and the HBM round trip
+  p.cost_reverse = rev;
+  p.cost_tangent = tan;
+  const bool tangent = o.mode == NT_MODE_TANGENT || (o.mode == NT_MODE_AUTO && tan < rev);
+  if (!tangent) return;
+  p.mode = NT_MODE_TANGENT;
+  p.ckpt = 0;
+  p.stored.assign(p.stored.size(), 0);
+  p.store_index.assign(p.store_index.size(), -1);
+  p.n_stored = 0;
+  p.ck_slots = p.tape_slots = 0;
+  if (!L.found) return;
+  // Iterations per loop trip: two when the registers the carried state and
+  // its tangents hold leave room (and always an even count when a step draws
+  // an odd number of normals, so both Box-Muller legs stay in one trip).
+  const int W = p.n_words;
+  int live = 0;
+  for (int j = 0; j < L.period; ++j) {
+    if (L.is_carry[j] || L.is_liveout[j]) live += 1 + popcount(&p.posdeps[static_cast<size_t>(j) * W], W);
+  }
+  const int w = p.precision == NT_FP64 ? 2 : 1;
+  int seg = o.seg_len > 0 ? o.seg_len : (live * w <= 64 ? 2 : 1);
+  if ((L.draws & 1) && (seg & 1)) seg += 1;
+  seg = std::max(1, std::min(seg, L.iters));
+  p.seg = seg;
+  p.nseg_full = L.iters / seg;
+  p.tail = L.iters % seg;
+}
+
+}  // namespace
 
 // ---- emission --------------------------------------------------------------------
 
@@ -503,6 +668,7 @@ class Emitter {
   // ---- straight-line regions ----
   std::string vname(int node) const;        // forward value of a straight-line node or live-out
   std::string dname(int node) const;        // adjoint of an active straight-line node or live-out
+  void line_draw(int lo, int i);
   void line_forward(int lo, int hi);
   void line_reverse(int lo, int hi);
 
@@ -510,6 +676,34 @@ class Emitter {
   std::string body_value(int u, int kind, int ref, bool recompute) const;
   void segment(int U, const std::string& sg, bool forward);
   int draw_partner(int U, int rel, int& pu, int& pj) const;
+
+  // ---- tangent mode ----
+  // Tangent names: "" for a structural zero, "#1" for the seed of an INPUT
+  // node, otherwise a variable.
+  bool has(int node, int j) const {
+    return (p_.deps[static_cast<size_t>(node) * p_.n_words + (j >> 6)] >> (j & 63)) & 1;
+  }
+  bool poshas(int pos, int j) const {
+    return (p_.posdeps[static_cast<size_t>(pos) * p_.n_words + (j >> 6)] >> (j & 63)) & 1;
+  }
+  std::vector<int> deplist(int node) const {
+    std::vector<int> d;
+    for (int j = 0; j < t_.n_in; ++j) if (has(node, j)) d.push_back(j);
+    return d;
+  }
+  std::vector<int> posdeplist(int pos) const {
+    std::vector<int> d;
+    for (int j = 0; j < t_.n_in; ++j) if (poshas(pos, j)) d.push_back(j);
+    return d;
+  }
+  std::string tname(int node, int j) const;  // straight-line node or loop live-out
+  void tangent(const std::string& ind, int op, const std::string& tn, const std::vector<int>& D, const std::string& Vi,
+               const std::string& Va, const std::string& Vb, const std::function<std::string(int)>& ta,
+               const std::function<std::string(int)>& tb);
+  void tline(int lo, int hi);
+  void tsegment(int U, const std::string& sg);
+  void body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const;
+  std::string run_tangent();
 };
 
 std::string Emitter::vname(int node) const {
@@ -526,24 +720,30 @@ std::string Emitter::dname(int node) const {
   return "d" + std::to_string(node);
 }
 
+// A draw of a straight-line region; both legs of a Philox block come from one
+// nt_normal_pair call (pairs_ is per region, `lo` keeps the names unique).
+void Emitter::line_draw(int lo, int i) {
+  const int k = t_.a[i];
+  const int ctr = k >> 1;
+  auto it = pairs_.find(ctr);
+  std::string stem;
+  if (it == pairs_.end()) {
+    stem = "zl" + std::to_string(lo) + "_" + std::to_string(ctr);
+    o_ << "    real " << stem << "c, " << stem << "s;\n";
+    o_ << "    nt_normal_pair(rlo, rhi, " << ctr << "u, " << stem << "c, " << stem << "s);\n";
+    pairs_[ctr] = stem;
+  } else {
+    stem = it->second;
+  }
+  o_ << "    const real v" << i << " = " << stem << ((k & 1) ? "s" : "c") << ";\n";
+}
+
 void Emitter::line_forward(int lo, int hi) {
   pairs_.clear();
   for (int i = lo; i < hi; ++i) {
     const int op = t_.op[i];
     if (op == NT_OP_RANDN) {
-      const int k = t_.a[i];
-      const int ctr = k >> 1;
-      auto it = pairs_.find(ctr);
-      std::string stem;
-      if (it == pairs_.end()) {
-        stem = "zl" + std::to_string(lo) + "_" + std::to_string(ctr);
-        o_ << "    real " << stem << "c, " << stem << "s;\n";
-        o_ << "    nt_normal_pair(rlo, rhi, " << ctr << "u, " << stem << "c, " << stem << "s);\n";
-        pairs_[ctr] = stem;
-      } else {
-        stem = it->second;
-      }
-      o_ << "    const real v" << i << " = " << stem << ((k & 1) ? "s" : "c") << ";\n";
+      line_draw(lo, i);
       continue;
     }
     const int ar = arity(op);
@@ -686,7 +886,254 @@ void Emitter::segment(int U, const std::string& sg, bool forward) {
   o_ << "    }\n";
 }
 
+// ---- tangent mode --------------------------------------------------------------
+
+std::string Emitter::tname(int node, int j) const {
+  if (L_.found && node >= L_.start && node < L_.end()) {
+    const int pos = node - (L_.start + (L_.iters - 1) * L_.period);
+    return poshas(pos, j) ? "ts" + std::to_string(pos) + "_" + std::to_string(j) : "";
+  }
+  if (!has(node, j)) return "";
+  if (t_.op[node] == NT_OP_INPUT) return "#1";
+  return "t" + std::to_string(node) + "_" + std::to_string(j);
+}
+
+// Tangent of one active node for each input j in D, named tn + j, from the
+// operand tangents ta(j), tb(j). The local derivatives are those of the
+// reverse rules in rev(): d/da and d/db of ADD SUB MUL DIV NEG EXP LOG SQRT
+// ABS, and MAX/MIN following operand a when a >= b (a <= b), else b.
+void Emitter::tangent(const std::string& ind, int op, const std::string& tn, const std::vector<int>& D,
+                      const std::string& Vi, const std::string& Va, const std::string& Vb,
+                      const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb) {
+  if (D.empty()) return;
+  const std::string one = f32_ ? "1.0f" : "1.0";
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  const std::string FMA = f("fma");
+  auto val = [&](const std::string& T) { return T == "#1" ? one : T; };
+  auto mulv = [&](const std::string& T, const std::string& v) { return T == "#1" ? v : "(" + T + " * " + v + ")"; };
+  bool needB = false;
+  for (int j : D) needB |= !tb(j).empty();
+  const std::string q = tn + "q", r = tn + "r", c = tn + "c";
+  switch (op) {
+    case NT_OP_DIV:
+      o_ << ind << "const real " << q << " = " << one << " / " << Vb << ";\n";
+      if (needB) o_ << ind << "const real " << r << " = " << Vi << " * " << q << ";\n";
+      break;
+    case NT_OP_LOG: o_ << ind << "const real " << q << " = " << one << " / " << Va << ";\n"; break;
+    case NT_OP_SQRT:
+      // sqrt(0) = 0 has an infinite local derivative. The reverse sweep never
+      // multiplies it by a zero adjoint (zero adjoints are skipped), so the
+      // factor is capped at a finite 2^(max exponent) here: a zero tangent
+      // (e.g. a full-truncation max(v, 0) that chose the constant) stays zero.
+      o_ << ind << "const real " << q << " = " << f("fmin") << "(" << (f32_ ? "0.5f" : "0.5") << " / " << Vi << ", "
+         << (f32_ ? "0x1p127f" : "0x1p1023") << ");\n";
+      break;
+    case NT_OP_ABS: o_ << ind << "const real " << q << " = " << Va << " < " << zero << " ? -" << one << " : " << one << ";\n"; break;
+    case NT_OP_MAX: o_ << ind << "const bool " << c << " = " << Va << " >= " << Vb << ";\n"; break;
+    case NT_OP_MIN: o_ << ind << "const bool " << c << " = " << Va << " <= " << Vb << ";\n"; break;
+    default: break;
+  }
+  for (int j : D) {
+    const std::string A = ta(j), B = tb(j);
+    std::string e;
+    switch (op) {
+      case NT_OP_ADD:
+        e = A.empty() ? (B.empty() ? "" : val(B)) : (B.empty() ? val(A) : val(A) + " + " + val(B));
+        break;
+      case NT_OP_SUB:
+        e = A.empty() ? (B.empty() ? "" : "-" + val(B)) : (B.empty() ? val(A) : val(A) + " - " + val(B));
+        break;
+      case NT_OP_MUL:
+        if (!A.empty() && !B.empty()) {
+          e = A == "#1" ? FMA + "(" + Va + ", " + val(B) + ", " + Vb + ")"
+                        : FMA + "(" + A + ", " + Vb + ", " + mulv(B, Va) + ")";
+        } else if (!A.empty()) {
+          e = mulv(A, Vb);
+        } else if (!B.empty()) {
+          e = mulv(B, Va);
+        }
+        break;
+      case NT_OP_DIV:
+        if (!A.empty() && !B.empty()) e = FMA + "(" + val(A) + ", " + q + ", -" + mulv(B, r) + ")";
+        else if (!A.empty()) e = mulv(A, q);
+        else if (!B.empty()) e = "-" + mulv(B, r);
+        break;
+      case NT_OP_NEG: if (!A.empty()) e = "-" + val(A); break;
+      case NT_OP_EXP: if (!A.empty()) e = mulv(A, Vi); break;
+      case NT_OP_LOG: case NT_OP_SQRT: case NT_OP_ABS: if (!A.empty()) e = mulv(A, q); break;
+      case NT_OP_MAX: case NT_OP_MIN:
+        if (!A.empty() || !B.empty()) e = c + " ? " + (A.empty() ? zero : val(A)) + " : " + (B.empty() ? zero : val(B));
+        break;
+      default: break;
+    }
+    o_ << ind << "const real " << tn << j << " = " << (e.empty() ? zero : e) << ";\n";
+  }
+}
+
+void Emitter::tline(int lo, int hi) {
+  pairs_.clear();
+  for (int i = lo; i < hi; ++i) {
+    const int op = t_.op[i];
+    if (op == NT_OP_RANDN) {
+      line_draw(lo, i);  // a draw is never active
+      continue;
+    }
+    const int ar = arity(op);
+    const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
+    const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
+    o_ << "    const real v" << i << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+    if (!t_.active[i] || ar == 0) continue;
+    const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
+    tangent("    ", op, "t" + std::to_string(i) + "_", deplist(i), "v" + std::to_string(i), x, y,
+            [&](int j) { return tname(a, j); }, [&](int j) { return b >= 0 ? tname(b, j) : std::string(); });
+  }
+}
+
+void Emitter::body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const {
+  if (kind == ARG_BODY) {
+    fn = [this, u, ref](int j) {
+      return poshas(ref, j) ? "tr" + std::to_string(u) + "_" + std::to_string(ref) + "_" + std::to_string(j) : std::string();
+    };
+  } else if (kind == ARG_CARRY) {
+    fn = [this, u, ref](int j) {
+      if (!poshas(ref, j)) return std::string();
+      return u > 0 ? "tr" + std::to_string(u - 1) + "_" + std::to_string(ref) + "_" + std::to_string(j)
+                   : "ts" + std::to_string(ref) + "_" + std::to_string(j);
+    };
+  } else if (kind == ARG_INV) {
+    fn = [this, ref](int j) { return tname(ref, j); };
+  } else {
+    fn = [](int) { return std::string(); };
+  }
+}
+
+// One trip of U loop iterations: values and their tangents, then the carried
+// state (values and tangents) advances.
+void Emitter::tsegment(int U, const std::string& sg) {
+  const int P = L_.period, s = L_.start, D = L_.draws;
+  const std::string ind = "      ";
+  o_ << "    {\n";
+  o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << p_.seg << "u;\n";
+  o_ << ind << "const nt_u32 kb = it0 * " << D << "u;\n";
+  std::map<int, std::string> pairs;
+  for (int u = 0; u < U; ++u) {
+    for (int j = 0; j < P; ++j) {
+      const int i = s + j;
+      const int op = t_.op[i];
+      const std::string name = "r" + std::to_string(u) + "_" + std::to_string(j);
+      if (op == NT_OP_RANDN) {
+        const int rel = L_.rand_base[j] + u * D;
+        const int key = rel >> 1;
+        auto it = pairs.find(key);
+        std::string stem;
+        if (it == pairs.end()) {
+          stem = "zp" + std::to_string(key);
+          o_ << ind << "real " << stem << "c, " << stem << "s;\n";
+          o_ << ind << "nt_normal_pair(rlo, rhi, (kb >> 1) + " << key << "u, " << stem << "c, " << stem << "s);\n";
+          pairs[key] = stem;
+        } else {
+          stem = it->second;
+        }
+        o_ << ind << "const real " << name << " = " << stem << ((rel & 1) ? "s" : "c") << ";\n";
+        continue;
+      }
+      const int ar = arity(op);
+      const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], false) : "";
+      const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], false) : "";
+      o_ << ind << "const real " << name << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+      if (!t_.active[i] || ar == 0) continue;
+      std::function<std::string(int)> ta, tb;
+      body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
+      body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
+      tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", posdeplist(j), name, x, y, ta, tb);
+    }
+  }
+  for (int j = 0; j < P; ++j) {
+    if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
+    o_ << ind << "st" << j << " = r" << (U - 1) << "_" << j << ";\n";
+    if (!t_.active[s + j]) continue;
+    for (int k : posdeplist(j)) o_ << ind << "ts" << j << "_" << k << " = tr" << (U - 1) << "_" << j << "_" << k << ";\n";
+  }
+  o_ << "    }\n";
+}
+
+std::string Emitter::run_tangent() {
+  const int n = t_.n;
+  const int nin = t_.n_in;
+  const int NCH = p_.n_channels;
+  const bool loop = L_.found;
+  const int ls = loop ? L_.start : n;
+  const int le = loop ? L_.end() : n;
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  const std::string one = f32_ ? "1.0f" : "1.0";
+  o_ << "// generated by nablatensor_amd lowering: " << n << " nodes, " << nin << " inputs, "
+     << (loop ? "rolled loop" : "straight line") << ", tangent mode\n";
+  if (loop) {
+    o_ << "// loop: start " << L_.start << ", period " << L_.period << ", iterations " << L_.iters << ", draws/iter "
+       << L_.draws << ", " << p_.seg << " iterations per trip (" << p_.nseg_full << " trips + tail " << p_.tail << ")\n";
+  }
+  o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent\n";
+  o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
+  if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
+  if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";
+  o_ << "#include \"nt_skeleton.h\"\n";
+  o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
+  o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block << ") void nt_replay(\n"
+     << "    const double* __restrict__ inputs, nt_u64 n_paths, nt_u64 path_offset, nt_u64 seed,\n"
+     << "    double* __restrict__ partials, real* __restrict__ scratch,\n"
+     << "    double* __restrict__ out_v, double* __restrict__ out_g) {\n";
+  o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
+  o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
+  o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
+  bool draws = false;
+  for (int i = 0; i < n; ++i) draws |= t_.op[i] == NT_OP_RANDN;
+  if (draws && !f32_) o_ << "  nt_tables_load();\n";
+  for (int j = 0; j < nin; ++j) o_ << "  const real in" << j << " = (real)inputs[" << j << "];\n";
+  o_ << "  double acc[" << NCH << "];\n";
+  o_ << "  for (int c = 0; c < " << NCH << "; ++c) acc[c] = 0.0;\n";
+  o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
+  o_ << "    const nt_u64 path = p + path_offset;\n";
+  o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
+  o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
+  tline(0, ls);
+  if (loop) {
+    for (int j = 0; j < L_.period; ++j) {
+      if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
+      const int init = L_.is_carry[j] ? L_.carry_init[j] : -1;
+      o_ << "    real st" << j << " = " << (init >= 0 ? "v" + std::to_string(init) : zero) << ";\n";
+      if (!t_.active[L_.start + j]) continue;
+      for (int k : posdeplist(j)) {
+        const std::string tin = init >= 0 ? tname(init, k) : "";
+        o_ << "    real ts" << j << "_" << k << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin) << ";\n";
+      }
+    }
+    if (p_.nseg_full > 0) {
+      o_ << "    for (nt_u32 sg = 0; sg < " << p_.nseg_full << "u; ++sg)\n";
+      tsegment(p_.seg, "sg");
+    }
+    if (p_.tail) tsegment(p_.tail, std::to_string(p_.nseg_full) + "u");
+    tline(le, n);
+  }
+  o_ << "    const double y = (double)" << vname(t_.output) << ";\n";
+  o_ << "    acc[0] += y;\n    acc[1] += y * y;\n";
+  auto grad = [&](int j) {
+    const std::string g = tname(t_.output, j);
+    return g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g;
+  };
+  for (int j = 0; j < nin; ++j) o_ << "    acc[" << 2 + j << "] += " << grad(j) << ";\n";
+  o_ << "#ifdef NT_DUMP_PATHS\n";
+  o_ << "    out_v[p] = y;\n";
+  for (int j = 0; j < nin; ++j) o_ << "    out_g[p * " << nin << "u + " << j << "u] = " << grad(j) << ";\n";
+  o_ << "#endif\n";
+  o_ << "  }\n";
+  o_ << "  __shared__ double nt_lds[" << NCH << " * (" << p_.block << " / 64)];\n";
+  o_ << "  nt_block_store<" << NCH << ">(acc, partials, nt_lds);\n";
+  o_ << "}\n";
+  return o_.str();
+}
+
 std::string Emitter::run() {
+  if (p_.mode == NT_MODE_TANGENT) return run_tangent();
   const int n = t_.n;
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;
@@ -700,7 +1147,7 @@ std::string Emitter::run() {
        << L_.draws << ", segment " << p_.seg << " (" << p_.nseg_full << " full + tail " << p_.tail
        << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
   }
-  o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << "\n";
+  o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << " mode=reverse\n";
   o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
   if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
   if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";

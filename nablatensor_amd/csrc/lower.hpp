@@ -14,6 +14,12 @@
 //             then sweeping its iterations backwards; prologue adjoints.
 // The adjoint accumulation order equals the oracle's node order, so fp64
 // paths agree to rounding (FMA contraction aside).
+//
+// Tangent mode emits no reverse sweep: every active value carries the
+// derivatives with respect to the inputs it depends on (a sparse set known at
+// lowering time), propagated by the same local derivative rules. A Monte-Carlo
+// step body then needs neither checkpoints nor recomputation; the cost model
+// in make_plan picks it when those savings exceed the extra tangent work.
 #pragma once
 
 #include <cstdint>
@@ -51,6 +57,11 @@ struct LoopPlan {
 
 struct Plan {
   int precision = NT_FP64;
+  int mode = NT_MODE_REVERSE;             // resolved NT_MODE_REVERSE or NT_MODE_TANGENT
+  int n_words = 0;                        // 64-bit words per dependency set
+  std::vector<uint64_t> deps;             // node -> inputs it depends on (bitset), tangent mode
+  std::vector<uint64_t> posdeps;          // loop position -> union over the iterations
+  double cost_reverse = 0, cost_tangent = 0;  // estimated extra VALU work per path of each mode
   int adjoints = 1;
   int block = 256;
   bool contract = false;                  // FMA contraction allowed in the generated code

@@ -232,6 +232,7 @@ void fill_static_info(const Lowered& l, nt_exec_info& info) {
   info.n_segments = l.plan.nseg_full + (l.plan.tail ? 1 : 0);
   info.checkpoint = L.found ? l.plan.ckpt : 0;
   info.tape_slots = l.plan.tape_slots;
+  info.mode = l.plan.mode;
   info.block = l.plan.block;
 }
 

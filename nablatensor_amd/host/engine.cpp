@@ -409,6 +409,7 @@ std::unique_ptr<AadExecutable> RocmAadEngine::compile(TapePtr tape, const AadOpt
   o.roll = optionInt(options, "roll", 1);
   o.contract = optionInt(options, "contract", 0);
   o.libm = optionInt(options, "libm", 0);
+  o.mode = optionInt(options, "mode", 0);
   const auto t0 = std::chrono::steady_clock::now();
   nt_exec* exec = nullptr;
   int rc = a.create(&ct, &o, &exec);

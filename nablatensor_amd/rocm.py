@@ -18,6 +18,8 @@ NT_OK = 0
 NT_E_INVALID, NT_E_UNSUPPORTED, NT_E_NO_DEVICE, NT_E_COMPILE, NT_E_CLOSED, NT_E_INTERNAL = -1, -2, -3, -4, -5, -6
 NT_FP64, NT_FP32 = 0, 1
 NT_CKPT_AUTO, NT_CKPT_RECOMPUTE, NT_CKPT_STORE_DRAWS, NT_CKPT_STORE_ALL = 0, 1, 2, 3
+NT_MODE_AUTO, NT_MODE_REVERSE, NT_MODE_TANGENT = 0, 1, 2
+ABI_VERSION = 2
 
 EXPORTS = ("nt_probe", "nt_device_name", "nt_lower", "nt_compile_check", "nt_exec_create", "nt_exec_set_inputs",
            "nt_exec_replay", "nt_exec_replay_paths", "nt_exec_info_get", "nt_exec_source", "nt_exec_destroy",
@@ -34,14 +36,15 @@ class NtTape(C.Structure):
 class NtOptions(C.Structure):
     _fields_ = [("precision", C.c_int32), ("adjoints", C.c_int32), ("block", C.c_int32),
                 ("max_blocks", C.c_int32), ("checkpoint", C.c_int32), ("seg_len", C.c_int32),
-                ("roll", C.c_int32), ("contract", C.c_int32), ("libm", C.c_int32), ("reserved", C.c_int32 * 7)]
+                ("roll", C.c_int32), ("contract", C.c_int32), ("libm", C.c_int32), ("mode", C.c_int32),
+                ("reserved", C.c_int32 * 6)]
 
 
 class NtExecInfo(C.Structure):
     _fields_ = [(name, C.c_int32) for name in (
         "n_nodes", "n_active", "n_inputs", "n_channels", "loop_start", "loop_period", "loop_iters",
         "loop_carries", "seg_len", "n_segments", "checkpoint", "tape_slots", "vgprs", "sgprs", "agprs",
-        "scratch_bytes", "lds_bytes", "block", "grid_cap")] + [("compile_seconds", C.c_double)]
+        "scratch_bytes", "lds_bytes", "block", "grid_cap", "mode")] + [("compile_seconds", C.c_double)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -110,9 +113,9 @@ class TapeArrays:
 
 def options(precision: str = "fp64", adjoints: bool = True, block: int = 0, max_blocks: int = 0,
             checkpoint: int = NT_CKPT_AUTO, seg_len: int = 0, roll: int = 1, contract: int = 0,
-            libm: int = 0) -> NtOptions:
+            libm: int = 0, mode: int = 0) -> NtOptions:
     return NtOptions(NT_FP32 if precision == "fp32" else NT_FP64, 1 if adjoints else 0, block, max_blocks,
-                     checkpoint, seg_len, roll, contract, libm)
+                     checkpoint, seg_len, roll, contract, libm, mode)
 
 
 def probe() -> int:

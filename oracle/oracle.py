@@ -160,7 +160,19 @@ def conditioning(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs
 def path_errors(values, grads, ref_values, ref_grads):
     """Per path: value error |dv| / max(1, |v|) and normwise gradient error
     max_j |dg_j| / max(1, max_j |g_j|)."""
-    ev = np.abs(values - ref_values) / np.maximum(1.0, np.abs(ref_values))
-    scale = np.maximum(1.0, np.max(np.abs(ref_grads), axis=1)) if ref_grads.size else np.ones(len(values))
-    eg = np.max(np.abs(grads - ref_grads), axis=1) / scale if ref_grads.size else np.zeros(len(values))
+    def absdiff(a, b):
+        # equal values (also equal infinities) and NaN against NaN count as
+        # agreement; any other non-finite difference is an infinite error
+        a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+        with np.errstate(invalid="ignore"):
+            d = np.abs(a - b)
+            d = np.where((a == b) | (np.isnan(a) & np.isnan(b)), 0.0, d)
+        return np.where(np.isnan(d), np.inf, d)
+
+    with np.errstate(invalid="ignore"):
+        ev = absdiff(values, ref_values) / np.maximum(1.0, np.nan_to_num(np.abs(ref_values), nan=1.0))
+        if not ref_grads.size:
+            return ev, np.zeros(len(values))
+        scale = np.maximum(1.0, np.nan_to_num(np.max(np.abs(ref_grads), axis=1), nan=1.0))
+        eg = np.max(absdiff(grads, ref_grads), axis=1) / scale
     return ev, eg

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function(rocm):
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(rocm.EXPORTS)
-    assert lib.nt_abi_version() == 1
+    assert lib.nt_abi_version() == 2
 
 
 @pytest.mark.skipif(gpu_available(), reason="checks the no-device path")

@@ -1,0 +1,71 @@
+"""bench.py's JSON contract, exercised on the CPU with the device measurements
+replaced by fixed numbers (no GPU is touched)."""
+from __future__ import annotations
+
+import json
+import sys
+
+import pytest
+
+import conftest
+
+sys.path.insert(0, str(conftest.ROOT))
+import bench  # noqa: E402
+
+
+def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0):
+    ms = 2.0 if precision == "fp64" else 1.0
+    resolved = "reverse" if mode == 1 else "tangent"
+    return {"value": paths / (ms / 1e3), "ms_per_step": ms, "kernel_ms": ms, "replay_kernel_ms": ms,
+            "kernel_scenarios_per_s": paths / (ms / 1e3),
+            "roofline": {"bound": "valu", "kernel": "nt_replay", "achieved": 10.0, "peak": 78.6, "unit": "TFLOP/s",
+                         "frac": 10.0 / 78.6, "traffic": None, "traffic_source": None, "algorithmic_bytes": 1,
+                         "flops_per_scenario": 18723, "convention": "NT-FLOP v1"},
+            "kernel": {"vgprs": 100, "mode": resolved}}
+
+
+@pytest.fixture
+def patched(monkeypatch):
+    from nablatensor_amd import rocm
+
+    monkeypatch.setattr(rocm, "probe", lambda: 1)
+    monkeypatch.setattr(bench, "measure", fake_measure)
+    monkeypatch.setattr(bench, "cpu_baseline", lambda flat, sample, seed: {
+        "value": 1e6, "unit": "scenarios/s", "cores": 16, "kind": "port", "sample": "fake"})
+
+
+def run_main(monkeypatch, capsys, argv):
+    monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
+    assert bench.main() == 0
+    lines = [ln for ln in capsys.readouterr().out.splitlines() if ln.strip()]
+    assert len(lines) == 1
+    return json.loads(lines[0])
+
+
+def test_headline_line_has_the_contract_fields(patched, monkeypatch, capsys):
+    out = run_main(monkeypatch, capsys, ["--steps", "2", "--warmup", "1"])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in out, key
+    assert out["n_gpus"] == 1 and out["steps"] == 2 and out["warmup"] == 1
+    assert out["dtype"] == "f64" and out["higher_is_better"] is True
+    assert out["vs_baseline"] == pytest.approx(out["value"] / bench.REFERENCE_ROCM_FP64)
+    assert out["roofline"]["frac"] == pytest.approx(out["roofline"]["achieved"] / out["roofline"]["peak"])
+    assert out["cpu_baseline"]["kind"] in ("port", "reference")
+    assert out["reverse"]["kernel"]["mode"] == "reverse"
+    assert out["fp32"]["value"] > 0
+
+
+@pytest.mark.parametrize("workload", ["C1", "C3", "C4", "C5"])
+def test_other_workloads_print_one_line(patched, monkeypatch, capsys, workload):
+    out = run_main(monkeypatch, capsys, ["--workload", workload, "--steps", "1", "--warmup", "0"])
+    assert out["config"]["workload"].startswith(workload)
+    assert out["value"] > 0
+    if workload == "C5":
+        assert out["projection_1e10_seconds"] > 0
+
+
+def test_more_than_one_gpu_is_refused(monkeypatch, capsys):
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "8"])
+    assert bench.main() == 2
+    assert "one GPU" in capsys.readouterr().err

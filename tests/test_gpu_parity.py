@@ -1,6 +1,7 @@
 """GPU parity of the HIP replay engine against the CPU oracle, through the C ABI.
 
-Bars (fp64): per path within 1e-12 of the oracle (value relative with floor 1,
+Both derivative modes (the reverse sweep under each checkpoint policy, and
+tangent mode) are held to the same bars. Bars (fp64): per path within 1e-12 of the oracle (value relative with floor 1,
 gradient normwise) on every path that stays at least 1e-5 from a singular point
 of an active node, with the bound scaled by the conditioning below that
 (conftest.per_path_bounds); sums over paths within 1e-10. fp32 reconciles with the fp64 oracle within 1e-5 on price
@@ -32,49 +33,61 @@ def test_device_is_gfx950(rocm):
     assert arch.startswith("gfx950"), (name, arch)
 
 
+# (derivative mode, checkpoint policy): the reverse sweep under each policy, and tangent mode
+VARIANTS = [(1, 1), (1, 2), (1, 3), (2, 0)]
+
+
 @pytest.mark.parametrize("libm", [0, 1])
-@pytest.mark.parametrize("ckpt", [1, 2, 3])
+@pytest.mark.parametrize("mode,ckpt", VARIANTS)
 @pytest.mark.parametrize("name,paths", [("C1", 4096), ("C2", 2048), ("C3", 1024), ("C4", 512)])
-def test_per_path_fp64_matches_oracle(rocm, tapes, name, paths, ckpt, libm):
+def test_per_path_fp64_matches_oracle(rocm, tapes, name, paths, mode, ckpt, libm):
     t = tapes[name]
-    print(f"case {name} ckpt={ckpt} libm={libm} paths={paths}", flush=True)
-    with rocm.Executable(t, rocm.options("fp64", checkpoint=ckpt, libm=libm)) as x:
+    print(f"case {name} mode={mode} ckpt={ckpt} libm={libm} paths={paths}", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", checkpoint=ckpt, libm=libm, mode=mode)) as x:
         v, g = x.replay_paths(paths, OFFSET, 42)
         info = x.info()
     assert info["scratch_bytes"] == 0
+    assert info["mode"] == mode
     summary = check_per_path(v, g, t, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
     print(summary)
 
 
-def test_per_path_fp64_heston_many_paths(rocm, tapes):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_per_path_fp64_heston_many_paths(rocm, tapes, mode):
     """4096 Heston paths: the conditioning-scaled bound holds on all of them."""
     t = tapes["C4"]
-    with rocm.Executable(t, rocm.options("fp64")) as x:
+    print(f"case C4 mode={mode} paths=4096 seed=7", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         v, g = x.replay_paths(4096, OFFSET, 7)
     print(check_per_path(v, g, t, 4096, OFFSET, 7, min_strict=0.5))
 
 
-def test_per_path_fp64_worst_of_matches_oracle(rocm, tapes):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_per_path_fp64_worst_of_matches_oracle(rocm, tapes, mode):
     t = tapes["C5"]
-    with rocm.Executable(t, rocm.options("fp64")) as x:
+    print(f"case C5 mode={mode} paths=256", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         v, g = x.replay_paths(256, 7, 42)
     print(check_per_path(v, g, t, 256, 7, 42, min_strict=0.99))
 
 
+@pytest.mark.parametrize("mode", [1, 2])
 @pytest.mark.parametrize("name,paths", [("C1", 1_000_000), ("C2", 200_000), ("C3", 100_000)])
-def test_sums_fp64_match_oracle(rocm, tapes, name, paths):
+def test_sums_fp64_match_oracle(rocm, tapes, name, paths, mode):
     t = tapes[name]
-    with rocm.Executable(t, rocm.options("fp64")) as x:
+    print(f"case {name} mode={mode} paths={paths}", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         sums, _ = x.replay(paths, 0, 42)
     ref = oracle.replay_sums(t, paths, 0, 42)
     assert rel_err(sums[[0] + list(range(2, len(sums)))], ref[[0] + list(range(2, len(ref)))], floor=1e-300) <= 1e-10
     assert abs(sums[1] - ref[1]) <= 1e-10 * abs(ref[1])
 
 
-def test_published_asian_aggregates(rocm, tapes):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_published_asian_aggregates(rocm, tapes, mode):
     """Asian call, 252 fixings, ATM 1y, fp64, seed 42, 1,000,000 scenarios:
     the oracle values printed in the reference's evidence pack."""
-    with rocm.Executable(tapes["C2"], rocm.options("fp64")) as x:
+    with rocm.Executable(tapes["C2"], rocm.options("fp64", mode=mode)) as x:
         sums, _ = x.replay(1_000_000, 0, 42)
     r = oracle.to_result(sums, 1_000_000)
     published = {"price": 5.3058639800, "delta": 0.56198939096, "dK": -0.50893075116, "vega": 22.412432861,
@@ -85,10 +98,11 @@ def test_published_asian_aggregates(rocm, tapes):
         assert abs(got[k] - ref) <= 5e-11 * abs(ref), (k, got[k], ref)
 
 
+@pytest.mark.parametrize("mode", [1, 2])
 @pytest.mark.parametrize("name,paths", [("C2", 200_000), ("C3", 100_000)])
-def test_fp32_reconciles_with_fp64_oracle(rocm, tapes, name, paths):
+def test_fp32_reconciles_with_fp64_oracle(rocm, tapes, name, paths, mode):
     t = tapes[name]
-    with rocm.Executable(t, rocm.options("fp32")) as x:
+    with rocm.Executable(t, rocm.options("fp32", mode=mode)) as x:
         sums, _ = x.replay(paths, 0, 42)
     ref = oracle.replay_sums(t, paths, 0, 42)
     got = oracle.to_result(sums, paths)
@@ -96,13 +110,14 @@ def test_fp32_reconciles_with_fp64_oracle(rocm, tapes, name, paths):
     errs = {"price": abs(got["price"] - want["price"]) / abs(want["price"])}
     for j, gj in enumerate(want["gradient"]):
         errs[f"grad{j}"] = abs(got["gradient"][j] - gj) / max(abs(gj), 1e-12)
-    print(name, {k: f"{v:.2e}" for k, v in errs.items()})
+    print(name, "mode", mode, {k: f"{v:.2e}" for k, v in errs.items()})
     assert max(errs.values()) <= 1e-5, errs
 
 
-def test_ragged_path_count_and_offset(rocm, tapes):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_ragged_path_count_and_offset(rocm, tapes, mode):
     t = tapes["C2"]
-    with rocm.Executable(t, rocm.options("fp64", max_blocks=3)) as x:
+    with rocm.Executable(t, rocm.options("fp64", max_blocks=3, mode=mode)) as x:
         sums, _ = x.replay(513, OFFSET, 0x12345678FEDCBA98)
     ref = oracle.replay_sums(t, 513, OFFSET, 0x12345678FEDCBA98)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-12

@@ -2,10 +2,12 @@
 
 The generated kernel source is compiled for the host (tests/host_emu) with the
 same IEEE arithmetic as the oracle (no FMA contraction, glibc libm) and run
-over an emulated grid with the device's scratch indexing. fp64 results must
-then equal the oracle bit for bit: any slip in loop detection, carry handling,
-segment checkpoints, stored values, draw pairing or the order of adjoint
-accumulation shows up as a difference.
+over an emulated grid with the device's scratch indexing. Reverse-mode fp64
+results must then equal the oracle bit for bit: any slip in loop detection,
+carry handling, segment checkpoints, stored values, draw pairing or the order
+of adjoint accumulation shows up as a difference. Tangent mode computes the
+same values bit for bit and the same derivatives in another order, so its
+gradients are held to the per-path bar instead.
 """
 from __future__ import annotations
 
@@ -37,7 +39,7 @@ def rocm():
 def test_emulated_fp64_is_bit_exact(rocm, tapes, name, paths, ckpt):
     """With libm Box-Muller (NT_DEVICE_LIBM, glibc on the host) every fp64 bit matches."""
     flat = tapes[name]
-    sums, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1), paths, rocm=rocm)
+    sums, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1, mode=1), paths, rocm=rocm)
     ov, og = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
     assert np.array_equal(v, ov)
     assert np.array_equal(g, og)
@@ -45,20 +47,47 @@ def test_emulated_fp64_is_bit_exact(rocm, tapes, name, paths, ckpt):
     assert rel_err(sums, ref, floor=1e-300) <= 1e-13
 
 
+@pytest.mark.parametrize("name,paths", [("C1", 700), ("C2", 400), ("C3", 300), ("C4", 150), ("C5", 40)])
+def test_emulated_tangent_values_bit_exact_gradients_within_bar(rocm, tapes, name, paths):
+    """Tangent mode: same forward arithmetic (values bit for bit with libm
+    Box-Muller); derivatives within the per-path bar."""
+    flat = tapes[name]
+    sums, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=2), paths, rocm=rocm)
+    ov, _ = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov)
+    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
+    ref = oracle.replay_sums(flat, paths, OFFSET, 42, threads=1)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-12
+
+
 @pytest.mark.parametrize("seg", [2, 4, 10, 50])
 def test_segment_lengths_with_tail(rocm, tapes, seg):
     """Segment lengths that do not divide 252 leave a tail segment."""
     flat = tapes["C2"]
-    _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=1, seg_len=seg, libm=1), 200, rocm=rocm)
+    _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=1, seg_len=seg, libm=1, mode=1), 200, rocm=rocm)
     ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, threads=1)
     assert np.array_equal(v, ov) and np.array_equal(g, og)
 
 
+@pytest.mark.parametrize("seg", [1, 3, 4, 10])
+def test_tangent_trip_lengths_with_tail(rocm, tapes, seg):
+    """Tangent loop trips that do not divide the iteration count (C4 draws two
+    normals per step, so odd trips are allowed)."""
+    flat = tapes["C4"]
+    _, v, g = run_emulated(flat, rocm.options("fp64", seg_len=seg, libm=1, mode=2), 64, rocm=rocm)
+    ov, _ = oracle.replay_paths(flat, 64, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov)
+    check_per_path(v, g, flat, 64, OFFSET, 42, min_strict=0.5)
+
+
 def test_unrolled_straight_line_matches(rocm, tapes):
     flat = equity_tape_flat = tapes["C2"]
-    _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1, libm=1), 64, rocm=rocm)
+    _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1, libm=1, mode=1), 64, rocm=rocm)
     ov, og = oracle.replay_paths(flat, 64, OFFSET, 42, threads=1)
     assert np.array_equal(v, ov) and np.array_equal(g, og)
+    _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1, libm=1, mode=2), 64, rocm=rocm)
+    assert np.array_equal(v, ov)
+    check_per_path(v, g, flat, 64, OFFSET, 42)
 
 
 def test_price_only_and_moved_inputs(rocm, tapes):
@@ -70,18 +99,20 @@ def test_price_only_and_moved_inputs(rocm, tapes):
     assert np.all(sums[2:] == 0.0)
 
 
+@pytest.mark.parametrize("mode", [1, 2])
 @pytest.mark.parametrize("name,paths", [("C1", 700), ("C2", 300), ("C3", 200), ("C4", 100), ("C5", 30)])
-def test_emulated_own_math_within_1e12(rocm, tapes, name, paths):
+def test_emulated_own_math_within_1e12(rocm, tapes, name, paths, mode):
     """The skeleton's own log/sqrt/sincos keep paths within the per-path bar."""
     flat = tapes[name]
-    _, v, g = run_emulated(flat, rocm.options("fp64"), paths, rocm=rocm)
+    _, v, g = run_emulated(flat, rocm.options("fp64", mode=mode), paths, rocm=rocm)
     check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
 
 
+@pytest.mark.parametrize("mode", [1, 2])
 @pytest.mark.parametrize("name", ["C2", "C3"])
-def test_emulated_fp32_tracks_fp32_oracle(rocm, tapes, name):
+def test_emulated_fp32_tracks_fp32_oracle(rocm, tapes, name, mode):
     flat = tapes[name]
-    sums, v, g = run_emulated(flat, rocm.options("fp32"), 300, rocm=rocm)
+    sums, v, g = run_emulated(flat, rocm.options("fp32", mode=mode), 300, rocm=rocm)
     ov, og = oracle.replay_paths(flat, 300, OFFSET, 42, f32=True, threads=1)
     assert rel_err(v, ov) < 2e-4
     assert rel_err(g, og) < 2e-3
@@ -93,10 +124,13 @@ def test_lookback_and_digital_tapes(nt, rocm):
                     nt.ExoticProducts.digitalCash(nt.OptionTypeEnum.CALL, 1.0, 0.5),
                     nt.ExoticProducts.barrier(nt.OptionTypeEnum.PUT, nt.ExoticProducts.BarrierEnum.UP_OUT, 120.0, 2.0)):
         flat = equity_tape(nt, product, m, 24).flat()
+        ov, og = oracle.replay_paths(flat, 96, OFFSET, 42, threads=1)
         for ckpt in (1, 2, 3):
-            _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1), 96, rocm=rocm)
-            ov, og = oracle.replay_paths(flat, 96, OFFSET, 42, threads=1)
+            _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1, mode=1), 96, rocm=rocm)
             assert np.array_equal(v, ov) and np.array_equal(g, og), (product.label, ckpt)
+        _, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=2), 96, rocm=rocm)
+        assert np.array_equal(v, ov), product.label
+        check_per_path(v, g, flat, 96, OFFSET, 42, min_strict=0.5)
 
 
 def test_loop_plan_of_the_workloads(rocm, tapes):
@@ -112,6 +146,48 @@ def test_loop_plan_of_the_workloads(rocm, tapes):
 
 
 def test_draw_pairs_share_one_philox_block(rocm, tapes):
-    src = rocm.lower(tapes["C2"], rocm.options("fp64", checkpoint=1, seg_len=14))
-    fwd = src.split("for (nt_u32 sg = 0;")[1].split("const double y")[0]
-    assert fwd.count("nt_normal_pair(") == 7  # 14 draws per segment, two legs per block
+    for mode in (1, 2):
+        src = rocm.lower(tapes["C2"], rocm.options("fp64", checkpoint=1, seg_len=14, mode=mode))
+        fwd = src.split("for (nt_u32 sg = 0;")[1].split("const double y")[0]
+        assert fwd.count("nt_normal_pair(") == 7  # 14 draws per segment, two legs per block
+
+
+def _mode(rocm, flat, **kw):
+    head = [ln for ln in rocm.lower(flat, rocm.options(**kw)).splitlines() if ln.startswith("// nt-plan:")][0]
+    return dict(kv.split("=") for kv in head.split()[2:])["mode"]
+
+
+def _product_chain(n):
+    """y = x0 * x1 * ... * x(n-1): every node depends on all inputs before it."""
+    op, a, b = [1] * n, list(range(n)), [-1] * n
+    prev = 0
+    for i in range(1, n):
+        op.append(6)  # MUL
+        a.append(prev)
+        b.append(i)
+        prev = len(op) - 1
+    return {"op": np.array(op), "arg_a": np.array(a), "arg_b": np.array(b), "constant": np.zeros(len(op)),
+            "input_node": np.arange(n), "output_node": np.array([prev]), "n_streams": 1, "n_uniforms": 0,
+            "recorded_inputs": [1.0 + 0.01 * i for i in range(n)]}
+
+
+def test_cost_model_picks_the_cheaper_mode(rocm, tapes):
+    # A Monte-Carlo step loop whose state depends on few inputs: tangents are
+    # cheaper than recomputing the step for the reverse sweep.
+    assert _mode(rocm, tapes["C2"]) == "tangent"
+    assert _mode(rocm, tapes["C2"], mode=1) == "reverse"
+    # A product of 40 inputs: node k carries k tangents, the reverse sweep two
+    # adjoint updates per node.
+    chain = _product_chain(40)
+    assert _mode(rocm, chain) == "reverse"
+    assert _mode(rocm, chain, mode=2) == "tangent"
+    assert _mode(rocm, tapes["C2"], adjoints=False) == "reverse"  # price only: no derivative code at all
+
+
+def test_product_chain_both_modes_match_oracle(rocm):
+    flat = _product_chain(12)
+    ov, og = oracle.replay_paths(flat, 8, 0, 1, threads=1)
+    for mode in (1, 2):
+        _, v, g = run_emulated(flat, rocm.options("fp64", mode=mode), 8, offset=0, seed=1, rocm=rocm)
+        assert np.array_equal(v, ov)
+        assert rel_err(g, og) <= 1e-15
