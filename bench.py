@@ -58,11 +58,17 @@ def measured_traffic(precision: str, info: dict) -> dict | None:
     return None
 
 
-def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0):
+def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5):
     from nablatensor_amd import flops
 
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode)) as x:
         info = x.info()
+        # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
+        # (untimed) before the warmup steps, so a short --warmup does not time
+        # a cold device.
+        t_ramp = time.perf_counter()
+        while time.perf_counter() - t_ramp < ramp:
+            x.replay(paths, 0, seed)
         for w in range(warmup):
             x.replay(paths, w * paths, seed)
         replay_ms, kernel_ms = [], []
@@ -132,7 +138,7 @@ def other_workload(rocm, args) -> int:
     flat = workload_tape(args.workload)
     print(f"[bench] {args.workload} {desc}: {len(flat['op'])} nodes, {paths:,} scenarios/step, {prec}",
           file=sys.stderr, flush=True)
-    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode)
+    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -150,8 +156,10 @@ def other_workload(rocm, args) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ramp", type=float, default=0.5,
+                    help="seconds of untimed replays before the warmup steps, so the GPU clocks are up")
     ap.add_argument("--paths", type=int, default=2_000_000)
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--policy", type=int, default=0, help="checkpoint policy (0 auto, 1 recompute, 2 store draws, 3 store all)")
@@ -187,16 +195,17 @@ def main() -> int:
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()
     print(f"[bench] {WORKLOAD}: {len(flat['op'])} nodes, {args.paths:,} scenarios/step", file=sys.stderr, flush=True)
     f64 = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg,
-                  args.mode)
+                  args.mode, args.ramp)
     print(f"[bench] fp64 {f64['kernel']['mode']} {f64['value']:.3e} scen/s", file=sys.stderr, flush=True)
     rev = None
     if not args.no_reverse and f64["kernel"]["mode"] != "reverse":
-        rev = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg, 1)
+        rev = measure(rocm, flat, "fp64", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg, 1,
+                      args.ramp)
         print(f"[bench] fp64 reverse {rev['value']:.3e} scen/s", file=sys.stderr, flush=True)
     f32 = None
     if not args.no_fp32:
         f32 = measure(rocm, flat, "fp32", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg,
-                      args.mode)
+                      args.mode, args.ramp)
         print(f"[bench] fp32 {f32['kernel']['mode']} {f32['value']:.3e} scen/s", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(flat, args.cpu_sample, args.seed)
     out = {

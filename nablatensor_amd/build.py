@@ -102,8 +102,13 @@ def check_offline_hipcc(source: str, name: str = "check") -> Path:
     src = work / f"{name}.hip"
     src.write_text(source)
     out = work / f"{name}.hsaco"
+    feats = []
+    for line in source.splitlines():
+        if line.startswith("// nt-compile:"):
+            for f in line.split()[2:]:
+                feats += ["-Xclang", "-target-feature", "-Xclang", f]
     cmd = [str(ROCM / "bin" / "hipcc"), "--offload-arch=gfx950", "--cuda-device-only", "-O3", "-std=c++17",
-           *PACKED_FP32_OFF, f"-I{CSRC}", "-c", str(src), "-o", str(out)]
+           *PACKED_FP32_OFF, *feats, f"-I{CSRC}", "-c", str(src), "-o", str(out)]
     _run(cmd)
     return out
 

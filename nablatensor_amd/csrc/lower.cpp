@@ -544,16 +544,20 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.n_stored = 0;
   p.ck_slots = p.tape_slots = 0;
   if (!L.found) return;
-  // Iterations per loop trip: two when the registers the carried state and
-  // its tangents hold leave room (and always an even count when a step draws
-  // an odd number of normals, so both Box-Muller legs stay in one trip).
+  // Iterations per loop trip: up to four when the registers the carried
+  // state and its tangents hold leave room (and always an even count when a
+  // step draws an odd number of normals, so both Box-Muller legs stay in one
+  // trip). Longer trips let the scheduler overlap one step's Philox and
+  // transcendental latency with its neighbour's arithmetic and cut the
+  // register moves at the loop edge; measured on the Asian tape, 4 beats 2 by
+  // 16% with fewer VGPRs.
   const int W = p.n_words;
   int live = 0;
   for (int j = 0; j < L.period; ++j) {
     if (L.is_carry[j] || L.is_liveout[j]) live += 1 + popcount(&p.posdeps[static_cast<size_t>(j) * W], W);
   }
   const int w = p.precision == NT_FP64 ? 2 : 1;
-  int seg = o.seg_len > 0 ? o.seg_len : (live * w <= 64 ? 2 : 1);
+  int seg = o.seg_len > 0 ? o.seg_len : (live * w <= 32 ? 4 : live * w <= 64 ? 2 : 1);
   if ((L.draws & 1) && (seg & 1)) seg += 1;
   seg = std::max(1, std::min(seg, L.iters));
   p.seg = seg;
@@ -597,6 +601,15 @@ class Emitter {
   }
   std::string f(const char* name) const { return f32_ ? std::string(name) + "f" : std::string(name); }
 
+  // fp64 Box-Muller and exp read LDS tables that each block loads first.
+  bool needs_tables() const {
+    if (f32_) return false;
+    for (int i = 0; i < t_.n; ++i) {
+      if (t_.op[i] == NT_OP_RANDN || t_.op[i] == NT_OP_EXP) return true;
+    }
+    return false;
+  }
+
   std::string expr(int op, const std::string& x, const std::string& y, double c, int a) const {
     switch (op) {
       case NT_OP_CONST: return lit(c);
@@ -606,7 +619,10 @@ class Emitter {
       case NT_OP_MUL: return x + " * " + y;
       case NT_OP_DIV: return x + " / " + y;
       case NT_OP_NEG: return "-" + x;
-      case NT_OP_EXP: return f("exp") + "(" + x + ")";
+      case NT_OP_EXP:
+        if (f32_) return "nt_expf(" + x + ")";
+        if (p_.libm == 1 || slow_) return "exp(" + x + ")";
+        return "nt_exp_fast(" + x + ", nt_slow)";
       case NT_OP_LOG: return f("log") + "(" + x + ")";
       case NT_OP_SQRT: return f("sqrt") + "(" + x + ")";
       case NT_OP_ABS: return f("fabs") + "(" + x + ")";
@@ -703,7 +719,19 @@ class Emitter {
   void tline(int lo, int hi);
   void tsegment(int U, const std::string& sg);
   void body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const;
-  std::string run_tangent();
+
+  // ---- kernel frame ----
+  bool slow_ = false;  // emitting the device-libm re-evaluation of a flagged path
+  bool exp_fallback() const {
+    if (f32_ || p_.libm == 1) return false;
+    for (int i = 0; i < t_.n; ++i) {
+      if (t_.op[i] == NT_OP_EXP) return true;
+    }
+    return false;
+  }
+  void header();
+  void body_tangent();
+  void body_reverse();
 };
 
 std::string Emitter::vname(int node) const {
@@ -1057,22 +1085,30 @@ void Emitter::tsegment(int U, const std::string& sg) {
   o_ << "    }\n";
 }
 
-std::string Emitter::run_tangent() {
+void Emitter::header() {
   const int n = t_.n;
   const int nin = t_.n_in;
-  const int NCH = p_.n_channels;
   const bool loop = L_.found;
-  const int ls = loop ? L_.start : n;
-  const int le = loop ? L_.end() : n;
-  const std::string zero = f32_ ? "0.0f" : "0.0";
-  const std::string one = f32_ ? "1.0f" : "1.0";
+  const bool tangent = p_.mode == NT_MODE_TANGENT;
   o_ << "// generated by nablatensor_amd lowering: " << n << " nodes, " << nin << " inputs, "
-     << (loop ? "rolled loop" : "straight line") << ", tangent mode\n";
-  if (loop) {
+     << (loop ? "rolled loop" : "straight line") << (tangent ? ", tangent mode" : "") << "\n";
+  if (loop && tangent) {
     o_ << "// loop: start " << L_.start << ", period " << L_.period << ", iterations " << L_.iters << ", draws/iter "
        << L_.draws << ", " << p_.seg << " iterations per trip (" << p_.nseg_full << " trips + tail " << p_.tail << ")\n";
+  } else if (loop) {
+    o_ << "// loop: start " << L_.start << ", period " << L_.period << ", iterations " << L_.iters << ", draws/iter "
+       << L_.draws << ", segment " << p_.seg << " (" << p_.nseg_full << " full + tail " << p_.tail
+       << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
   }
-  o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent\n";
+  if (tangent) {
+    o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent\n";
+    // Polynomial constants held in VGPRs make v_fmac_f64 (accumulator tied to
+    // the destination) cost a 64-bit copy per term; the three-source v_fma_f64
+    // needs none.
+    if (!f32_) o_ << "// nt-compile: -fmacf64-inst\n";
+  } else {
+    o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << " mode=reverse\n";
+  }
   o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
   if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
   if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";
@@ -1085,16 +1121,25 @@ std::string Emitter::run_tangent() {
   o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
   o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
   o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
-  bool draws = false;
-  for (int i = 0; i < n; ++i) draws |= t_.op[i] == NT_OP_RANDN;
-  if (draws && !f32_) o_ << "  nt_tables_load();\n";
+  if (needs_tables()) o_ << "  nt_tables_load();\n";
   for (int j = 0; j < nin; ++j) o_ << "  const real in" << j << " = (real)inputs[" << j << "];\n";
-  o_ << "  double acc[" << NCH << "];\n";
-  o_ << "  for (int c = 0; c < " << NCH << "; ++c) acc[c] = 0.0;\n";
+  o_ << "  double acc[" << p_.n_channels << "];\n";
+  o_ << "  for (int c = 0; c < " << p_.n_channels << "; ++c) acc[c] = 0.0;\n";
   o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
   o_ << "    const nt_u64 path = p + path_offset;\n";
   o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
   o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
+}
+
+// Values and tangents of one path; leaves the output in nt_y and its
+// derivatives in nt_g.
+void Emitter::body_tangent() {
+  const int n = t_.n;
+  const bool loop = L_.found;
+  const int ls = loop ? L_.start : n;
+  const int le = loop ? L_.end() : n;
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  const std::string one = f32_ ? "1.0f" : "1.0";
   tline(0, ls);
   if (loop) {
     for (int j = 0; j < L_.period; ++j) {
@@ -1114,63 +1159,22 @@ std::string Emitter::run_tangent() {
     if (p_.tail) tsegment(p_.tail, std::to_string(p_.nseg_full) + "u");
     tline(le, n);
   }
-  o_ << "    const double y = (double)" << vname(t_.output) << ";\n";
-  o_ << "    acc[0] += y;\n    acc[1] += y * y;\n";
-  auto grad = [&](int j) {
+  o_ << "    nt_y = (double)" << vname(t_.output) << ";\n";
+  if (!p_.adjoints) return;
+  for (int j = 0; j < t_.n_in; ++j) {
     const std::string g = tname(t_.output, j);
-    return g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g;
-  };
-  for (int j = 0; j < nin; ++j) o_ << "    acc[" << 2 + j << "] += " << grad(j) << ";\n";
-  o_ << "#ifdef NT_DUMP_PATHS\n";
-  o_ << "    out_v[p] = y;\n";
-  for (int j = 0; j < nin; ++j) o_ << "    out_g[p * " << nin << "u + " << j << "u] = " << grad(j) << ";\n";
-  o_ << "#endif\n";
-  o_ << "  }\n";
-  o_ << "  __shared__ double nt_lds[" << NCH << " * (" << p_.block << " / 64)];\n";
-  o_ << "  nt_block_store<" << NCH << ">(acc, partials, nt_lds);\n";
-  o_ << "}\n";
-  return o_.str();
+    o_ << "    nt_g[" << j << "] = " << (g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g)
+       << ";\n";
+  }
 }
 
-std::string Emitter::run() {
-  if (p_.mode == NT_MODE_TANGENT) return run_tangent();
+// Forward pass, then the reverse sweep; leaves the output in nt_y and the
+// adjoints of the inputs in nt_g.
+void Emitter::body_reverse() {
   const int n = t_.n;
-  const int nin = t_.n_in;
-  const int NCH = p_.n_channels;
   const bool loop = L_.found;
   const int ls = loop ? L_.start : n;
   const int le = loop ? L_.end() : n;
-  o_ << "// generated by nablatensor_amd lowering: " << n << " nodes, " << nin << " inputs, "
-     << (loop ? "rolled loop" : "straight line") << "\n";
-  if (loop) {
-    o_ << "// loop: start " << L_.start << ", period " << L_.period << ", iterations " << L_.iters << ", draws/iter "
-       << L_.draws << ", segment " << p_.seg << " (" << p_.nseg_full << " full + tail " << p_.tail
-       << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
-  }
-  o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << " mode=reverse\n";
-  o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
-  if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
-  if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";
-  o_ << "#include \"nt_skeleton.h\"\n";
-  o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
-  o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block << ") void nt_replay(\n"
-     << "    const double* __restrict__ inputs, nt_u64 n_paths, nt_u64 path_offset, nt_u64 seed,\n"
-     << "    double* __restrict__ partials, real* __restrict__ scratch,\n"
-     << "    double* __restrict__ out_v, double* __restrict__ out_g) {\n";
-  o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
-  o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
-  o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
-  bool draws = false;
-  for (int i = 0; i < n; ++i) draws |= t_.op[i] == NT_OP_RANDN;
-  if (draws && !f32_) o_ << "  nt_tables_load();\n";
-  for (int j = 0; j < nin; ++j) o_ << "  const real in" << j << " = (real)inputs[" << j << "];\n";
-  o_ << "  double acc[" << NCH << "];\n";
-  o_ << "  for (int c = 0; c < " << NCH << "; ++c) acc[c] = 0.0;\n";
-  o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
-  o_ << "    const nt_u64 path = p + path_offset;\n";
-  o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
-  o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
-  // forward
   line_forward(0, ls);
   if (loop) {
     for (int j = 0; j < L_.period; ++j) {
@@ -1185,50 +1189,76 @@ std::string Emitter::run() {
     if (p_.tail) segment(p_.tail, std::to_string(p_.nseg_full) + "u", true);
     line_forward(le, n);
   }
-  const std::string y = vname(t_.output);
-  o_ << "    const double y = (double)" << y << ";\n";
-  o_ << "    acc[0] += y;\n    acc[1] += y * y;\n";
-  if (p_.adjoints) {
-    const std::string zero = f32_ ? "0.0f" : "0.0";
-    const std::string one = f32_ ? "1.0f" : "1.0";
-    for (int i = 0; i < ls; ++i) {
+  o_ << "    nt_y = (double)" << vname(t_.output) << ";\n";
+  if (!p_.adjoints) return;
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  const std::string one = f32_ ? "1.0f" : "1.0";
+  for (int i = 0; i < ls; ++i) {
+    if (t_.active[i]) o_ << "    real d" << i << " = " << zero << ";\n";
+  }
+  if (loop) {
+    for (int j = 0; j < L_.period; ++j) {
+      if ((L_.is_carry[j] || L_.is_liveout[j]) && t_.active[L_.start + j]) o_ << "    real gs" << j << " = " << zero << ";\n";
+    }
+    for (int i = le; i < n; ++i) {
       if (t_.active[i]) o_ << "    real d" << i << " = " << zero << ";\n";
     }
+  }
+  if (t_.active[t_.output]) {
+    o_ << "    " << dname(t_.output) << " = " << one << ";\n";
+    if (loop) line_reverse(le, n);
     if (loop) {
-      for (int j = 0; j < L_.period; ++j) {
-        if ((L_.is_carry[j] || L_.is_liveout[j]) && t_.active[L_.start + j]) o_ << "    real gs" << j << " = " << zero << ";\n";
+      if (p_.tail) segment(p_.tail, std::to_string(p_.nseg_full) + "u", false);
+      if (p_.nseg_full > 0) {
+        o_ << "    for (int sgi = " << (p_.nseg_full - 1) << "; sgi >= 0; --sgi)\n";
+        segment(p_.seg, "(nt_u32)sgi", false);
       }
-      for (int i = le; i < n; ++i) {
-        if (t_.active[i]) o_ << "    real d" << i << " = " << zero << ";\n";
+      for (int c : p_.carries) {
+        const int init = L_.carry_init[c];
+        if (t_.active[L_.start + c] && init >= 0 && t_.active[init]) o_ << "    d" << init << " += gs" << c << ";\n";
       }
     }
-    if (t_.active[t_.output]) {
-      o_ << "    " << dname(t_.output) << " = " << one << ";\n";
-      if (loop) line_reverse(le, n);
-      if (loop) {
-        if (p_.tail) segment(p_.tail, std::to_string(p_.nseg_full) + "u", false);
-        if (p_.nseg_full > 0) {
-          o_ << "    for (int sgi = " << (p_.nseg_full - 1) << "; sgi >= 0; --sgi)\n";
-          segment(p_.seg, "(nt_u32)sgi", false);
-        }
-        for (int c : p_.carries) {
-          const int init = L_.carry_init[c];
-          if (t_.active[L_.start + c] && init >= 0 && t_.active[init]) o_ << "    d" << init << " += gs" << c << ";\n";
-        }
-      }
-      line_reverse(0, ls);
-    }
-    for (int j = 0; j < nin; ++j) {
-      const int node = t_.input_node[j];
-      o_ << "    acc[" << 2 + j << "] += (double)" << (t_.active[t_.output] ? dname(node) : "0.0") << ";\n";
-    }
+    line_reverse(0, ls);
+  }
+  for (int j = 0; j < t_.n_in; ++j) {
+    const int node = t_.input_node[j];
+    o_ << "    nt_g[" << j << "] = " << (t_.active[t_.output] ? "(double)" + dname(node) : std::string("0.0")) << ";\n";
+  }
+}
+
+std::string Emitter::run() {
+  const int nin = t_.n_in;
+  const int NCH = p_.n_channels;
+  const bool tangent = p_.mode == NT_MODE_TANGENT;
+  header();
+  // fp64 exp's fast path covers |x| <= 708; a path with an exponent outside
+  // flags itself and is evaluated again with device libm exp. The fast pass
+  // is the only one a Monte-Carlo path normally takes, and it stays one
+  // basic block per loop trip.
+  const bool fallback = exp_fallback();
+  o_ << "    double nt_y;\n";
+  if (p_.adjoints && nin > 0) o_ << "    double nt_g[" << nin << "];\n";
+  if (fallback) o_ << "    bool nt_slow = false;\n";
+  slow_ = false;
+  o_ << "    {\n";
+  if (tangent) body_tangent(); else body_reverse();
+  o_ << "    }\n";
+  if (fallback) {
+    o_ << "    if (nt_slow) {\n";
+    slow_ = true;
+    if (tangent) body_tangent(); else body_reverse();
+    slow_ = false;
+    o_ << "    }\n";
+  }
+  o_ << "    acc[0] += nt_y;\n    acc[1] += nt_y * nt_y;\n";
+  if (p_.adjoints) {
+    for (int j = 0; j < nin; ++j) o_ << "    acc[" << 2 + j << "] += nt_g[" << j << "];\n";
   }
   o_ << "#ifdef NT_DUMP_PATHS\n";
-  o_ << "    out_v[p] = y;\n";
+  o_ << "    out_v[p] = nt_y;\n";
   for (int j = 0; j < nin; ++j) {
-    const int node = t_.input_node[j];
-    o_ << "    out_g[p * " << nin << "u + " << j << "u] = "
-       << (p_.adjoints && t_.active[t_.output] ? "(double)" + dname(node) : "0.0") << ";\n";
+    o_ << "    out_g[p * " << nin << "u + " << j << "u] = " << (p_.adjoints ? "nt_g[" + std::to_string(j) + "]" : "0.0")
+       << ";\n";
   }
   o_ << "#endif\n";
   o_ << "  }\n";

@@ -88,16 +88,34 @@ void write_file_atomic(const std::string& path, const std::vector<char>& data) {
   std::rename(tmp.c_str(), path.c_str());
 }
 
-std::vector<std::string> compile_options(bool dump) {
+// Target features the generated source asks to turn off, from its
+// "// nt-compile: -feature ..." line.
+std::vector<std::string> source_features(const std::string& src) {
+  std::vector<std::string> out;
+  const std::string tag = "// nt-compile:";
+  const size_t at = src.find(tag);
+  if (at == std::string::npos) return out;
+  std::istringstream line(src.substr(at + tag.size(), src.find('\n', at) - at - tag.size()));
+  std::string f;
+  while (line >> f) {
+    if (f.size() > 1 && f[0] == '-') out.push_back(f);
+  }
+  return out;
+}
+
+std::vector<std::string> compile_options(const std::string& src, bool dump) {
   std::vector<std::string> o = {std::string("--offload-arch=") + kArch, "-O3", "-std=c++17",
                                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  for (const auto& f : source_features(src)) {
+    o.insert(o.end(), {"-Xclang", "-target-feature", "-Xclang", f});
+  }
   if (dump) o.push_back("-DNT_DUMP_PATHS=1");
   return o;
 }
 
 int compile_hiprtc(const std::string& src, bool dump, std::vector<char>& code, double& seconds) {
   const auto t0 = std::chrono::steady_clock::now();
-  const std::vector<std::string> opts = compile_options(dump);
+  const std::vector<std::string> opts = compile_options(src, dump);
   int major = 0, minor = 0;
   hiprtcVersion(&major, &minor);
   std::string key = src + "\n#opts";

@@ -23,14 +23,19 @@ typedef unsigned long long nt_u64;
 
 #define NT_UINT_SCALE 2.3283064365386963e-10
 
+#if !defined(NT_HOST_EMU)
+// a ^ b ^ c in one v_bitop3_b32 (truth table 0x96)
+__device__ __forceinline__ nt_u32 nt_xor3(nt_u32 a, nt_u32 b, nt_u32 c) { return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96); }
+#endif
+
 // Ten Philox2x32 rounds. The key schedule is a compile-time constant, so a
-// round is one 32x32->64 multiply and one three-input xor.
+// round is one 32x32->64 multiply (v_mad_u64_u32) and one three-input xor.
 __device__ __forceinline__ void nt_philox(nt_u32 c0, nt_u32 c1, nt_u32& o0, nt_u32& o1) {
 #pragma unroll
   for (int i = 0; i < 10; ++i) {
     const nt_u32 key = 0x1BD11BDAu + 0x9E3779B9u * static_cast<nt_u32>(i);
     const nt_u64 p = static_cast<nt_u64>(0xD256D193u) * c0;
-    c0 = static_cast<nt_u32>(p >> 32) ^ key ^ c1;
+    c0 = nt_xor3(static_cast<nt_u32>(p >> 32), key, c1);
     c1 = static_cast<nt_u32>(p);
   }
   o0 = c0;
@@ -46,44 +51,95 @@ __device__ __forceinline__ double nt_mk(nt_u32 hi, nt_u32 lo) {
   return __hiloint2double(static_cast<int>(hi), static_cast<int>(lo));
 }
 __device__ __forceinline__ double nt_rsq(double x) { return __builtin_amdgcn_rsq(x); }
+// fp32 hardware transcendentals (quarter-rate VALU): exp2, log2, sqrt, and
+// sin/cos of 2 pi x (the instructions take their argument in revolutions).
+__device__ __forceinline__ float nt_hw_exp2f(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float nt_hw_log2f(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float nt_hw_sqrtf(float x) { return __builtin_amdgcn_sqrtf(x); }
+__device__ __forceinline__ float nt_hw_sin2pif(float x) { return __builtin_amdgcn_sinf(x); }
+__device__ __forceinline__ float nt_hw_cos2pif(float x) { return __builtin_amdgcn_cosf(x); }
 #endif
 
+// fp32 exp as 2^(x log2 e) on the hardware exp2: the rounding of the product
+// adds |x| * 2^-24 relative error, well inside fp32 replay's 1e-5 reconcile
+// bar for Monte-Carlo exponents (|x| of order 1).
+__device__ __forceinline__ float nt_expf(float x) { return nt_hw_exp2f(x * 1.44269504088896341f); }
+
 #ifndef NT_DEVICE_LIBM
-// The log table lives in LDS; every block copies it once at kernel start.
-__constant__ NtLogTable nt_log_table_c = NT_LOG_TABLE_INIT;
-__shared__ NtLogTable nt_log_table;
+// The sin/cos, exp and log tables live in LDS; every block copies them once
+// at kernel start.
+__constant__ NtTables nt_tables_c = NT_TABLES_INIT;
+__shared__ NtTables nt_tables;
 
 __device__ __forceinline__ void nt_tables_load() {
-  const double* src = &nt_log_table_c.inv[0];
-  double* dst = &nt_log_table.inv[0];
-  for (unsigned i = threadIdx.x; i < 3u * 129u; i += blockDim.x) dst[i] = src[i];
+  const double* src = reinterpret_cast<const double*>(&nt_tables_c);
+  double* dst = reinterpret_cast<double*>(&nt_tables);
+  constexpr unsigned n = sizeof(NtTables) / sizeof(double);
+  for (unsigned i = threadIdx.x; i < n; i += blockDim.x) dst[i] = src[i];
   __syncthreads();
 }
 
+// exp(x) by Tang's table-driven method: x = (64 m + j) ln2/64 + r with
+// |r| <= ln2/128 (ln2/64 split in a 32-bit head and a tail, so the reduction
+// keeps r to one rounding), exp(x) = 2^m (T_j + T_j p(r)) with T_j =
+// 2^(j/64) as head + tail and p(r) = exp(r) - 1 through r^6. Below 1 ulp.
+// k = 64 m + j comes out of the low word of x 64/ln2 + 1.5 * 2^52 (rounded
+// to an integer by that addition), so no float-to-int conversion is needed.
+// The result is exact only for |x| <= 708 (results in the normal range);
+// outside it (and for infinities and NaN) it is garbage but harmless (the
+// table index stays in range) and `bad` is set, so the caller can evaluate
+// the path again with device libm.
+__device__ __forceinline__ double nt_exp_fast(double x, bool& bad) {
+  const double t = fma(x, NT_EXP_INV_L, 0x1.8p52);
+  const double kd = t - 0x1.8p52;
+  const int k = static_cast<int>(nt_lo(t));
+  double r = fma(-kd, NT_EXP_L_HI, x);
+  r = fma(-kd, NT_EXP_L_LO, r);
+  const int j = k & 63;
+  const int m = k >> 6;
+  double q = fma(r, NT_EXP_C6, NT_EXP_C5);
+  q = fma(r, q, NT_EXP_C4);
+  q = fma(r, q, NT_EXP_C3);
+  q = fma(r, q, NT_EXP_C2);
+  const double p = fma(r * r, q, r);
+  const double th = nt_tables.ex.t[2 * j];
+  const double tl = nt_tables.ex.t[2 * j + 1];
+  bad |= !(fabs(x) <= 708.0);
+  return ldexp(th + fma(th, p, tl), m);
+}
+
+// exp for any argument: the fast path, device libm where it does not apply.
+__device__ __forceinline__ double nt_exp(double x) {
+  bool bad = false;
+  const double y = nt_exp_fast(x, bad);
+  return bad ? exp(x) : y;
+}
+
 // -2 ln(u) for u = (c + 0.5) * 2^-32, by Tang's table-driven method: u = 2^e x
-// with x in [sqrt(1/2), sqrt(2)), F = x rounded to 7 fractional bits,
-// ln u = e ln2 + ln F + ln(1 + r), r = (x - F) / F, |r| <= 2^-8. x - F is
-// exact and F = 1 near u = 1, so ln u keeps full relative accuracy there.
+// with x in [sqrt(1/2), sqrt(2)), F = x rounded to 7 fractional bits of its
+// binade (rounding the high word at bit 13 moves F = 2 - 2^-7 up to the next
+// binade exactly), ln u = e ln2 + ln F + ln(1 + r), r = (x - F) / F,
+// |r| <= 2^-8. x - F is exact and F = 1 near u = 1, so ln u keeps full
+// relative accuracy there. Tables and constants carry the factor -2 (exact).
 __device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
   const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
   nt_u32 hx = nt_hi(u) + (0x3FF00000u - 0x3FE6A09Eu);
   const int e = static_cast<int>(hx >> 20) - 0x3FF;
   hx = (hx & 0x000FFFFFu) + 0x3FE6A09Eu;
   const double x = nt_mk(hx, nt_lo(u));
-  const nt_u32 j = (((hx >> 12) & 0xFFu) + 1u) >> 1;
-  const nt_u32 fhi = (hx & 0xFFF00000u) + (j << 13);
+  const nt_u32 fhi = (hx + 0x1000u) & 0xFFFFE000u;
   const nt_u32 idx = (fhi - 0x3FE6A000u) >> 13;
-  const double r = (x - nt_mk(fhi, 0u)) * nt_log_table.inv[idx];
-  double q = fma(r, 1.0 / 7.0, -1.0 / 6.0);
-  q = fma(r, q, 0.2);
-  q = fma(r, q, -0.25);
-  q = fma(r, q, 1.0 / 3.0);
-  q = fma(r, q, -0.5);
-  const double p = fma(r * r, q, r);
+  const double r = (x - nt_mk(fhi, 0u)) * nt_tables.lg.inv[idx];  // r' = -2 (x - F) / F
+  double q = fma(r, NT_LOGQ_5, NT_LOGQ_4);
+  q = fma(r, q, NT_LOGQ_3);
+  q = fma(r, q, NT_LOGQ_2);
+  q = fma(r, q, NT_LOGQ_1);
+  q = fma(r, q, NT_LOGQ_0);
+  const double p = fma(r * r, q, r);  // -2 ln(1 + (x - F) / F)
   const double ed = static_cast<double>(e);
-  const double hi = fma(ed, NT_LN2_HI, nt_log_table.hi[idx]);  // exact by the table's layout
-  const double lo = fma(ed, NT_LN2_LO, nt_log_table.lo[idx]) + p;
-  return -2.0 * (hi + lo);
+  const double hi = fma(ed, NT_M2LN2_HI, nt_tables.lg.hi[idx]);  // exact by the table's layout
+  const double lo = fma(ed, NT_M2LN2_LO, nt_tables.lg.lo[idx]) + p;
+  return hi + lo;
 }
 
 // sqrt(a) for a positive normal finite a: reciprocal square root seed and one
@@ -99,46 +155,39 @@ __device__ __forceinline__ double nt_sqrt_pos(double a) {
   return fma(d, h, g);
 }
 
-// sin and cos of theta = fl(6.283185307179586 * u) for u = (c + 0.5) * 2^-32:
-// the reference rounds its angle once, and so does this (theta is that rounded
-// product). The quarter turn q and the remainder f = u - q/4 in [-1/8, 1/8]
-// come exactly from the integer c and the polynomials are in f; the rounding
-// of theta, eps = theta - 2 pi u, is known exactly (one FMA) and applied as
-// sin(2 pi u + eps) = S + eps C, cos = C - eps S.
+// sin and cos of theta = fl(6.283185307179586 * u) for u = (c + 0.5) * 2^-32.
+// The reference rounds its angle once, and so does this (theta is that
+// rounded product). The circle is cut in 256 sectors: c = j 2^24 + d with d
+// the sign-extended low 24 bits, so u = j/256 + f exactly, f = (d + 0.5)
+// 2^-32, |f| <= 2^-9 turns. With (S, C) = (sin, cos)(2 pi j/256) from the
+// table, sin(2 pi u) = S cos(2 pi f) + C sin(2 pi f) and cos(2 pi u) =
+// C cos(2 pi f) - S sin(2 pi f), the small-angle parts being polynomials in
+// f. The rounding of theta, eps = theta - 2 pi u, is known exactly (two FMAs)
+// and enters as sin(2 pi f + eps) = sin(2 pi f) + eps to first order (the
+// second-order terms are below 1e-17).
 __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& co) {
-  const nt_u32 q = (c >> 30) + ((c >> 29) & 1u);
-  const int d = static_cast<int>(c - (q << 30));
+  const int d = static_cast<int>(c << 8) >> 8;
+  const nt_u32 j = (c - static_cast<nt_u32>(d)) >> 24;
   const double f = fma(static_cast<double>(d), 0x1p-32, 0x1p-33);
   const double t = f * f;
-  double ps = fma(t, NT_SIN2PI_7, NT_SIN2PI_6);
-  ps = fma(t, ps, NT_SIN2PI_5);
-  ps = fma(t, ps, NT_SIN2PI_4);
-  ps = fma(t, ps, NT_SIN2PI_3);
-  ps = fma(t, ps, NT_SIN2PI_2);
-  ps = fma(t, ps, NT_SIN2PI_1);
-  ps = fma(t, ps, NT_SIN2PI_0);
-  const double sn = f * ps;
-  double pc = fma(t, NT_COS2PI_8, NT_COS2PI_7);
-  pc = fma(t, pc, NT_COS2PI_6);
-  pc = fma(t, pc, NT_COS2PI_5);
-  pc = fma(t, pc, NT_COS2PI_4);
-  pc = fma(t, pc, NT_COS2PI_3);
-  pc = fma(t, pc, NT_COS2PI_2);
-  pc = fma(t, pc, NT_COS2PI_1);
-  const double cs = fma(t, pc, NT_COS2PI_0);
-  const nt_u32 qq = q & 3u;
-  const double sv = (qq & 1u) ? cs : sn;
-  const double cv = (qq & 1u) ? sn : cs;
-  const double s2 = (qq & 2u) ? -sv : sv;
-  const double c2 = ((qq + 1u) & 2u) ? -cv : cv;
+  double ps = fma(t, NT_SC_S7, NT_SC_S5);
+  ps = fma(t, ps, NT_SC_S3);
+  ps = fma(t, ps, NT_SC_S1);
+  double cq = fma(t, NT_SC_C6, NT_SC_C4);
+  cq = fma(t, cq, NT_SC_C2);
+  const double cm = t * cq;  // cos(2 pi f) - 1
   const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
   const double theta = NT_TWO_PI_D * u;
   const double eps = fma(NT_TWO_PI_D_ERR, u, -fma(NT_TWO_PI_D, u, -theta));
-  s = fma(eps, c2, s2);
-  co = fma(-eps, s2, c2);
+  const double sn = fma(f, ps, eps);  // sin(2 pi f) + eps
+  const double S = nt_tables.sc.t[2 * j];
+  const double C = nt_tables.sc.t[2 * j + 1];
+  s = S + fma(C, sn, S * cm);
+  co = C + fma(C, cm, -(S * sn));
 }
 #else
 __device__ __forceinline__ void nt_tables_load() {}
+__device__ __forceinline__ double nt_exp(double x) { return exp(x); }
 #endif
 
 // Both legs of the Box-Muller pair for Philox counter `ctr` of a path whose
@@ -169,17 +218,17 @@ __device__ __forceinline__ void nt_normal_pair(nt_u32 lo, nt_u32 hi, nt_u32 ctr,
   zs = r * s;
 }
 
-// fp32 pair: same counters, single-precision transcendentals.
+// fp32 pair: same counters and the reference's fp32 u; the transcendentals
+// are the hardware ones: ln u1 = ln2 * log2(u1), and sin/cos of 2 pi u2 read
+// u2 directly as revolutions (no multiplication by 2 pi rounds the angle).
 __device__ __forceinline__ void nt_normal_pair(nt_u32 lo, nt_u32 hi, nt_u32 ctr, float& zc, float& zs) {
   nt_u32 c0, c1;
   nt_philox(lo, hi ^ ctr, c0, c1);
   const float u1 = (static_cast<float>(c0) + 0.5f) * 2.3283064365386963e-10f;
   const float u2 = (static_cast<float>(c1) + 0.5f) * 2.3283064365386963e-10f;
-  const float r = sqrtf(-2.0f * logf(u1));
-  float s, c;
-  sincospif(2.0f * u2, &s, &c);
-  zc = r * c;
-  zs = r * s;
+  const float r = nt_hw_sqrtf(-1.38629436111989061f * nt_hw_log2f(u1));  // -2 ln 2 * log2(u1)
+  zc = r * nt_hw_cos2pif(u2);
+  zs = r * nt_hw_sin2pif(u2);
 }
 
 #ifndef NT_HOST_EMU  // the lowering's CPU tests provide their own reductions

@@ -14,7 +14,12 @@ void emu_neg2log(const nt_u32* c, double* out, long n) {
   for (long i = 0; i < n; ++i) out[i] = nt_neg2log_u32(c[i]);
 }
 void emu_sincos(const nt_u32* c, double* s, double* co, long n) {
+  load_tables();
   for (long i = 0; i < n; ++i) nt_sincos_2pi_u32(c[i], s[i], co[i]);
+}
+void emu_exp(const double* x, double* out, long n) {
+  load_tables();
+  for (long i = 0; i < n; ++i) out[i] = nt_exp(x[i]);
 }
 void emu_sqrt(const double* a, double* out, long n) {
   for (long i = 0; i < n; ++i) out[i] = nt_sqrt_pos(a[i]);

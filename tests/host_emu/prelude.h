@@ -25,6 +25,7 @@ inline double nt_mk(unsigned hi, unsigned lo) {
   std::memcpy(&x, &u, 8);
   return x;
 }
+inline unsigned nt_xor3(unsigned a, unsigned b, unsigned c) { return a ^ b ^ c; }
 // correctly rounded stand-in for the device's reciprocal-square-root seed
 inline double nt_rsq(double x) { return 1.0 / std::sqrt(x); }
 
@@ -32,6 +33,13 @@ struct nt_emu_dim3 {
   unsigned x = 0, y = 1, z = 1;
 };
 static nt_emu_dim3 gridDim, blockDim, blockIdx, threadIdx;
+
+// fp32 hardware transcendentals, evaluated in double and rounded once
+inline float nt_hw_exp2f(float x) { return static_cast<float>(::exp2(static_cast<double>(x))); }
+inline float nt_hw_log2f(float x) { return static_cast<float>(::log2(static_cast<double>(x))); }
+inline float nt_hw_sqrtf(float x) { return static_cast<float>(::sqrt(static_cast<double>(x))); }
+inline float nt_hw_sin2pif(float x) { return static_cast<float>(::sin(2.0 * M_PI * static_cast<double>(x))); }
+inline float nt_hw_cos2pif(float x) { return static_cast<float>(::cos(2.0 * M_PI * static_cast<double>(x))); }
 
 inline void sincospif(float x, float* s, float* c) {
   const double a = M_PI * static_cast<double>(x);

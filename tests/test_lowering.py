@@ -148,7 +148,7 @@ def test_loop_plan_of_the_workloads(rocm, tapes):
 def test_draw_pairs_share_one_philox_block(rocm, tapes):
     for mode in (1, 2):
         src = rocm.lower(tapes["C2"], rocm.options("fp64", checkpoint=1, seg_len=14, mode=mode))
-        fwd = src.split("for (nt_u32 sg = 0;")[1].split("const double y")[0]
+        fwd = src.split("for (nt_u32 sg = 0;")[1].split("nt_y = ")[0]
         assert fwd.count("nt_normal_pair(") == 7  # 14 draws per segment, two legs per block
 
 
@@ -191,3 +191,24 @@ def test_product_chain_both_modes_match_oracle(rocm):
         _, v, g = run_emulated(flat, rocm.options("fp64", mode=mode), 8, offset=0, seed=1, rocm=rocm)
         assert np.array_equal(v, ov)
         assert rel_err(g, og) <= 1e-15
+
+
+def test_exp_outside_fast_range_falls_back_per_path(rocm):
+    """y = exp(a z) with a = 300: paths with |z| > 2.36 put the exponent past
+    708; they are evaluated again with libm exp (overflow to inf included) and
+    agree with the oracle, the others take the table-driven exp."""
+    flat = {"op": np.array([1, 2, 6, 9]), "arg_a": np.array([0, 0, 0, 2]), "arg_b": np.array([-1, 0, 1, -1]),
+            "constant": np.zeros(4), "input_node": np.array([0]), "output_node": np.array([3]),
+            "n_streams": 1, "n_uniforms": 0, "recorded_inputs": [300.0]}
+    ov, og = oracle.replay_paths(flat, 3000, 0, 5, threads=1)
+    beyond = np.abs(np.log(np.abs(ov) + 1e-300)) > 708  # the exponent's own size, from the oracle
+    assert 10 < beyond.sum() < 300 and np.isinf(ov).any()
+    for mode in (1, 2):
+        # libm=2: own log/sqrt with libm sincos keeps the draws within an ulp or
+        # two of glibc's, so an exponent of 300 z does not amplify them past the bar
+        _, v, g = run_emulated(flat, rocm.options("fp64", mode=mode, libm=2), 3000, offset=0, seed=5, rocm=rocm)
+        ev, eg = oracle.path_errors(v, g, ov, og)
+        assert ev.max() <= 1e-12 and eg.max() <= 1e-12, mode
+        assert np.array_equal(np.isinf(v), np.isinf(ov))
+        fast = ~beyond & np.isfinite(ov)
+        assert ev[fast].max() <= 1e-12

@@ -1,6 +1,7 @@
-"""Accuracy of the skeleton's own fp64 log / sqrt / sincos (nt_skeleton.h),
-built for the host, against mpmath at 40 digits; and of the Box-Muller pair
-against the oracle's glibc evaluation of the reference formula."""
+"""Accuracy of the skeleton's own fp64 log / sqrt / sincos / exp
+(nt_skeleton.h), built for the host, against mpmath at 40 digits; and of the
+Box-Muller pair against the oracle's glibc evaluation of the reference
+formula."""
 from __future__ import annotations
 
 import ctypes as C
@@ -30,6 +31,7 @@ def lib():
     L.emu_neg2log.argtypes = [P(C.c_uint32), P(C.c_double), C.c_long]
     L.emu_sincos.argtypes = [P(C.c_uint32), P(C.c_double), P(C.c_double), C.c_long]
     L.emu_sqrt.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
+    L.emu_exp.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
     L.emu_normal_pair.argtypes = [P(C.c_uint32)] * 3 + [P(C.c_double)] * 2 + [C.c_long]
     return L
 
@@ -53,7 +55,10 @@ def sample_u32(n: int, seed: int) -> np.ndarray:
     rng = np.random.default_rng(seed)
     edges = [0, 1, 2, 3, 2**29 - 1, 2**29, 2**29 + 1, 2**30 - 1, 2**30, 2**31 - 1, 2**31, 3 * 2**30 - 1,
              3 * 2**30, 2**32 - 2**29 - 1, 2**32 - 2**29, 2**32 - 3, 2**32 - 2, 2**32 - 1]
-    return _u32(np.concatenate([edges, rng.integers(0, 2**32, n, dtype=np.uint64)]))
+    # both sides of the sine/cosine table's sector boundaries (j 2^24 +- 2^23)
+    sectors = [j * 2**24 + 2**23 + o for j in range(0, 256, 17) for o in (-1, 0, 1)]
+    sectors = [v % 2**32 for v in sectors]
+    return _u32(np.concatenate([edges, sectors, rng.integers(0, 2**32, n, dtype=np.uint64)]))
 
 
 def test_neg2log_within_two_ulp(lib):
@@ -110,3 +115,23 @@ def test_normal_pairs_track_the_reference_formula(lib):
     ref_s = np.array([oracle.normal(int(p), seed, 1) for p in paths])
     assert np.max(np.abs(zc - ref_c)) <= 4e-15
     assert np.max(np.abs(zs - ref_s)) <= 4e-15
+
+
+def test_exp_within_one_ulp_and_special_values(lib):
+    rng = np.random.default_rng(4)
+    x = np.concatenate([rng.uniform(-0.5, 0.5, 4000), rng.uniform(-30.0, 30.0, 2000),
+                        rng.uniform(-708.0, 708.0, 1000), np.arange(-64, 65) * np.log(2.0) / 64,
+                        [0.0, -0.0, 1e-300, -1e-300, 5e-324, 708.0, -708.0]])
+    x = np.ascontiguousarray(x)
+    out = np.zeros(len(x))
+    lib.emu_exp(_ptr(x, C.c_double), _ptr(out, C.c_double), len(x))
+    worst = max(ulp_err(o, mp.exp(mp.mpf(float(xi)))) for xi, o in zip(x, out))
+    assert worst <= 1.0, worst
+    # beyond +-708, the infinities and NaN go to libm: overflow, underflow to
+    # subnormals and zero, NaN propagation
+    sp = np.ascontiguousarray([709.5, 710.0, 1e10, np.inf, -720.0, -745.0, -746.0, -1e10, -np.inf, np.nan])
+    out = np.zeros(len(sp))
+    lib.emu_exp(_ptr(sp, C.c_double), _ptr(out, C.c_double), len(sp))
+    with np.errstate(over="ignore"):
+        want = np.exp(sp[:-1])
+    assert np.array_equal(out[:-1], want) and np.isnan(out[-1])
