@@ -172,7 +172,8 @@ def main() -> int:
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
                     help="C2 (default) prints the headline line; the others print the same fields for that workload")
     ap.add_argument("--precision", choices=["fp64", "fp32"], default=None,
-                    help="precision of a non-default workload (default: the workload's own)")
+                    help="run one workload at one precision and print its line (default: the workload's own; "
+                         "for C2 without it, the headline line with fp64, the reverse sweep and fp32)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -190,7 +191,7 @@ def main() -> int:
     if rocm.probe() < 1:
         print("no gfx950 device visible", file=sys.stderr)
         return 1
-    if args.workload != "C2":
+    if args.workload != "C2" or args.precision:
         return other_workload(rocm, args)
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()
     print(f"[bench] {WORKLOAD}: {len(flat['op'])} nodes, {args.paths:,} scenarios/step", file=sys.stderr, flush=True)
