@@ -81,6 +81,9 @@ def lib() -> C.CDLL:
         L.nt_exec_info_get.argtypes = [C.c_void_p, C.POINTER(NtExecInfo)]
         L.nt_exec_source.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64)]
         L.nt_exec_destroy.argtypes = [C.c_void_p]
+        if L.nt_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI version {L.nt_abi_version()}, this binding expects {ABI_VERSION}: "
+                              "rebuild it")
         _lib = L
     return _lib
 
