@@ -284,6 +284,8 @@ LoopPlan detect_loop(const TapeIR& t) {
 namespace {
 int plan_reverse_loop(const TapeIR& t, const nt_options& o, Plan& p, std::string& err);
 void choose_mode(const TapeIR& t, const nt_options& o, Plan& p);
+double fwd_cost(int op, bool f32);
+double store_cost(bool f32);
 }  // namespace
 
 int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err) {
@@ -371,7 +373,22 @@ int plan_reverse_loop(const TapeIR& t, const nt_options& o, Plan& p, std::string
       }
     }
   }
-  if (ck == NT_CKPT_AUTO) ck = anyFrontier ? NT_CKPT_STORE_DRAWS : NT_CKPT_RECOMPUTE;
+  if (ck == NT_CKPT_AUTO) {
+    // Store the frontier only when recomputing the inactive part of a step
+    // costs more than writing and re-reading its frontier values through HBM
+    // (measured on MI355X: about 48 VALU instructions' worth per 4 bytes at
+    // the replay's rate). With the skeleton's own Box-Muller a draw costs ~30
+    // (fp64), so GBM steps recompute their normals (C2 fp64: 2.1 ms against
+    // 2.7 ms storing them; C5 fp32, 16 correlated normals: 8.5 against 11.6).
+    const bool f32 = p.precision == NT_FP32;
+    double recompute = 0;
+    int nf = 0;
+    for (int j = 0; j < P; ++j) {
+      if (!body_active(j)) recompute += fwd_cost(t.op[s + j], f32);
+      nf += frontier[j];
+    }
+    ck = anyFrontier && store_cost(f32) * nf < recompute ? NT_CKPT_STORE_DRAWS : NT_CKPT_RECOMPUTE;
+  }
   if (!p.adjoints) ck = NT_CKPT_RECOMPUTE;
   p.ckpt = ck;
   if (p.adjoints && ck == NT_CKPT_STORE_DRAWS) {
@@ -453,18 +470,23 @@ int popcount(const uint64_t* x, int W) {
   return n;
 }
 
-// Estimated VALU instructions per lane (fp64 weights; fp32 scales them alike).
-double fwd_cost(int op) {
+// Estimated VALU instructions per lane (fp64 weights; fp32 scales them alike,
+// except for draws, whose fp32 transcendentals are single instructions).
+double fwd_cost(int op, bool f32) {
   switch (op) {
     case NT_OP_ADD: case NT_OP_SUB: case NT_OP_MUL: return 1;
     case NT_OP_MAX: case NT_OP_MIN: return 1;
     case NT_OP_DIV: return 10;
     case NT_OP_EXP: case NT_OP_LOG: return 20;
     case NT_OP_SQRT: return 8;
-    case NT_OP_RANDN: return 45;  // half a Box-Muller pair with its Philox block
+    case NT_OP_RANDN: return f32 ? 15 : 30;  // half a Box-Muller pair with its Philox block
     default: return 0;
   }
 }
+
+// One value per iteration stored in the forward pass and read back in the
+// reverse sweep, in VALU instructions' worth (the HBM round trip dominates).
+double store_cost(bool f32) { return f32 ? 48 : 96; }
 
 double rev_cost(int op, bool aa, bool ba) {
   const double A = aa ? 1 : 0, B = ba ? 1 : 0;
@@ -520,19 +542,20 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   compute_deps(t, p);
   const LoopPlan& L = p.loop;
   const int le = L.found ? L.end() : 0;
+  const bool f32 = p.precision == NT_FP32;
   double rev = 0, tan = 0;
   for (int i = 0; i < t.n; ++i) {
     const int ar = arity(t.op[i]);
     const bool inLoop = L.found && i >= L.start && i < le;
-    if (inLoop && p.ckpt == NT_CKPT_RECOMPUTE && !t.active[i]) rev += fwd_cost(t.op[i]);
+    if (inLoop && p.ckpt == NT_CKPT_RECOMPUTE && !t.active[i]) rev += fwd_cost(t.op[i], f32);
     if (!t.active[i] || ar == 0) continue;
     const bool aa = t.active[t.a[i]] != 0;
     const bool ba = ar >= 2 && t.active[t.b[i]] != 0;
     rev += rev_cost(t.op[i], aa, ba);
-    if (inLoop && p.ckpt != NT_CKPT_STORE_ALL) rev += fwd_cost(t.op[i]);  // the reverse recomputes it
+    if (inLoop && p.ckpt != NT_CKPT_STORE_ALL) rev += fwd_cost(t.op[i], f32);  // the reverse recomputes it
     tan += tan_cost(t, p, i);
   }
-  if (L.found) rev += 8.0 * L.iters * p.n_stored;  // store, reload and the HBM round trip
+  if (L.found) rev += store_cost(f32) * L.iters * p.n_stored;
   p.cost_reverse = rev;
   p.cost_tangent = tan;
   const bool tangent = o.mode == NT_MODE_TANGENT || (o.mode == NT_MODE_AUTO && tan < rev);
@@ -1104,10 +1127,11 @@ void Emitter::header() {
     o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent\n";
     // Polynomial constants held in VGPRs make v_fmac_f64 (accumulator tied to
     // the destination) cost a 64-bit copy per term; the three-source v_fma_f64
-    // needs none.
+    // needs none. (The reverse sweep below asks for the same.)
     if (!f32_) o_ << "// nt-compile: -fmacf64-inst\n";
   } else {
     o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << " mode=reverse\n";
+    if (!f32_) o_ << "// nt-compile: -fmacf64-inst\n";
   }
   o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
   if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
