@@ -90,7 +90,9 @@ typedef struct nt_options {
   int32_t contract;         /* FMA contraction: 0 default (off for fp64, on for fp32), 1 on, -1 off */
   int32_t libm;             /* fp64 Box-Muller: 0 the skeleton's own log/sqrt/sincos, 1 device libm, 2 own log/sqrt + libm sincos */
   int32_t mode;             /* NT_MODE_* */
-  int32_t reserved[6];
+  int32_t markets;          /* nt_lower / nt_compile_check only: lower the kernel that prices this many input
+                               sets from each path's draws (what nt_exec_replay_many compiles); 0 or 1 = one */
+  int32_t reserved[5];
 } nt_options;
 
 typedef struct nt_exec nt_exec;
@@ -153,6 +155,17 @@ int nt_exec_set_inputs(nt_exec *exec, const double *inputs, int32_t n);
  * sums instead of means so callers can combine dispatches exactly. */
 int nt_exec_replay(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed,
                    double *sums, int32_t n_sums, double *timing);
+
+/* Prices `markets` input sets (row-major [markets][n_inputs]) over the same paths and seed in one
+ * dispatch; sums[m * (2 + n_inputs) + c] as nt_exec_replay's sums for set m. In tangent mode each path's
+ * draws are generated once and shared by the sets in registers (a kernel is compiled per set count on
+ * first use); a reverse-sweep executable replays the sets one after another. Either way the sums are
+ * bit-identical to `markets` separate nt_exec_replay calls with those inputs. The executable's bound
+ * inputs are left unchanged. Replaces VulkanAadKernel.replayMany (nablatensor-engine-vulkan/.../
+ * VulkanAadKernel.java:162-238), the draw-sharing form of ScenarioRunner ladders
+ * (nablatensor-core/.../ScenarioRunner.java:36-70). */
+int nt_exec_replay_many(nt_exec *exec, const double *input_sets, int32_t markets, uint64_t paths,
+                        uint64_t offset, uint64_t seed, double *sums, int32_t n_sums, double *timing);
 
 /* Per-path value and adjoints for paths [offset, offset + paths):
  * values[p] and grads[p * n_inputs + j]. A testing aid with no counterpart in

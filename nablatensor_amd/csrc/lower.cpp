@@ -306,6 +306,12 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   if (o.checkpoint < NT_CKPT_AUTO || o.checkpoint > NT_CKPT_STORE_ALL) { err = "unknown checkpoint policy"; return NT_E_INVALID; }
   if (o.seg_len < 0) { err = "seg_len must be >= 0"; return NT_E_INVALID; }
   if (o.mode < NT_MODE_AUTO || o.mode > NT_MODE_TANGENT) { err = "unknown derivative mode"; return NT_E_INVALID; }
+  if (o.markets < 0 || o.markets > 64) { err = "markets must be between 1 and 64"; return NT_E_INVALID; }
+  p.markets = std::max(1, o.markets);
+  if (p.markets > 1 && o.mode == NT_MODE_REVERSE) {
+    err = "several markets per dispatch share draws in tangent mode only";
+    return NT_E_INVALID;
+  }
   if (o.roll >= 0) p.loop = detect_loop(t);
   if (p.loop.found) {
     const int rc = plan_reverse_loop(t, o, p, err);
@@ -538,7 +544,7 @@ double tan_cost(const TapeIR& t, const Plan& p, int i) {
 
 void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.mode = NT_MODE_REVERSE;
-  if (!p.adjoints) return;
+  if (!p.adjoints && p.markets == 1) return;
   compute_deps(t, p);
   const LoopPlan& L = p.loop;
   const int le = L.found ? L.end() : 0;
@@ -558,7 +564,9 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   if (L.found) rev += store_cost(f32) * L.iters * p.n_stored;
   p.cost_reverse = rev;
   p.cost_tangent = tan;
-  const bool tangent = o.mode == NT_MODE_TANGENT || (o.mode == NT_MODE_AUTO && tan < rev);
+  // Several markets per dispatch are priced in tangent mode (also price-only:
+  // the tangent frame without tangents).
+  const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || (p.adjoints && o.mode == NT_MODE_AUTO && tan < rev);
   if (!tangent) return;
   p.mode = NT_MODE_TANGENT;
   p.ckpt = 0;
@@ -580,7 +588,8 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
     if (L.is_carry[j] || L.is_liveout[j]) live += 1 + popcount(&p.posdeps[static_cast<size_t>(j) * W], W);
   }
   const int w = p.precision == NT_FP64 ? 2 : 1;
-  int seg = o.seg_len > 0 ? o.seg_len : (live * w <= 32 ? 4 : live * w <= 64 ? 2 : 1);
+  const int regs = live * w * p.markets;
+  int seg = o.seg_len > 0 ? o.seg_len : (regs <= 32 ? 4 : regs <= 64 ? 2 : 1);
   if ((L.draws & 1) && (seg & 1)) seg += 1;
   seg = std::max(1, std::min(seg, L.iters));
   p.seg = seg;
@@ -636,7 +645,7 @@ class Emitter {
   std::string expr(int op, const std::string& x, const std::string& y, double c, int a) const {
     switch (op) {
       case NT_OP_CONST: return lit(c);
-      case NT_OP_INPUT: return "in" + std::to_string(a);
+      case NT_OP_INPUT: return "in" + std::to_string(a) + ms(true);
       case NT_OP_ADD: return x + " + " + y;
       case NT_OP_SUB: return x + " - " + y;
       case NT_OP_MUL: return x + " * " + y;
@@ -645,7 +654,7 @@ class Emitter {
       case NT_OP_EXP:
         if (f32_) return "nt_expf(" + x + ")";
         if (p_.libm == 1 || slow_) return "exp(" + x + ")";
-        return "nt_exp_fast(" + x + ", nt_slow)";
+        return "nt_exp_fast(" + x + ", nt_slow" + ms(exp_active_) + ")";
       case NT_OP_LOG: return f("log") + "(" + x + ")";
       case NT_OP_SQRT: return f("sqrt") + "(" + x + ")";
       case NT_OP_ABS: return f("fabs") + "(" + x + ")";
@@ -736,12 +745,20 @@ class Emitter {
     return d;
   }
   std::string tname(int node, int j) const;  // straight-line node or loop live-out
-  void tangent(const std::string& ind, int op, const std::string& tn, const std::vector<int>& D, const std::string& Vi,
-               const std::string& Va, const std::string& Vb, const std::function<std::string(int)>& ta,
-               const std::function<std::string(int)>& tb);
+  void tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx, const std::vector<int>& D,
+               const std::string& Vi, const std::string& Va, const std::string& Vb,
+               const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb);
   void tline(int lo, int hi);
   void tsegment(int U, const std::string& sg);
   void body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const;
+
+  // ---- markets (tangent mode): several input sets share each path's draws ----
+  int m_ = 0, mlo_ = 0, mhi_ = 1;  // market being emitted; range of markets in the current body
+  bool exp_active_ = true;         // the EXP being emitted depends on the inputs (per-market flag)
+  std::string ms(bool active) const {
+    return (p_.markets > 1 && active) ? "_m" + std::to_string(m_) : std::string();
+  }
+  std::string msuf(int m) const { return p_.markets > 1 ? "_m" + std::to_string(m) : std::string(); }
 
   // ---- kernel frame ----
   bool slow_ = false;  // emitting the device-libm re-evaluation of a flagged path
@@ -759,9 +776,10 @@ class Emitter {
 
 std::string Emitter::vname(int node) const {
   if (L_.found && node >= L_.start && node < L_.end()) {
-    return "st" + std::to_string(node - (L_.start + (L_.iters - 1) * L_.period));
+    const int pos = node - (L_.start + (L_.iters - 1) * L_.period);
+    return "st" + std::to_string(pos) + ms(t_.active[L_.start + pos]);
   }
-  return "v" + std::to_string(node);
+  return "v" + std::to_string(node) + ms(t_.active[node]);
 }
 
 std::string Emitter::dname(int node) const {
@@ -821,12 +839,13 @@ void Emitter::line_reverse(int lo, int hi) {
 // operands of the first iteration come from the segment-start state (st* in
 // the forward pass, checkpoint k* in the recompute).
 std::string Emitter::body_value(int u, int kind, int ref, bool recompute) const {
-  if (kind == ARG_BODY) return "r" + std::to_string(u) + "_" + std::to_string(ref);
+  if (kind == ARG_BODY) return "r" + std::to_string(u) + "_" + std::to_string(ref) + ms(t_.active[L_.start + ref]);
   if (kind == ARG_CARRY) {
-    if (u > 0) return "r" + std::to_string(u - 1) + "_" + std::to_string(ref);
-    return (recompute ? "k" : "st") + std::to_string(ref);
+    const std::string m = ms(t_.active[L_.start + ref]);
+    if (u > 0) return "r" + std::to_string(u - 1) + "_" + std::to_string(ref) + m;
+    return (recompute ? "k" : "st") + std::to_string(ref) + m;
   }
-  return "v" + std::to_string(ref);
+  return "v" + std::to_string(ref) + ms(t_.active[ref]);
 }
 
 // Emits one segment of U iterations. `sg` is the segment index expression;
@@ -942,19 +961,19 @@ void Emitter::segment(int U, const std::string& sg, bool forward) {
 std::string Emitter::tname(int node, int j) const {
   if (L_.found && node >= L_.start && node < L_.end()) {
     const int pos = node - (L_.start + (L_.iters - 1) * L_.period);
-    return poshas(pos, j) ? "ts" + std::to_string(pos) + "_" + std::to_string(j) : "";
+    return poshas(pos, j) ? "ts" + std::to_string(pos) + "_" + std::to_string(j) + ms(true) : "";
   }
   if (!has(node, j)) return "";
   if (t_.op[node] == NT_OP_INPUT) return "#1";
-  return "t" + std::to_string(node) + "_" + std::to_string(j);
+  return "t" + std::to_string(node) + "_" + std::to_string(j) + ms(true);
 }
 
 // Tangent of one active node for each input j in D, named tn + j, from the
 // operand tangents ta(j), tb(j). The local derivatives are those of the
 // reverse rules in rev(): d/da and d/db of ADD SUB MUL DIV NEG EXP LOG SQRT
 // ABS, and MAX/MIN following operand a when a >= b (a <= b), else b.
-void Emitter::tangent(const std::string& ind, int op, const std::string& tn, const std::vector<int>& D,
-                      const std::string& Vi, const std::string& Va, const std::string& Vb,
+void Emitter::tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx,
+                      const std::vector<int>& D, const std::string& Vi, const std::string& Va, const std::string& Vb,
                       const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb) {
   if (D.empty()) return;
   const std::string one = f32_ ? "1.0f" : "1.0";
@@ -964,7 +983,7 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
   auto mulv = [&](const std::string& T, const std::string& v) { return T == "#1" ? v : "(" + T + " * " + v + ")"; };
   bool needB = false;
   for (int j : D) needB |= !tb(j).empty();
-  const std::string q = tn + "q", r = tn + "r", c = tn + "c";
+  const std::string q = tn + "q" + sfx, r = tn + "r" + sfx, c = tn + "c" + sfx;
   switch (op) {
     case NT_OP_DIV:
       o_ << ind << "const real " << q << " = " << one << " / " << Vb << ";\n";
@@ -1017,7 +1036,7 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
         break;
       default: break;
     }
-    o_ << ind << "const real " << tn << j << " = " << (e.empty() ? zero : e) << ";\n";
+    o_ << ind << "const real " << tn << j << sfx << " = " << (e.empty() ? zero : e) << ";\n";
   }
 }
 
@@ -1026,30 +1045,37 @@ void Emitter::tline(int lo, int hi) {
   for (int i = lo; i < hi; ++i) {
     const int op = t_.op[i];
     if (op == NT_OP_RANDN) {
-      line_draw(lo, i);  // a draw is never active
+      line_draw(lo, i);  // a draw is never active: one per path, shared by the markets
       continue;
     }
     const int ar = arity(op);
-    const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
-    const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
-    o_ << "    const real v" << i << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
-    if (!t_.active[i] || ar == 0) continue;
-    const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
-    tangent("    ", op, "t" + std::to_string(i) + "_", deplist(i), "v" + std::to_string(i), x, y,
-            [&](int j) { return tname(a, j); }, [&](int j) { return b >= 0 ? tname(b, j) : std::string(); });
+    const bool act = t_.active[i] != 0;
+    for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+      m_ = m;
+      exp_active_ = act;
+      const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
+      const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
+      o_ << "    const real v" << i << ms(act) << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+      if (!act || ar == 0 || !p_.adjoints) continue;
+      const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
+      tangent("    ", op, "t" + std::to_string(i) + "_", ms(true), deplist(i), "v" + std::to_string(i) + ms(true), x, y,
+              [&](int j) { return tname(a, j); }, [&](int j) { return b >= 0 ? tname(b, j) : std::string(); });
+    }
   }
 }
 
 void Emitter::body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const {
+  const std::string m = ms(true);
   if (kind == ARG_BODY) {
-    fn = [this, u, ref](int j) {
-      return poshas(ref, j) ? "tr" + std::to_string(u) + "_" + std::to_string(ref) + "_" + std::to_string(j) : std::string();
+    fn = [this, u, ref, m](int j) {
+      return poshas(ref, j) ? "tr" + std::to_string(u) + "_" + std::to_string(ref) + "_" + std::to_string(j) + m
+                            : std::string();
     };
   } else if (kind == ARG_CARRY) {
-    fn = [this, u, ref](int j) {
+    fn = [this, u, ref, m](int j) {
       if (!poshas(ref, j)) return std::string();
-      return u > 0 ? "tr" + std::to_string(u - 1) + "_" + std::to_string(ref) + "_" + std::to_string(j)
-                   : "ts" + std::to_string(ref) + "_" + std::to_string(j);
+      return u > 0 ? "tr" + std::to_string(u - 1) + "_" + std::to_string(ref) + "_" + std::to_string(j) + m
+                   : "ts" + std::to_string(ref) + "_" + std::to_string(j) + m;
     };
   } else if (kind == ARG_INV) {
     fn = [this, ref](int j) { return tname(ref, j); };
@@ -1089,21 +1115,34 @@ void Emitter::tsegment(int U, const std::string& sg) {
         continue;
       }
       const int ar = arity(op);
-      const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], false) : "";
-      const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], false) : "";
-      o_ << ind << "const real " << name << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
-      if (!t_.active[i] || ar == 0) continue;
-      std::function<std::string(int)> ta, tb;
-      body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
-      body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
-      tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", posdeplist(j), name, x, y, ta, tb);
+      const bool act = t_.active[i] != 0;
+      for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+        m_ = m;
+        exp_active_ = act;
+        const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], false) : "";
+        const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], false) : "";
+        o_ << ind << "const real " << name << ms(act) << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+        if (!act || ar == 0 || !p_.adjoints) continue;
+        std::function<std::string(int)> ta, tb;
+        body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
+        body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
+        tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", ms(true), posdeplist(j),
+                name + ms(true), x, y, ta, tb);
+      }
     }
   }
   for (int j = 0; j < P; ++j) {
     if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
-    o_ << ind << "st" << j << " = r" << (U - 1) << "_" << j << ";\n";
-    if (!t_.active[s + j]) continue;
-    for (int k : posdeplist(j)) o_ << ind << "ts" << j << "_" << k << " = tr" << (U - 1) << "_" << j << "_" << k << ";\n";
+    const bool act = t_.active[s + j] != 0;
+    for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+      m_ = m;
+      const std::string sm = ms(act);
+      o_ << ind << "st" << j << sm << " = r" << (U - 1) << "_" << j << sm << ";\n";
+      if (!act || !p_.adjoints) continue;
+      for (int k : posdeplist(j)) {
+        o_ << ind << "ts" << j << "_" << k << sm << " = tr" << (U - 1) << "_" << j << "_" << k << sm << ";\n";
+      }
+    }
   }
   o_ << "    }\n";
 }
@@ -1146,9 +1185,14 @@ void Emitter::header() {
   o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
   o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
   if (needs_tables()) o_ << "  nt_tables_load();\n";
-  for (int j = 0; j < nin; ++j) o_ << "  const real in" << j << " = (real)inputs[" << j << "];\n";
-  o_ << "  double acc[" << p_.n_channels << "];\n";
-  o_ << "  for (int c = 0; c < " << p_.n_channels << "; ++c) acc[c] = 0.0;\n";
+  for (int m = 0; m < p_.markets; ++m) {
+    for (int j = 0; j < nin; ++j) {
+      o_ << "  const real in" << j << msuf(m) << " = (real)inputs[" << m * nin + j << "];\n";
+    }
+  }
+  const int nacc = p_.n_channels * p_.markets;
+  o_ << "  double acc[" << nacc << "];\n";
+  o_ << "  for (int c = 0; c < " << nacc << "; ++c) acc[c] = 0.0;\n";
   o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
   o_ << "    const nt_u64 path = p + path_offset;\n";
   o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
@@ -1169,11 +1213,16 @@ void Emitter::body_tangent() {
     for (int j = 0; j < L_.period; ++j) {
       if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
       const int init = L_.is_carry[j] ? L_.carry_init[j] : -1;
-      o_ << "    real st" << j << " = " << (init >= 0 ? "v" + std::to_string(init) : zero) << ";\n";
-      if (!t_.active[L_.start + j]) continue;
-      for (int k : posdeplist(j)) {
-        const std::string tin = init >= 0 ? tname(init, k) : "";
-        o_ << "    real ts" << j << "_" << k << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin) << ";\n";
+      const bool act = t_.active[L_.start + j] != 0;
+      for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+        m_ = m;
+        o_ << "    real st" << j << ms(act) << " = " << (init >= 0 ? vname(init) : zero) << ";\n";
+        if (!act || !p_.adjoints) continue;
+        for (int k : posdeplist(j)) {
+          const std::string tin = init >= 0 ? tname(init, k) : "";
+          o_ << "    real ts" << j << "_" << k << ms(true) << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin)
+             << ";\n";
+        }
       }
     }
     if (p_.nseg_full > 0) {
@@ -1183,12 +1232,15 @@ void Emitter::body_tangent() {
     if (p_.tail) tsegment(p_.tail, std::to_string(p_.nseg_full) + "u");
     tline(le, n);
   }
-  o_ << "    nt_y = (double)" << vname(t_.output) << ";\n";
-  if (!p_.adjoints) return;
-  for (int j = 0; j < t_.n_in; ++j) {
-    const std::string g = tname(t_.output, j);
-    o_ << "    nt_g[" << j << "] = " << (g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g)
-       << ";\n";
+  for (int m = mlo_; m < mhi_; ++m) {
+    m_ = m;
+    o_ << "    nt_y" << msuf(m) << " = (double)" << vname(t_.output) << ";\n";
+    if (!p_.adjoints) continue;
+    for (int j = 0; j < t_.n_in; ++j) {
+      const std::string g = tname(t_.output, j);
+      o_ << "    nt_g" << msuf(m) << "[" << j << "] = "
+         << (g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g) << ";\n";
+    }
   }
 }
 
@@ -1260,34 +1312,56 @@ std::string Emitter::run() {
   // is the only one a Monte-Carlo path normally takes, and it stays one
   // basic block per loop trip.
   const bool fallback = exp_fallback();
-  o_ << "    double nt_y;\n";
-  if (p_.adjoints && nin > 0) o_ << "    double nt_g[" << nin << "];\n";
-  if (fallback) o_ << "    bool nt_slow = false;\n";
+  const int M = p_.markets;
+  for (int m = 0; m < M; ++m) {
+    o_ << "    double nt_y" << msuf(m) << ";\n";
+    if (p_.adjoints && nin > 0) o_ << "    double nt_g" << msuf(m) << "[" << nin << "];\n";
+  }
+  if (fallback) {
+    o_ << "    bool nt_slow = false;\n";  // an exponent shared by every market
+    for (int m = 0; m < M && M > 1; ++m) o_ << "    bool nt_slow" << msuf(m) << " = false;\n";
+  }
   slow_ = false;
+  mlo_ = 0;
+  mhi_ = M;
   o_ << "    {\n";
   if (tangent) body_tangent(); else body_reverse();
   o_ << "    }\n";
   if (fallback) {
-    o_ << "    if (nt_slow) {\n";
+    // Each market is evaluated again alone, so its result is the one a
+    // single-market kernel gives it.
     slow_ = true;
-    if (tangent) body_tangent(); else body_reverse();
+    for (int m = 0; m < M; ++m) {
+      o_ << "    if (nt_slow" << (M > 1 ? " || nt_slow" + msuf(m) : std::string()) << ") {\n";
+      mlo_ = m;
+      mhi_ = m + 1;
+      if (tangent) body_tangent(); else body_reverse();
+      o_ << "    }\n";
+    }
     slow_ = false;
-    o_ << "    }\n";
+    mlo_ = 0;
+    mhi_ = M;
   }
-  o_ << "    acc[0] += nt_y;\n    acc[1] += nt_y * nt_y;\n";
-  if (p_.adjoints) {
-    for (int j = 0; j < nin; ++j) o_ << "    acc[" << 2 + j << "] += nt_g[" << j << "];\n";
+  for (int m = 0; m < M; ++m) {
+    const std::string y = "nt_y" + msuf(m);
+    o_ << "    acc[" << m * NCH << "] += " << y << ";\n    acc[" << m * NCH + 1 << "] += " << y << " * " << y << ";\n";
+    if (p_.adjoints) {
+      for (int j = 0; j < nin; ++j) o_ << "    acc[" << m * NCH + 2 + j << "] += nt_g" << msuf(m) << "[" << j << "];\n";
+    }
   }
   o_ << "#ifdef NT_DUMP_PATHS\n";
-  o_ << "    out_v[p] = nt_y;\n";
-  for (int j = 0; j < nin; ++j) {
-    o_ << "    out_g[p * " << nin << "u + " << j << "u] = " << (p_.adjoints ? "nt_g[" + std::to_string(j) + "]" : "0.0")
-       << ";\n";
+  for (int m = 0; m < M; ++m) {
+    const std::string row = M > 1 ? "(" + std::to_string(m) + "u * n_paths + p)" : std::string("p");
+    o_ << "    out_v[" << row << "] = nt_y" << msuf(m) << ";\n";
+    for (int j = 0; j < nin; ++j) {
+      o_ << "    out_g[" << row << " * " << nin << "u + " << j << "u] = "
+         << (p_.adjoints ? "nt_g" + msuf(m) + "[" + std::to_string(j) + "]" : std::string("0.0")) << ";\n";
+    }
   }
   o_ << "#endif\n";
   o_ << "  }\n";
-  o_ << "  __shared__ double nt_lds[" << NCH << " * (" << p_.block << " / 64)];\n";
-  o_ << "  nt_block_store<" << NCH << ">(acc, partials, nt_lds);\n";
+  o_ << "  __shared__ double nt_lds[" << NCH * M << " * (" << p_.block << " / 64)];\n";
+  o_ << "  nt_block_store<" << NCH * M << ">(acc, partials, nt_lds);\n";
   o_ << "}\n";
   return o_.str();
 }

@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <sstream>
@@ -274,7 +275,18 @@ int device_index(int& dev) {
 
 }  // namespace
 
+// A kernel that prices several input sets per path (nt_exec_replay_many).
+struct MarketVariant {
+  int vgprs = 0, scratch = 0;
+  hipModule_t mod = nullptr;
+  hipFunction_t fn = nullptr, fn_finish = nullptr;
+  double* d_inputs = nullptr;
+  double* d_partials = nullptr;
+  double* d_sums = nullptr;
+};
+
 struct nt_exec {
+  nt_options opts{};
   Lowered low;
   nt_exec_info info{};
   std::vector<char> code;
@@ -290,6 +302,9 @@ struct nt_exec {
   int grid_cap = 1;
   std::vector<double> inputs;
   bool dirty = true;
+  std::map<int, MarketVariant> markets;  // by set count
+  int market_chunk = 0;                  // input sets per multi-market dispatch, 0 until chosen
+  double* d_set_inputs = nullptr;        // one input set at a time (reverse-sweep executables)
 };
 
 extern "C" {
@@ -355,6 +370,8 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   if (!out) return fail(NT_E_INVALID, "out is null");
   *out = nullptr;
   std::unique_ptr<nt_exec> x(new nt_exec());
+  if (options) x->opts = *options;
+  if (x->opts.markets > 1) return fail(NT_E_INVALID, "markets is a lowering option; price several input sets with nt_exec_replay_many");
   int rc = lower(tape, options, x->low);
   if (rc != NT_OK) return rc;
   rc = device_index(x->dev);
@@ -400,12 +417,30 @@ int nt_exec_set_inputs(nt_exec* x, const double* inputs, int32_t n) {
   return NT_OK;
 }
 
+// Grid of a dispatch over `paths`: one block per 256 paths up to the resident
+// cap. Every kernel of an executable (single- or multi-market) uses it, so a
+// path always lands on the same lane and block and the sums agree bit for bit.
+static int grid_for(const nt_exec* x, uint64_t paths) {
+  const int block = x->low.plan.block;
+  const uint64_t need = (paths + static_cast<uint64_t>(block) - 1) / static_cast<uint64_t>(block);
+  return std::max(1, static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap))));
+}
+
+static int launch_kernel(nt_exec* x, hipFunction_t fn, double* d_inputs, double* d_partials, uint64_t paths,
+                         uint64_t offset, uint64_t seed, double* out_v, double* out_g, int& grid) {
+  const int block = x->low.plan.block;
+  grid = grid_for(x, paths);
+  void* args[] = {&d_inputs, &paths, &offset, &seed, &d_partials, &x->d_scratch, &out_v, &out_g};
+  NT_HIP(hipModuleLaunchKernel(fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0, x->stream,
+                               args, nullptr),
+         "hipModuleLaunchKernel(nt_replay)");
+  return NT_OK;
+}
+
 static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v,
                          double* out_g, int& grid) {
   const int block = x->low.plan.block;
-  const uint64_t need = (paths + static_cast<uint64_t>(block) - 1) / static_cast<uint64_t>(block);
-  grid = static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap)));
-  grid = std::max(grid, 1);
+  grid = grid_for(x, paths);
   if (x->dirty) {
     if (!x->inputs.empty()) {
       NT_HIP(hipMemcpyAsync(x->d_inputs, x->inputs.data(), sizeof(double) * x->inputs.size(), hipMemcpyHostToDevice,
@@ -440,6 +475,152 @@ int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, d
          "hipModuleLaunchKernel(nt_finish)");
   NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
   NT_HIP(hipMemcpyAsync(sums, x->d_sums, sizeof(double) * nch, hipMemcpyDeviceToHost, x->stream), "hipMemcpyAsync(sums)");
+  NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  if (timing) {
+    float all = 0, rep = 0;
+    NT_HIP(hipEventElapsedTime(&all, x->ev[0], x->ev[2]), "hipEventElapsedTime");
+    NT_HIP(hipEventElapsedTime(&rep, x->ev[0], x->ev[1]), "hipEventElapsedTime");
+    timing[0] = all;
+    timing[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    timing[2] = rep;
+  }
+  return NT_OK;
+}
+
+static int market_variant(nt_exec* x, int markets, MarketVariant*& out) {
+  auto it = x->markets.find(markets);
+  if (it != x->markets.end()) {
+    out = &it->second;
+    return NT_OK;
+  }
+  nt_options o = x->opts;
+  o.markets = markets;
+  o.mode = NT_MODE_TANGENT;
+  std::string err;
+  ntl::Plan plan;
+  int rc = ntl::make_plan(x->low.ir, &o, plan, err);
+  if (rc != NT_OK) return fail(rc, err);
+  const std::string src = ntl::emit_source(x->low.ir, plan);
+  std::vector<char> code;
+  double secs = 0;
+  rc = compile_hiprtc(src, false, code, secs);
+  if (rc != NT_OK) return rc;
+  MarketVariant v;
+  nt_exec_info res{};
+  kernel_resources(code, "nt_replay", res);
+  v.vgprs = res.vgprs;
+  v.scratch = res.scratch_bytes;
+  NT_HIP(hipModuleLoadData(&v.mod, code.data()), "hipModuleLoadData(markets)");
+  const int nin = x->low.ir.n_in;
+  const size_t nch = static_cast<size_t>(x->low.plan.n_channels) * markets;
+  hipError_t e = hipModuleGetFunction(&v.fn, v.mod, "nt_replay");
+  if (e == hipSuccess) e = hipModuleGetFunction(&v.fn_finish, v.mod, "nt_finish");
+  if (e == hipSuccess) e = hipMalloc(&v.d_inputs, sizeof(double) * std::max<size_t>(1, static_cast<size_t>(nin) * markets));
+  if (e == hipSuccess) e = hipMalloc(&v.d_partials, sizeof(double) * static_cast<size_t>(x->grid_cap) * nch);
+  if (e == hipSuccess) e = hipMalloc(&v.d_sums, sizeof(double) * nch);
+  if (e != hipSuccess) {
+    if (v.d_sums) (void)hipFree(v.d_sums);
+    if (v.d_partials) (void)hipFree(v.d_partials);
+    if (v.d_inputs) (void)hipFree(v.d_inputs);
+    (void)hipModuleUnload(v.mod);
+    return hip_fail(e, "loading the multi-market kernel");
+  }
+  out = &(x->markets[markets] = v);
+  return NT_OK;
+}
+
+// Input sets per multi-market kernel: the most whose kernel keeps two waves
+// per SIMD (at most 256 VGPRs) without spilling. Each set adds its own copy of
+// the step's state, tangents and loop invariants to the registers, so beyond
+// that point occupancy or scratch costs more than the shared draws save.
+static int choose_market_chunk(nt_exec* x, int& chunk) {
+  if (x->market_chunk > 0) {
+    chunk = x->market_chunk;
+    return NT_OK;
+  }
+  MarketVariant* v1 = nullptr;
+  MarketVariant* v2 = nullptr;
+  int rc = market_variant(x, 1, v1);
+  if (rc == NT_OK) rc = market_variant(x, 2, v2);
+  if (rc != NT_OK) return rc;
+  const int per = std::max(1, v2->vgprs - v1->vgprs);
+  int c = std::max(1, std::min(8, 1 + (256 - v1->vgprs) / per));
+  if (v2->vgprs > 256 || v2->scratch > 0) c = 1;
+  while (c > 2) {
+    MarketVariant* v = nullptr;
+    rc = market_variant(x, c, v);
+    if (rc != NT_OK) return rc;
+    if (v->vgprs <= 256 && v->scratch == 0) break;
+    --c;
+  }
+  x->market_chunk = c;
+  chunk = c;
+  return NT_OK;
+}
+
+int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, uint64_t paths, uint64_t offset,
+                        uint64_t seed, double* sums, int32_t n_sums, double* timing) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  if (paths == 0) return fail(NT_E_INVALID, "paths must be positive");
+  if (markets < 1 || markets > 64) return fail(NT_E_INVALID, "markets must be between 1 and 64");
+  const int nin = x->low.ir.n_in;
+  const int nch = x->low.plan.n_channels;
+  if (nin > 0 && !input_sets) return fail(NT_E_INVALID, "input_sets is null");
+  if (!sums || n_sums != nch * markets) return fail(NT_E_INVALID, "sums must hold markets * (2 + n_inputs) doubles");
+  const auto t0 = std::chrono::steady_clock::now();
+  NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
+  const bool shared = x->low.plan.mode == NT_MODE_TANGENT;
+  NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");
+  int grid = 0;
+  if (shared) {
+    int chunk = 1;
+    int rc = choose_market_chunk(x, chunk);
+    if (rc != NT_OK) return rc;
+    NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");  // after any first-use compiles
+    for (int m0 = 0; m0 < markets; m0 += chunk) {
+      const int k = std::min(chunk, markets - m0);
+      MarketVariant* v = nullptr;
+      rc = market_variant(x, k, v);
+      if (rc != NT_OK) return rc;
+      if (nin > 0) {
+        NT_HIP(hipMemcpyAsync(v->d_inputs, input_sets + static_cast<size_t>(m0) * nin, sizeof(double) * nin * k,
+                              hipMemcpyHostToDevice, x->stream),
+               "hipMemcpyAsync(input sets)");
+      }
+      rc = launch_kernel(x, v->fn, v->d_inputs, v->d_partials, paths, offset, seed, nullptr, nullptr, grid);
+      if (rc != NT_OK) return rc;
+      unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch * k);
+      void* fargs[] = {&v->d_partials, &blocks, &nchu, &v->d_sums};
+      NT_HIP(hipModuleLaunchKernel(v->fn_finish, 1, 1, 1, 256, 1, 1, 0, x->stream, fargs, nullptr),
+             "hipModuleLaunchKernel(nt_finish)");
+      NT_HIP(hipMemcpyAsync(sums + static_cast<size_t>(m0) * nch, v->d_sums, sizeof(double) * nch * k,
+                            hipMemcpyDeviceToHost, x->stream),
+             "hipMemcpyAsync(sums)");
+    }
+    NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
+    NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
+  } else {
+    // The reverse sweep keeps one set's state per lane: replay the sets in turn.
+    if (!x->d_set_inputs) NT_HIP(hipMalloc(&x->d_set_inputs, sizeof(double) * std::max(1, nin)), "hipMalloc(set inputs)");
+    for (int m = 0; m < markets; ++m) {
+      if (nin > 0) {
+        NT_HIP(hipMemcpyAsync(x->d_set_inputs, input_sets + static_cast<size_t>(m) * nin, sizeof(double) * nin,
+                              hipMemcpyHostToDevice, x->stream),
+               "hipMemcpyAsync(input set)");
+      }
+      int rc = launch_kernel(x, x->fn, x->d_set_inputs, x->d_partials, paths, offset, seed, nullptr, nullptr, grid);
+      if (rc != NT_OK) return rc;
+      unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
+      void* fargs[] = {&x->d_partials, &blocks, &nchu, &x->d_sums};
+      NT_HIP(hipModuleLaunchKernel(x->fn_finish, 1, 1, 1, 256, 1, 1, 0, x->stream, fargs, nullptr),
+             "hipModuleLaunchKernel(nt_finish)");
+      NT_HIP(hipMemcpyAsync(sums + static_cast<size_t>(m) * nch, x->d_sums, sizeof(double) * nch, hipMemcpyDeviceToHost,
+                            x->stream),
+             "hipMemcpyAsync(sums)");
+    }
+    NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
+    NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
+  }
   NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
   if (timing) {
     float all = 0, rep = 0;
@@ -513,6 +694,14 @@ int nt_exec_destroy(nt_exec* x) {
   if (x->d_sums) (void)hipFree(x->d_sums);
   if (x->d_partials) (void)hipFree(x->d_partials);
   if (x->d_inputs) (void)hipFree(x->d_inputs);
+  for (auto& kv : x->markets) {
+    MarketVariant& v = kv.second;
+    if (v.d_sums) (void)hipFree(v.d_sums);
+    if (v.d_partials) (void)hipFree(v.d_partials);
+    if (v.d_inputs) (void)hipFree(v.d_inputs);
+    if (v.mod) (void)hipModuleUnload(v.mod);
+  }
+  if (x->d_set_inputs) (void)hipFree(x->d_set_inputs);
   if (x->mod_dump) (void)hipModuleUnload(x->mod_dump);
   if (x->mod) (void)hipModuleUnload(x->mod);
   delete x;

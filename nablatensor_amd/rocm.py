@@ -22,8 +22,8 @@ NT_MODE_AUTO, NT_MODE_REVERSE, NT_MODE_TANGENT = 0, 1, 2
 ABI_VERSION = 2
 
 EXPORTS = ("nt_probe", "nt_device_name", "nt_lower", "nt_compile_check", "nt_exec_create", "nt_exec_set_inputs",
-           "nt_exec_replay", "nt_exec_replay_paths", "nt_exec_info_get", "nt_exec_source", "nt_exec_destroy",
-           "nt_last_error", "nt_abi_version")
+           "nt_exec_replay", "nt_exec_replay_many", "nt_exec_replay_paths", "nt_exec_info_get", "nt_exec_source",
+           "nt_exec_destroy", "nt_last_error", "nt_abi_version")
 
 
 class NtTape(C.Structure):
@@ -37,7 +37,7 @@ class NtOptions(C.Structure):
     _fields_ = [("precision", C.c_int32), ("adjoints", C.c_int32), ("block", C.c_int32),
                 ("max_blocks", C.c_int32), ("checkpoint", C.c_int32), ("seg_len", C.c_int32),
                 ("roll", C.c_int32), ("contract", C.c_int32), ("libm", C.c_int32), ("mode", C.c_int32),
-                ("reserved", C.c_int32 * 6)]
+                ("markets", C.c_int32), ("reserved", C.c_int32 * 5)]
 
 
 class NtExecInfo(C.Structure):
@@ -76,6 +76,8 @@ def lib() -> C.CDLL:
         L.nt_exec_set_inputs.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.c_int32]
         L.nt_exec_replay.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(C.c_double),
                                      C.c_int32, C.POINTER(C.c_double)]
+        L.nt_exec_replay_many.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.c_int32, C.c_uint64, C.c_uint64,
+                                          C.c_uint64, C.POINTER(C.c_double), C.c_int32, C.POINTER(C.c_double)]
         L.nt_exec_replay_paths.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64,
                                            C.POINTER(C.c_double), C.POINTER(C.c_double)]
         L.nt_exec_info_get.argtypes = [C.c_void_p, C.POINTER(NtExecInfo)]
@@ -116,9 +118,9 @@ class TapeArrays:
 
 def options(precision: str = "fp64", adjoints: bool = True, block: int = 0, max_blocks: int = 0,
             checkpoint: int = NT_CKPT_AUTO, seg_len: int = 0, roll: int = 1, contract: int = 0,
-            libm: int = 0, mode: int = 0) -> NtOptions:
+            libm: int = 0, mode: int = 0, markets: int = 0) -> NtOptions:
     return NtOptions(NT_FP32 if precision == "fp32" else NT_FP64, 1 if adjoints else 0, block, max_blocks,
-                     checkpoint, seg_len, roll, contract, libm, mode)
+                     checkpoint, seg_len, roll, contract, libm, mode, markets)
 
 
 def probe() -> int:
@@ -177,6 +179,21 @@ class Executable:
         _check(lib().nt_exec_replay(self._h, paths, offset & 0xFFFFFFFFFFFFFFFF, seed & 0xFFFFFFFFFFFFFFFF,
                                     sums.ctypes.data_as(C.POINTER(C.c_double)), len(sums),
                                     timing.ctypes.data_as(C.POINTER(C.c_double))))
+        return sums, {"kernel_ms": timing[0], "wall_ms": timing[1], "replay_ms": timing[2]}
+
+    def replay_many(self, input_sets, paths: int, offset: int = 0, seed: int = 42):
+        """Raw sums per input set, shape (markets, 2 + n_inputs), from one dispatch
+        that shares each path's draws across the sets; and timing as replay()."""
+        x = np.ascontiguousarray(input_sets, dtype=np.float64)
+        markets = x.shape[0] if x.ndim == 2 else 1
+        if x.size != markets * self.n_inputs:
+            raise ValueError(f"expected {markets} x {self.n_inputs} input values, got shape {x.shape}")
+        sums = np.zeros((markets, 2 + self.n_inputs), dtype=np.float64)
+        timing = np.zeros(3, dtype=np.float64)
+        _check(lib().nt_exec_replay_many(self._h, x.ctypes.data_as(C.POINTER(C.c_double)), markets, paths,
+                                         offset & 0xFFFFFFFFFFFFFFFF, seed & 0xFFFFFFFFFFFFFFFF,
+                                         sums.ctypes.data_as(C.POINTER(C.c_double)), sums.size,
+                                         timing.ctypes.data_as(C.POINTER(C.c_double))))
         return sums, {"kernel_ms": timing[0], "wall_ms": timing[1], "replay_ms": timing[2]}
 
     def replay_paths(self, paths: int, offset: int = 0, seed: int = 42):

@@ -44,12 +44,19 @@ class EmulatedKernel:
         self.n_inputs = n_inputs
         self.slots = tape_slots
 
-    def run(self, inputs, paths: int, offset: int = 0, seed: int = 42, grid: int = 4, block: int = 64):
-        x = np.ascontiguousarray(inputs, dtype=np.float64)
-        sums = np.zeros(2 + self.n_inputs)
-        values = np.zeros(paths)
-        grads = np.zeros((paths, max(1, self.n_inputs)))
+    def run(self, inputs, paths: int, offset: int = 0, seed: int = 42, grid: int = 4, block: int = 64,
+            markets: int = 1):
+        """One emulated dispatch. With markets > 1, `inputs` holds one row per
+        market and every result gains a leading market axis."""
+        x = np.ascontiguousarray(inputs, dtype=np.float64).reshape(-1)
+        sums = np.zeros(markets * (2 + self.n_inputs))
+        values = np.zeros(markets * paths)
+        grads = np.zeros((markets * paths, max(1, self.n_inputs)))
         p = lambda a: a.ctypes.data_as(C.POINTER(C.c_double))
         self.lib.emu_run(paths, offset & (2**64 - 1), seed & (2**64 - 1), p(x), p(sums), p(values), p(grads),
                          grid, block, self.slots)
-        return sums, values, grads[:, :self.n_inputs]
+        grads = grads[:, :self.n_inputs]
+        if markets == 1:
+            return sums, values, grads
+        return (sums.reshape(markets, 2 + self.n_inputs), values.reshape(markets, paths),
+                grads.reshape(markets, paths, self.n_inputs))

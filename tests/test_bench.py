@@ -69,3 +69,11 @@ def test_more_than_one_gpu_is_refused(monkeypatch, capsys):
     monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "8"])
     assert bench.main() == 2
     assert "one GPU" in capsys.readouterr().err
+
+
+def test_markets_line(patched, monkeypatch, capsys):
+    monkeypatch.setattr(bench, "measure_markets", lambda *a, **k: {
+        "value": 1e9, "ms_per_step": 2.0, "replay_kernel_ms": 2.0, "single_market_kernel_ms": 1.0, "markets": 4,
+        "mode": "tangent", "speedup_vs_separate": 2.0})
+    out = run_main(monkeypatch, capsys, ["--workload", "C2", "--markets", "4", "--steps", "1", "--warmup", "0"])
+    assert out["unit"] == "market-scenarios/s" and out["config"]["markets"] == 4

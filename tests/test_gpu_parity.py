@@ -153,3 +153,35 @@ def test_price_only_kernel(rocm, tapes):
     ref = oracle.replay_sums(tapes["C2"], 50_000, 0, 42, adjoints=False)
     assert abs(sums[0] - ref[0]) <= 1e-10 * abs(ref[0])
     assert np.all(sums[2:] == 0.0)
+
+
+@pytest.mark.parametrize("name,mode,paths", [("C2", 0, 200_000), ("C4", 0, 20_000), ("C3", 1, 50_000)])
+def test_replay_many_equals_separate_replays(rocm, tapes, name, mode, paths):
+    """Several input sets in one dispatch (draws shared in tangent mode, one
+    replay per set for a reverse-sweep executable): each set's sums equal a
+    separate replay with those inputs bit for bit, and the oracle's to 1e-10."""
+    t = tapes[name]
+    x0 = np.array(t["recorded_inputs"])
+    sets = np.stack([x0, x0 * 1.02, x0 * 0.98, x0 * 1.05])
+    print(f"case {name} mode={mode} markets=4 paths={paths}", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
+        many, _ = x.replay_many(sets, paths, OFFSET, 42)
+        for m in range(len(sets)):
+            x.set_inputs(sets[m])
+            one, _ = x.replay(paths, OFFSET, 42)
+            assert np.array_equal(many[m], one), m
+    ref = oracle.replay_sums(t, paths, OFFSET, 42, inputs=sets[1])
+    # price and sum of squares componentwise; the gradient normwise (a Heston
+    # gradient component can nearly cancel over 20k paths)
+    assert rel_err(many[1][:2], ref[:2], floor=1e-300) <= 1e-10
+    assert np.max(np.abs(many[1][2:] - ref[2:])) <= 1e-10 * np.max(np.abs(ref[2:]))
+
+
+def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
+    t = tapes["C2"]
+    with rocm.Executable(t, rocm.options("fp64")) as x:
+        one, _ = x.replay(10_000, 0, 7)
+        many, _ = x.replay_many(np.array([t["recorded_inputs"]]), 10_000, 0, 7)
+        assert np.array_equal(many[0], one)
+        with pytest.raises(ValueError):
+            x.replay_many(np.zeros((2, 3)), 10_000, 0, 7)

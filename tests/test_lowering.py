@@ -152,6 +152,11 @@ def test_draw_pairs_share_one_philox_block(rocm, tapes):
         assert fwd.count("nt_normal_pair(") == 7  # 14 draws per segment, two legs per block
 
 
+def tape_plan(src):
+    head = [ln for ln in src.splitlines() if ln.startswith("// nt-plan:")][0]
+    return dict(kv.split("=") for kv in head.split()[2:])
+
+
 def _mode(rocm, flat, **kw):
     head = [ln for ln in rocm.lower(flat, rocm.options(**kw)).splitlines() if ln.startswith("// nt-plan:")][0]
     return dict(kv.split("=") for kv in head.split()[2:])["mode"]
@@ -212,3 +217,23 @@ def test_exp_outside_fast_range_falls_back_per_path(rocm):
         assert np.array_equal(np.isinf(v), np.isinf(ov))
         fast = ~beyond & np.isfinite(ov)
         assert ev[fast].max() <= 1e-12
+
+
+@pytest.mark.parametrize("name,paths", [("C2", 200), ("C4", 64)])
+def test_markets_share_draws_and_match_single_market_bit_for_bit(rocm, tapes, name, paths):
+    """A kernel pricing three input sets per path gives each set exactly the
+    single-market kernel's per-path values, derivatives and sums."""
+    flat = tapes[name]
+    x0 = np.array(flat["recorded_inputs"])
+    sets = np.stack([x0, x0 * 1.01, x0 * 0.97])
+    src = rocm.lower(flat, rocm.options("fp64", markets=3))
+    # the fast pass draws once per path, as a single-market kernel with the same trip length does
+    one = rocm.lower(flat, rocm.options("fp64", mode=2, seg_len=int(tape_plan(src)["seg"])))
+    fast = lambda text: text.split("if (nt_slow")[0].count("nt_normal_pair(")
+    assert fast(src) == fast(one) > 0
+    k = emu.EmulatedKernel(src, len(x0), 0)
+    sums, v, g = k.run(sets, paths, OFFSET, 42, grid=3, block=64, markets=3)
+    for m in range(3):
+        s1, v1, g1 = run_emulated(flat, rocm.options("fp64", mode=2), paths, inputs=sets[m], rocm=rocm)
+        assert np.array_equal(v[m], v1) and np.array_equal(g[m], g1), m
+        assert np.array_equal(sums[m], s1), m
