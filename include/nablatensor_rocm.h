@@ -146,9 +146,10 @@ int nt_exec_create(const nt_tape *tape, const nt_options *options, nt_exec **out
 int nt_exec_set_inputs(nt_exec *exec, const double *inputs, int32_t n);
 
 /* One dispatch over paths [offset, offset + paths) with Philox seed `seed`.
- * sums[0] = sum of the output, sums[1] = sum of its square, sums[2 + j] = sum
- * of the adjoint of input j (zero when built price-only); n_sums must be
- * 2 + n_inputs. timing (nullable) receives {kernel_ms, wall_ms}: kernel_ms from
+ * Per output o, at sums[o * (2 + n_inputs)]: the sum of the output, the sum of
+ * its square, and the sum of its derivative with respect to each input j (zero
+ * when built price-only), the AadTotals fields (AadTotals.java:30-40); n_sums
+ * must be n_outputs * (2 + n_inputs). timing (nullable) receives {kernel_ms, wall_ms}: kernel_ms from
  * HIP events around the replay and finishing kernels on the executable's
  * stream, wall_ms from entry to sums on the host. Replaces
  * DeviceAadExecutable.replay (DeviceAadExecutable.java:139-168), returning raw
@@ -157,7 +158,7 @@ int nt_exec_replay(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed
                    double *sums, int32_t n_sums, double *timing);
 
 /* Prices `markets` input sets (row-major [markets][n_inputs]) over the same paths and seed in one
- * dispatch; sums[m * (2 + n_inputs) + c] as nt_exec_replay's sums for set m. In tangent mode each path's
+ * dispatch; sums[m * n_sums_one + c] as nt_exec_replay's sums (n_sums_one of them) for set m. In tangent mode each path's
  * draws are generated once and shared by the sets in registers (a kernel is compiled per set count on
  * first use); a reverse-sweep executable replays the sets one after another. Either way the sums are
  * bit-identical to `markets` separate nt_exec_replay calls with those inputs. The executable's bound
@@ -168,8 +169,10 @@ int nt_exec_replay_many(nt_exec *exec, const double *input_sets, int32_t markets
                         uint64_t offset, uint64_t seed, double *sums, int32_t n_sums, double *timing);
 
 /* Per-path value and adjoints for paths [offset, offset + paths):
- * values[p] and grads[p * n_inputs + j]. A testing aid with no counterpart in
- * the reference; it runs the same lowered sweep with a per-path store. */
+ * values[p * n_outputs + o] and grads[(p * n_outputs + o) * n_inputs + j]
+ * (values[p] and grads[p * n_inputs + j] for a one-output tape). A testing aid
+ * with no counterpart in the reference; it runs the same lowered sweep with a
+ * per-path store. */
 int nt_exec_replay_paths(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed,
                          double *values, double *grads);
 

@@ -39,14 +39,7 @@ int build_ir(const nt_tape* t, TapeIR& ir, std::string& err) {
     return NT_E_INVALID;
   }
   if (t->n_outputs < 1 || !t->output_node) { err = "no output was recorded"; return NT_E_INVALID; }
-  if (t->n_outputs > 1) {
-    err = "engine 'rocm' does not yet support multi-output tapes; use cpu-jit or cpu for this tape";
-    return NT_E_UNSUPPORTED;
-  }
-  if (t->n_streams > 1 || t->n_uniforms > 0) {
-    err = "engine 'rocm' does not yet support rec.randu() or named random streams; use cpu-jit or cpu for this tape";
-    return NT_E_UNSUPPORTED;
-  }
+  if (t->n_streams < 1) { err = "a tape has at least one random stream"; return NT_E_INVALID; }
   if (t->n_inputs < 0 || (t->n_inputs > 0 && !t->input_node)) { err = "bad input list"; return NT_E_INVALID; }
   const int n = t->n_nodes;
   ir.n = n;
@@ -56,7 +49,10 @@ int build_ir(const nt_tape* t, TapeIR& ir, std::string& err) {
   ir.b.assign(t->arg_b, t->arg_b + n);
   ir.c.assign(t->constant, t->constant + n);
   ir.input_node.assign(t->input_node, t->input_node + t->n_inputs);
-  ir.output = t->output_node[0];
+  ir.outputs.assign(t->output_node, t->output_node + t->n_outputs);
+  ir.output = ir.outputs[0];
+  ir.n_streams = t->n_streams;
+  ir.simple_draws = t->n_streams == 1;
   for (int i = 0; i < n; ++i) {
     const int op = ir.op[i], a = ir.a[i], b = ir.b[i];
     char buf[160];
@@ -65,14 +61,18 @@ int build_ir(const nt_tape* t, TapeIR& ir, std::string& err) {
       err = buf;
       return NT_E_INVALID;
     }
-    if (op == NT_OP_RANDU || (op == NT_OP_RANDN && b != 0)) {
-      err = "engine 'rocm' does not yet support rec.randu() or named random streams; use cpu-jit or cpu for this tape";
-      return NT_E_UNSUPPORTED;
-    }
-    if (op == NT_OP_RANDN && a < 0) {
-      std::snprintf(buf, sizeof buf, "draw node %d has negative ordinal %d", i, a);
-      err = buf;
-      return NT_E_INVALID;
+    if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
+      if (a < 0) {
+        std::snprintf(buf, sizeof buf, "draw node %d has negative ordinal %d", i, a);
+        err = buf;
+        return NT_E_INVALID;
+      }
+      if (b < 0 || b >= t->n_streams) {
+        std::snprintf(buf, sizeof buf, "draw node %d names stream %d of %d", i, b, t->n_streams);
+        err = buf;
+        return NT_E_INVALID;
+      }
+      if (op == NT_OP_RANDU) ir.simple_draws = false;
     }
     if (op == NT_OP_INPUT && (a < 0 || a >= ir.n_in || ir.input_node[a] != i)) {
       std::snprintf(buf, sizeof buf, "input node %d has bad input index %d", i, a);
@@ -93,7 +93,9 @@ int build_ir(const nt_tape* t, TapeIR& ir, std::string& err) {
       return NT_E_INVALID;
     }
   }
-  if (ir.output < 0 || ir.output >= n) { err = "output node out of range"; return NT_E_INVALID; }
+  for (int out : ir.outputs) {
+    if (out < 0 || out >= n) { err = "output node out of range"; return NT_E_INVALID; }
+  }
   ir.active.assign(n, 0);
   for (int i = 0; i < n; ++i) {
     const int op = ir.op[i];
@@ -109,13 +111,23 @@ int build_ir(const nt_tape* t, TapeIR& ir, std::string& err) {
 
 namespace {
 
-// Node k = i + P repeats node i: same op and literal, draw ordinal advanced by D,
+bool is_draw(int op) { return op == NT_OP_RANDN || op == NT_OP_RANDU; }
+
+// A draw k repeating draw i: same kind and stream, ordinal advanced by D (for
+// a tape with one stream of normals) or by any positive step (several streams
+// or uniforms: verify() then checks that each kind and stream advances evenly).
+bool draw_repeats(const TapeIR& t, int i, int k, int D) {
+  if (t.b[i] != t.b[k]) return false;
+  return t.simple_draws ? t.a[k] - t.a[i] == D : t.a[k] > t.a[i];
+}
+
+// Node k = i + P repeats node i: same op and literal, draw ordinal advanced,
 // each operand either shifted by P (same iteration / carried) or unchanged (invariant).
 bool repeats(const TapeIR& t, int i, int k, int P, int D) {
   const int op = t.op[i];
   if (op != t.op[k] || op == NT_OP_INPUT) return false;
   if (op == NT_OP_CONST) return bits(t.c[i]) == bits(t.c[k]);
-  if (op == NT_OP_RANDN) return t.b[i] == t.b[k] && t.a[k] - t.a[i] == D;
+  if (is_draw(op)) return draw_repeats(t, i, k, D);
   const int ar = arity(op);
   if (ar >= 1 && !(t.a[k] == t.a[i] + P || t.a[k] == t.a[i])) return false;
   if (ar >= 2 && !(t.b[k] == t.b[i] + P || t.b[k] == t.b[i])) return false;
@@ -132,7 +144,7 @@ bool extends(const TapeIR& t, int s0, int P, int D) {
     const int op = t.op[i];
     if (op != t.op[k] || op == NT_OP_INPUT) return false;
     if (op == NT_OP_CONST) { if (bits(t.c[i]) != bits(t.c[k])) return false; continue; }
-    if (op == NT_OP_RANDN) { if (t.b[i] != t.b[k] || t.a[k] - t.a[i] != D) return false; continue; }
+    if (is_draw(op)) { if (!draw_repeats(t, i, k, D)) return false; continue; }
     const int ar = arity(op);
     for (int slot = 0; slot < ar; ++slot) {
       const int xk = slot == 0 ? t.a[k] : t.b[k];
@@ -154,6 +166,7 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
   L.kind_a.assign(P, ARG_NONE); L.ref_a.assign(P, -1);
   L.kind_b.assign(P, ARG_NONE); L.ref_b.assign(P, -1);
   L.rand_base.assign(P, -1);
+  L.rand_step.assign(P, 0);
   L.carry_init.assign(P, -1);
   L.is_carry.assign(P, 0);
   L.is_liveout.assign(P, 0);
@@ -172,7 +185,26 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
       (slot == 0 ? L.ref_a : L.ref_b)[j] = ref;
       if (kind == ARG_CARRY) L.is_carry[ref] = 1;
     }
-    if (t.op[s + j] == NT_OP_RANDN) { L.rand_base[j] = t.a[s + j]; if (L.rand_base[j] < 0) return V_FAIL; }
+    if (is_draw(t.op[s + j])) {
+      L.rand_base[j] = t.a[s + j];
+      L.rand_step[j] = t.a[s1 + j] - t.a[s + j];
+      if (L.rand_base[j] < 0 || L.rand_step[j] <= 0 || t.b[s1 + j] != t.b[s + j]) return V_FAIL;
+    }
+  }
+  // every draw of one kind and stream advances by the same step per iteration
+  L.normal_step.clear();
+  L.need_even = false;
+  std::map<std::pair<int, int>, int> step;
+  for (int j = 0; j < P; ++j) {
+    if (!is_draw(t.op[s + j])) continue;
+    const auto key = std::make_pair(t.op[s + j], t.b[s + j]);
+    auto it = step.find(key);
+    if (it == step.end()) step[key] = L.rand_step[j];
+    else if (it->second != L.rand_step[j]) return V_FAIL;
+    if (t.op[s + j] == NT_OP_RANDN) {
+      L.normal_step[t.b[s + j]] = L.rand_step[j];
+      if (L.rand_step[j] & 1) L.need_even = true;
+    }
   }
   for (int it = 0; it < iters; ++it) {
     const int fail = it == 0 ? V_ITER0 : V_FAIL;
@@ -182,7 +214,7 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
       if (op != t.op[s1 + j]) return fail;
       if (op == NT_OP_CONST && bits(t.c[i]) != bits(t.c[s + j])) return fail;
       if (op == NT_OP_INPUT) return fail;
-      if (op == NT_OP_RANDN && (t.b[i] != 0 || t.a[i] != L.rand_base[j] + it * D)) return fail;
+      if (is_draw(op) && (t.b[i] != t.b[s + j] || t.a[i] != L.rand_base[j] + it * L.rand_step[j])) return fail;
       // one body serves every iteration, so activity must not change along the loop
       if (t.active[i] != t.active[s1 + j]) return fail;
       const int ar = arity(op);
@@ -217,9 +249,11 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
       }
     }
   }
-  if (t.output >= s && t.output < e) {
-    if (t.output < last) return V_EPI;
-    L.is_liveout[t.output - last] = 1;
+  for (int out : t.outputs) {
+    if (out >= s && out < e) {
+      if (out < last) return V_EPI;
+      L.is_liveout[out - last] = 1;
+    }
   }
   L.found = true;
   return V_OK;
@@ -230,7 +264,7 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
 LoopPlan detect_loop(const TapeIR& t) {
   std::vector<int> rp;
   for (int i = 0; i < t.n; ++i) {
-    if (t.op[i] == NT_OP_RANDN) rp.push_back(i);
+    if (is_draw(t.op[i])) rp.push_back(i);
   }
   LoopPlan none;
   if (rp.size() < 8) return none;
@@ -263,7 +297,7 @@ LoopPlan detect_loop(const TapeIR& t) {
   const int P = bestP, D = bestD;
   int s = bestX;
   for (int j = 0; j < P && bestX + j < t.n; ++j) {
-    if (t.op[bestX + j] == NT_OP_RANDN) { s = bestX + j; break; }
+    if (is_draw(t.op[bestX + j])) { s = bestX + j; break; }
   }
   int iters = (bestY + P - s) / P;
   while (s - P >= 0 && extends(t, s - P, P, D)) { s -= P; ++iters; }
@@ -302,7 +336,7 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   p.libm = (o.libm == 1 || o.libm == 2) ? o.libm : 0;
   p.block = o.block > 0 ? o.block : 256;
   if (p.block % 64 != 0 || p.block > 1024) { err = "block must be a multiple of 64, at most 1024"; return NT_E_INVALID; }
-  p.n_channels = 2 + t.n_in;
+  p.n_channels = static_cast<int>(t.outputs.size()) * (2 + t.n_in);
   if (o.checkpoint < NT_CKPT_AUTO || o.checkpoint > NT_CKPT_STORE_ALL) { err = "unknown checkpoint policy"; return NT_E_INVALID; }
   if (o.seg_len < 0) { err = "seg_len must be >= 0"; return NT_E_INVALID; }
   if (o.mode < NT_MODE_AUTO || o.mode > NT_MODE_TANGENT) { err = "unknown derivative mode"; return NT_E_INVALID; }
@@ -311,6 +345,10 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   if (p.markets > 1 && o.mode == NT_MODE_REVERSE) {
     err = "several markets per dispatch share draws in tangent mode only";
     return NT_E_INVALID;
+  }
+  if (t.outputs.size() > 1 && o.mode == NT_MODE_REVERSE && o.adjoints) {
+    err = "the reverse sweep follows one output; a multi-output tape takes tangent mode";
+    return NT_E_UNSUPPORTED;
   }
   if (o.roll >= 0) p.loop = detect_loop(t);
   if (p.loop.found) {
@@ -419,15 +457,15 @@ int plan_reverse_loop(const TapeIR& t, const nt_options& o, Plan& p, std::string
     seg = std::max(1, 96 / std::max(1, taped * w));
   }
   seg = std::max(1, std::min({seg, L.iters, 64}));
-  if ((L.draws & 1) && (seg & 1)) seg = seg > 1 ? seg - 1 : 2;
+  if (L.need_even && (seg & 1)) seg = seg > 1 ? seg - 1 : 2;
   seg = std::min(seg, L.iters);
   if (o.seg_len <= 0) {
     for (int cand = seg; cand >= std::max(1, seg / 2); --cand) {
-      if (L.iters % cand == 0 && (!(L.draws & 1) || !(cand & 1))) { seg = cand; break; }
+      if (L.iters % cand == 0 && (!L.need_even || !(cand & 1))) { seg = cand; break; }
     }
   }
-  if ((L.draws & 1) && (seg & 1)) {
-    err = "an odd seg_len needs an even number of draws per iteration";
+  if (L.need_even && (seg & 1)) {
+    err = "an odd seg_len needs an even number of normal draws per iteration in every stream";
     return NT_E_INVALID;
   }
   p.seg = seg;
@@ -486,6 +524,7 @@ double fwd_cost(int op, bool f32) {
     case NT_OP_EXP: case NT_OP_LOG: return 20;
     case NT_OP_SQRT: return 8;
     case NT_OP_RANDN: return f32 ? 15 : 30;  // half a Box-Muller pair with its Philox block
+    case NT_OP_RANDU: return 12;             // one Philox block
     default: return 0;
   }
 }
@@ -544,7 +583,8 @@ double tan_cost(const TapeIR& t, const Plan& p, int i) {
 
 void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.mode = NT_MODE_REVERSE;
-  if (!p.adjoints && p.markets == 1) return;
+  const bool multi = t.outputs.size() > 1;
+  if (!p.adjoints && p.markets == 1 && !multi) return;
   compute_deps(t, p);
   const LoopPlan& L = p.loop;
   const int le = L.found ? L.end() : 0;
@@ -566,7 +606,10 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.cost_tangent = tan;
   // Several markets per dispatch are priced in tangent mode (also price-only:
   // the tangent frame without tangents).
-  const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || (p.adjoints && o.mode == NT_MODE_AUTO && tan < rev);
+  // Several outputs get their Jacobian rows from one tangent sweep (the
+  // reverse sweep here follows one output).
+  const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || multi ||
+                       (p.adjoints && o.mode == NT_MODE_AUTO && tan < rev);
   if (!tangent) return;
   p.mode = NT_MODE_TANGENT;
   p.ckpt = 0;
@@ -590,7 +633,7 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   const int w = p.precision == NT_FP64 ? 2 : 1;
   const int regs = live * w * p.markets;
   int seg = o.seg_len > 0 ? o.seg_len : (regs <= 32 ? 4 : regs <= 64 ? 2 : 1);
-  if ((L.draws & 1) && (seg & 1)) seg += 1;
+  if (L.need_even && (seg & 1)) seg += 1;
   seg = std::max(1, std::min(seg, L.iters));
   p.seg = seg;
   p.nseg_full = L.iters / seg;
@@ -615,7 +658,15 @@ class Emitter {
   const bool f32_;
   const LoopPlan& L_;
   std::ostringstream o_;
-  std::map<int, std::string> pairs_;  // counter -> pair variable stem, per straight-line region
+  // (stream, Philox counter) -> pair variable stem, per straight-line region
+  std::map<std::pair<int, int>, std::string> pairs_;
+
+  // Counter high word of a stream: the path's for stream 0, xor s * 0x9E3779B1
+  // for stream s (Philox.java:44-52); declared once per path.
+  static std::string rhi(int stream) { return stream == 0 ? std::string("rhi") : "rhi" + std::to_string(stream); }
+  std::string uniform_call(int stream, const std::string& ordinal) const {
+    return std::string(f32_ ? "nt_uniformf" : "nt_uniform") + "(rlo, " + rhi(stream) + ", " + ordinal + ")";
+  }
 
   std::string lit(double v) const {
     char buf[64];
@@ -717,6 +768,8 @@ class Emitter {
   std::string vname(int node) const;        // forward value of a straight-line node or live-out
   std::string dname(int node) const;        // adjoint of an active straight-line node or live-out
   void line_draw(int lo, int i);
+  void trip_counters(const std::string& ind);
+  std::string body_draw(int u, int j, std::map<std::pair<int, int>, std::string>& pairs, const std::string& ind);
   void line_forward(int lo, int hi);
   void line_reverse(int lo, int hi);
 
@@ -793,25 +846,66 @@ std::string Emitter::dname(int node) const {
 // nt_normal_pair call (pairs_ is per region, `lo` keeps the names unique).
 void Emitter::line_draw(int lo, int i) {
   const int k = t_.a[i];
+  const int stream = t_.b[i];
+  if (t_.op[i] == NT_OP_RANDU) {
+    o_ << "    const real v" << i << " = " << uniform_call(stream, std::to_string(k) + "u") << ";\n";
+    return;
+  }
   const int ctr = k >> 1;
-  auto it = pairs_.find(ctr);
+  auto it = pairs_.find({stream, ctr});
   std::string stem;
   if (it == pairs_.end()) {
-    stem = "zl" + std::to_string(lo) + "_" + std::to_string(ctr);
+    stem = "zl" + std::to_string(lo) + "_" + std::to_string(stream) + "_" + std::to_string(ctr);
     o_ << "    real " << stem << "c, " << stem << "s;\n";
-    o_ << "    nt_normal_pair(rlo, rhi, " << ctr << "u, " << stem << "c, " << stem << "s);\n";
-    pairs_[ctr] = stem;
+    o_ << "    nt_normal_pair(rlo, " << rhi(stream) << ", " << ctr << "u, " << stem << "c, " << stem << "s);\n";
+    pairs_[{stream, ctr}] = stem;
   } else {
     stem = it->second;
   }
   o_ << "    const real v" << i << " = " << stem << ((k & 1) ? "s" : "c") << ";\n";
 }
 
+// Per-trip draw counters: normals of stream s in this trip start at ordinal
+// it0 * step_s (even, since the trip length times an odd step is even).
+void Emitter::trip_counters(const std::string& ind) {
+  for (const auto& kv : L_.normal_step) {
+    o_ << ind << "const nt_u32 kb" << kv.first << " = it0 * " << kv.second << "u;\n";
+  }
+}
+
+// Value of loop draw position j in iteration u of a trip: both legs of a
+// normal pair come from one nt_normal_pair call (pairs keyed by stream and
+// counter within the trip); a uniform is one Philox block.
+std::string Emitter::body_draw(int u, int j, std::map<std::pair<int, int>, std::string>& pairs,
+                               const std::string& ind) {
+  const int i = L_.start + j;
+  const int stream = t_.b[i];
+  const int step = L_.rand_step[j];
+  if (t_.op[i] == NT_OP_RANDU) {
+    return uniform_call(stream, "(it0 + " + std::to_string(u) + "u) * " + std::to_string(step) + "u + " +
+                                    std::to_string(L_.rand_base[j]) + "u");
+  }
+  const int rel = L_.rand_base[j] + u * step;
+  const int key = rel >> 1;
+  auto it = pairs.find({stream, key});
+  std::string stem;
+  if (it == pairs.end()) {
+    stem = "zp" + std::to_string(stream) + "_" + std::to_string(key);
+    o_ << ind << "real " << stem << "c, " << stem << "s;\n";
+    o_ << ind << "nt_normal_pair(rlo, " << rhi(stream) << ", (kb" << stream << " >> 1) + " << key << "u, " << stem << "c, "
+       << stem << "s);\n";
+    pairs[{stream, key}] = stem;
+  } else {
+    stem = it->second;
+  }
+  return stem + ((rel & 1) ? "s" : "c");
+}
+
 void Emitter::line_forward(int lo, int hi) {
   pairs_.clear();
   for (int i = lo; i < hi; ++i) {
     const int op = t_.op[i];
-    if (op == NT_OP_RANDN) {
+    if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
       line_draw(lo, i);
       continue;
     }
@@ -852,12 +946,12 @@ std::string Emitter::body_value(int u, int kind, int ref, bool recompute) const 
 // the iteration base is it0 = sg * SEG. forward: compute, store, advance the
 // state. !forward: recompute (reloading stored values), then reverse.
 void Emitter::segment(int U, const std::string& sg, bool forward) {
-  const int P = L_.period, s = L_.start, D = L_.draws;
+  const int P = L_.period, s = L_.start;
   const int NC = static_cast<int>(p_.carries.size());
   const std::string ind = "      ";
   o_ << "    {\n";
   o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << p_.seg << "u;\n";
-  o_ << ind << "const nt_u32 kb = it0 * " << D << "u;\n";
+  trip_counters(ind);
   const bool ckpt = p_.adjoints;
   if (forward && ckpt) {
     for (int ci = 0; ci < NC; ++ci) {
@@ -871,8 +965,8 @@ void Emitter::segment(int U, const std::string& sg, bool forward) {
          << "u) * T + tid];\n";
     }
   }
-  // draws of this segment by relative ordinal, for pairing the two legs
-  std::map<int, std::string> pairs;
+  // draws of this segment by stream and relative counter, for pairing the two legs
+  std::map<std::pair<int, int>, std::string> pairs;
   for (int u = 0; u < U; ++u) {
     for (int j = 0; j < P; ++j) {
       const int i = s + j;
@@ -885,20 +979,9 @@ void Emitter::segment(int U, const std::string& sg, bool forward) {
         o_ << ind << "const real " << name << " = scratch[" << slot << "];\n";
         continue;
       }
-      if (op == NT_OP_RANDN) {
-        const int rel = L_.rand_base[j] + u * D;
-        const int key = rel >> 1;
-        auto it = pairs.find(key);
-        std::string stem;
-        if (it == pairs.end()) {
-          stem = "zp" + std::to_string(key);
-          o_ << ind << "real " << stem << "c, " << stem << "s;\n";
-          o_ << ind << "nt_normal_pair(rlo, rhi, (kb >> 1) + " << key << "u, " << stem << "c, " << stem << "s);\n";
-          pairs[key] = stem;
-        } else {
-          stem = it->second;
-        }
-        o_ << ind << "const real " << name << " = " << stem << ((rel & 1) ? "s" : "c") << ";\n";
+      if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
+        const std::string d = body_draw(u, j, pairs, ind);
+        o_ << ind << "const real " << name << " = " << d << ";\n";
       } else {
         const int ar = arity(op);
         const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], !forward) : "";
@@ -1044,7 +1127,7 @@ void Emitter::tline(int lo, int hi) {
   pairs_.clear();
   for (int i = lo; i < hi; ++i) {
     const int op = t_.op[i];
-    if (op == NT_OP_RANDN) {
+    if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
       line_draw(lo, i);  // a draw is never active: one per path, shared by the markets
       continue;
     }
@@ -1087,31 +1170,20 @@ void Emitter::body_tangent_operand(int u, int kind, int ref, std::function<std::
 // One trip of U loop iterations: values and their tangents, then the carried
 // state (values and tangents) advances.
 void Emitter::tsegment(int U, const std::string& sg) {
-  const int P = L_.period, s = L_.start, D = L_.draws;
+  const int P = L_.period, s = L_.start;
   const std::string ind = "      ";
   o_ << "    {\n";
   o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << p_.seg << "u;\n";
-  o_ << ind << "const nt_u32 kb = it0 * " << D << "u;\n";
-  std::map<int, std::string> pairs;
+  trip_counters(ind);
+  std::map<std::pair<int, int>, std::string> pairs;
   for (int u = 0; u < U; ++u) {
     for (int j = 0; j < P; ++j) {
       const int i = s + j;
       const int op = t_.op[i];
       const std::string name = "r" + std::to_string(u) + "_" + std::to_string(j);
-      if (op == NT_OP_RANDN) {
-        const int rel = L_.rand_base[j] + u * D;
-        const int key = rel >> 1;
-        auto it = pairs.find(key);
-        std::string stem;
-        if (it == pairs.end()) {
-          stem = "zp" + std::to_string(key);
-          o_ << ind << "real " << stem << "c, " << stem << "s;\n";
-          o_ << ind << "nt_normal_pair(rlo, rhi, (kb >> 1) + " << key << "u, " << stem << "c, " << stem << "s);\n";
-          pairs[key] = stem;
-        } else {
-          stem = it->second;
-        }
-        o_ << ind << "const real " << name << " = " << stem << ((rel & 1) ? "s" : "c") << ";\n";
+      if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
+        const std::string d = body_draw(u, j, pairs, ind);
+        o_ << ind << "const real " << name << " = " << d << ";\n";
         continue;
       }
       const int ar = arity(op);
@@ -1197,6 +1269,12 @@ void Emitter::header() {
   o_ << "    const nt_u64 path = p + path_offset;\n";
   o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
   o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
+  for (int st = 1; st < t_.n_streams; ++st) {
+    const uint32_t mult = static_cast<uint32_t>(st) * 0x9E3779B1u;
+    char buf[96];
+    std::snprintf(buf, sizeof buf, "    const nt_u32 rhi%d = rhi ^ 0x%08Xu;\n", st, mult);
+    o_ << buf;
+  }
 }
 
 // Values and tangents of one path; leaves the output in nt_y and its
@@ -1232,14 +1310,18 @@ void Emitter::body_tangent() {
     if (p_.tail) tsegment(p_.tail, std::to_string(p_.nseg_full) + "u");
     tline(le, n);
   }
+  const int nin = t_.n_in;
   for (int m = mlo_; m < mhi_; ++m) {
     m_ = m;
-    o_ << "    nt_y" << msuf(m) << " = (double)" << vname(t_.output) << ";\n";
-    if (!p_.adjoints) continue;
-    for (int j = 0; j < t_.n_in; ++j) {
-      const std::string g = tname(t_.output, j);
-      o_ << "    nt_g" << msuf(m) << "[" << j << "] = "
-         << (g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g) << ";\n";
+    for (size_t o = 0; o < t_.outputs.size(); ++o) {
+      const int out = t_.outputs[o];
+      o_ << "    nt_y" << msuf(m) << "[" << o << "] = (double)" << vname(out) << ";\n";
+      if (!p_.adjoints) continue;
+      for (int j = 0; j < nin; ++j) {
+        const std::string g = tname(out, j);
+        o_ << "    nt_g" << msuf(m) << "[" << o * nin + j << "] = "
+           << (g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g) << ";\n";
+      }
     }
   }
 }
@@ -1265,7 +1347,7 @@ void Emitter::body_reverse() {
     if (p_.tail) segment(p_.tail, std::to_string(p_.nseg_full) + "u", true);
     line_forward(le, n);
   }
-  o_ << "    nt_y = (double)" << vname(t_.output) << ";\n";
+  o_ << "    nt_y[0] = (double)" << vname(t_.output) << ";\n";
   if (!p_.adjoints) return;
   const std::string zero = f32_ ? "0.0f" : "0.0";
   const std::string one = f32_ ? "1.0f" : "1.0";
@@ -1313,9 +1395,10 @@ std::string Emitter::run() {
   // basic block per loop trip.
   const bool fallback = exp_fallback();
   const int M = p_.markets;
+  const int O = static_cast<int>(t_.outputs.size());
   for (int m = 0; m < M; ++m) {
-    o_ << "    double nt_y" << msuf(m) << ";\n";
-    if (p_.adjoints && nin > 0) o_ << "    double nt_g" << msuf(m) << "[" << nin << "];\n";
+    o_ << "    double nt_y" << msuf(m) << "[" << O << "];\n";
+    if (p_.adjoints && nin > 0) o_ << "    double nt_g" << msuf(m) << "[" << O * nin << "];\n";
   }
   if (fallback) {
     o_ << "    bool nt_slow = false;\n";  // an exponent shared by every market
@@ -1342,20 +1425,28 @@ std::string Emitter::run() {
     mlo_ = 0;
     mhi_ = M;
   }
+  // channels: [market][output][value, value^2, derivative per input]
   for (int m = 0; m < M; ++m) {
-    const std::string y = "nt_y" + msuf(m);
-    o_ << "    acc[" << m * NCH << "] += " << y << ";\n    acc[" << m * NCH + 1 << "] += " << y << " * " << y << ";\n";
-    if (p_.adjoints) {
-      for (int j = 0; j < nin; ++j) o_ << "    acc[" << m * NCH + 2 + j << "] += nt_g" << msuf(m) << "[" << j << "];\n";
+    for (int o = 0; o < O; ++o) {
+      const int base = m * NCH + o * (2 + nin);
+      const std::string y = "nt_y" + msuf(m) + "[" + std::to_string(o) + "]";
+      o_ << "    acc[" << base << "] += " << y << ";\n    acc[" << base + 1 << "] += " << y << " * " << y << ";\n";
+      if (!p_.adjoints) continue;
+      for (int j = 0; j < nin; ++j) {
+        o_ << "    acc[" << base + 2 + j << "] += nt_g" << msuf(m) << "[" << o * nin + j << "];\n";
+      }
     }
   }
-  o_ << "#ifdef NT_DUMP_PATHS\n";
+  o_ << "#ifdef NT_DUMP_PATHS\n";  // rows [market][path][output], as the oracle's per-path rows
   for (int m = 0; m < M; ++m) {
-    const std::string row = M > 1 ? "(" + std::to_string(m) + "u * n_paths + p)" : std::string("p");
-    o_ << "    out_v[" << row << "] = nt_y" << msuf(m) << ";\n";
-    for (int j = 0; j < nin; ++j) {
-      o_ << "    out_g[" << row << " * " << nin << "u + " << j << "u] = "
-         << (p_.adjoints ? "nt_g" + msuf(m) + "[" + std::to_string(j) + "]" : std::string("0.0")) << ";\n";
+    const std::string path_row = M > 1 ? "(" + std::to_string(m) + "u * n_paths + p)" : std::string("p");
+    for (int o = 0; o < O; ++o) {
+      const std::string row = O > 1 ? "(" + path_row + " * " + std::to_string(O) + "u + " + std::to_string(o) + "u)" : path_row;
+      o_ << "    out_v[" << row << "] = nt_y" << msuf(m) << "[" << o << "];\n";
+      for (int j = 0; j < nin; ++j) {
+        o_ << "    out_g[" << row << " * " << nin << "u + " << j << "u] = "
+           << (p_.adjoints ? "nt_g" + msuf(m) + "[" + std::to_string(o * nin + j) + "]" : std::string("0.0")) << ";\n";
+      }
     }
   }
   o_ << "#endif\n";

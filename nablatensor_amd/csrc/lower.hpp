@@ -23,6 +23,7 @@
 #pragma once
 
 #include <cstdint>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -32,7 +33,10 @@ namespace ntl {
 
 // Validated copy of a tape with activity (AadTape.markActive, AadTape.java:70-81).
 struct TapeIR {
-  int n = 0, n_in = 0, output = -1;
+  int n = 0, n_in = 0, output = -1;  // output: the first (primary) output node
+  std::vector<int> outputs;          // every output node, in output order
+  int n_streams = 1;
+  bool simple_draws = true;          // one stream and no uniform draws
   std::vector<int32_t> op, a, b;
   std::vector<double> c;
   std::vector<int32_t> input_node;
@@ -45,10 +49,13 @@ enum { ARG_NONE = 0, ARG_BODY = 1, ARG_CARRY = 2, ARG_INV = 3 };
 struct LoopPlan {
   bool found = false;
   int start = 0, period = 0, iters = 0;
-  int draws = 0;                      // RANDN nodes per iteration
+  int draws = 0;                      // draw nodes per iteration (normals and uniforms)
   std::vector<int> kind_a, ref_a;     // per body position
   std::vector<int> kind_b, ref_b;
-  std::vector<int> rand_base;         // RANDN ordinal in iteration 0, -1 otherwise
+  std::vector<int> rand_base;         // draw ordinal in iteration 0, -1 otherwise
+  std::vector<int> rand_step;         // draw ordinal advance per iteration, 0 otherwise
+  std::map<int, int> normal_step;     // stream -> normals drawn per iteration
+  bool need_even = false;             // some stream draws an odd number of normals per iteration
   std::vector<int> carry_init;        // init node of a carried position, -1 otherwise
   std::vector<uint8_t> is_carry;      // read as carry-in by the next iteration
   std::vector<uint8_t> is_liveout;    // read by the epilogue from the last iteration

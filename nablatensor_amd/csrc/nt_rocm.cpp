@@ -461,7 +461,7 @@ int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, d
   if (!x) return fail(NT_E_CLOSED, "executable is closed");
   if (paths == 0) return fail(NT_E_INVALID, "paths must be positive");
   const int nch = x->low.plan.n_channels;
-  if (!sums || n_sums != nch) return fail(NT_E_INVALID, "sums must hold 2 + n_inputs doubles");
+  if (!sums || n_sums != nch) return fail(NT_E_INVALID, "sums must hold n_outputs * (2 + n_inputs) doubles");
   const auto t0 = std::chrono::steady_clock::now();
   NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
   NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");
@@ -566,7 +566,9 @@ int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, u
   const int nin = x->low.ir.n_in;
   const int nch = x->low.plan.n_channels;
   if (nin > 0 && !input_sets) return fail(NT_E_INVALID, "input_sets is null");
-  if (!sums || n_sums != nch * markets) return fail(NT_E_INVALID, "sums must hold markets * (2 + n_inputs) doubles");
+  if (!sums || n_sums != nch * markets) {
+    return fail(NT_E_INVALID, "sums must hold markets * n_outputs * (2 + n_inputs) doubles");
+  }
   const auto t0 = std::chrono::steady_clock::now();
   NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
   const bool shared = x->low.plan.mode == NT_MODE_TANGENT;
@@ -648,10 +650,11 @@ int nt_exec_replay_paths(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t s
     NT_HIP(hipModuleLoadData(&x->mod_dump, code.data()), "hipModuleLoadData(dump)");
     NT_HIP(hipModuleGetFunction(&x->fn_dump, x->mod_dump, "nt_replay"), "hipModuleGetFunction(dump)");
   }
+  const uint64_t rows = paths * static_cast<uint64_t>(x->low.ir.outputs.size());
   double* d_v = nullptr;
   double* d_g = nullptr;
-  NT_HIP(hipMalloc(&d_v, sizeof(double) * paths), "hipMalloc(values)");
-  hipError_t e = hipMalloc(&d_g, sizeof(double) * paths * static_cast<uint64_t>(std::max(1, nin)));
+  NT_HIP(hipMalloc(&d_v, sizeof(double) * rows), "hipMalloc(values)");
+  hipError_t e = hipMalloc(&d_g, sizeof(double) * rows * static_cast<uint64_t>(std::max(1, nin)));
   if (e != hipSuccess) {
     (void)hipFree(d_v);
     return hip_fail(e, "hipMalloc(grads)");
@@ -659,9 +662,9 @@ int nt_exec_replay_paths(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t s
   int grid = 0;
   int rc = launch_replay(x, x->fn_dump, paths, offset, seed, d_v, d_g, grid);
   if (rc == NT_OK) {
-    e = hipMemcpyAsync(values, d_v, sizeof(double) * paths, hipMemcpyDeviceToHost, x->stream);
+    e = hipMemcpyAsync(values, d_v, sizeof(double) * rows, hipMemcpyDeviceToHost, x->stream);
     if (e == hipSuccess && nin > 0) {
-      e = hipMemcpyAsync(grads, d_g, sizeof(double) * paths * nin, hipMemcpyDeviceToHost, x->stream);
+      e = hipMemcpyAsync(grads, d_g, sizeof(double) * rows * nin, hipMemcpyDeviceToHost, x->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(x->stream);
     if (e != hipSuccess) rc = hip_fail(e, "replay_paths copy-back");

@@ -190,6 +190,19 @@ __device__ __forceinline__ void nt_tables_load() {}
 __device__ __forceinline__ double nt_exp(double x) { return exp(x); }
 #endif
 
+// The k-th uniform of a stream whose counter words are (lo, hi): the Philox
+// block at counter (lo, hi ^ (k | 2^30)) (the tag keeps uniforms and normals
+// on disjoint counters), u = (c0 + 0.5) 2^-32 (Philox.java:81-94). fp32 rounds
+// the double uniform once, as the fp32 oracle does.
+__device__ __forceinline__ double nt_uniform(nt_u32 lo, nt_u32 hi, nt_u32 k) {
+  nt_u32 c0, c1;
+  nt_philox(lo, hi ^ (k | 0x40000000u), c0, c1);
+  return fma(static_cast<double>(c0), 0x1p-32, 0x1p-33);
+}
+__device__ __forceinline__ float nt_uniformf(nt_u32 lo, nt_u32 hi, nt_u32 k) {
+  return static_cast<float>(nt_uniform(lo, hi, k));
+}
+
 // Both legs of the Box-Muller pair for Philox counter `ctr` of a path whose
 // counter words are (lo, hi): u = (c + 0.5) * 2^-32, r = sqrt(-2 log u1),
 // z = r cos(2 pi u2) for even draws and r sin(2 pi u2) for odd ones. With

@@ -279,10 +279,16 @@ PYBIND11_MODULE(_host, m) {
       .def("engineOptions", &AadOptions::engineOptions);
 
   py::class_<AadResult>(m, "AadResult")
-      .def("value", &AadResult::value)
-      .def("standardError", &AadResult::standardError)
-      .def("gradients", &AadResult::gradients)
-      .def("gradient", &AadResult::gradient)
+      .def("value", py::overload_cast<>(&AadResult::value, py::const_))
+      .def("standardError", py::overload_cast<>(&AadResult::standardError, py::const_))
+      .def("gradients", py::overload_cast<>(&AadResult::gradients, py::const_))
+      .def("gradients", py::overload_cast<const std::string&>(&AadResult::gradients, py::const_))
+      .def("gradient", py::overload_cast<const std::string&>(&AadResult::gradient, py::const_))
+      .def("gradient", py::overload_cast<const std::string&, const std::string&>(&AadResult::gradient, py::const_))
+      .def("outputNames", &AadResult::outputNames)
+      .def("outputCount", &AadResult::outputCount)
+      .def("valueOf", py::overload_cast<const std::string&>(&AadResult::value, py::const_))
+      .def("standardErrorOf", py::overload_cast<const std::string&>(&AadResult::standardError, py::const_))
       .def("inputNames", &AadResult::inputNames)
       .def("paths", &AadResult::paths)
       .def("seconds", &AadResult::seconds)
@@ -297,6 +303,8 @@ PYBIND11_MODULE(_host, m) {
       .def("setInput", &AadExecutable::setInput)
       .def("replay", &AadExecutable::replay, py::arg("paths"), py::arg("pathOffset"), py::arg("seed"),
            py::call_guard<py::gil_scoped_release>())
+      .def("replayMany", &AadExecutable::replayMany, py::arg("inputSets"), py::arg("paths"), py::arg("pathOffset"),
+           py::arg("seed"), py::call_guard<py::gil_scoped_release>())
       .def("replaySafe", &AadExecutable::replaySafe, py::call_guard<py::gil_scoped_release>())
       .def("calibrate", &AadExecutable::calibrate, py::call_guard<py::gil_scoped_release>())
       .def("measuredPathsPerSecond", &AadExecutable::measuredPathsPerSecond)

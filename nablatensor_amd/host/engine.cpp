@@ -19,7 +19,27 @@ namespace nablatensor {
 AadResult::AadResult(double value, double standardError, std::vector<double> gradients,
                      std::vector<std::string> inputNames, long long paths, double seconds)
     : value_(value), stderr_(standardError), gradients_(std::move(gradients)), input_names_(std::move(inputNames)),
-      paths_(paths), seconds_(seconds) {}
+      paths_(paths), seconds_(seconds) {
+  output_names_ = {"value"};
+  values_ = {value_};
+  stderrs_ = {stderr_};
+  jacobian_ = {gradients_};
+}
+
+int AadResult::outputIndex(const std::string& outputName) const {
+  for (size_t o = 0; o < output_names_.size(); ++o) {
+    if (output_names_[o] == outputName) return static_cast<int>(o);
+  }
+  throw std::invalid_argument("unknown output: " + outputName);
+}
+
+double AadResult::gradient(const std::string& outputName, const std::string& inputName) const {
+  const auto& row = jacobian_.at(outputIndex(outputName));
+  for (size_t i = 0; i < input_names_.size(); ++i) {
+    if (input_names_[i] == inputName) return row.at(i);
+  }
+  throw std::invalid_argument("unknown input: " + inputName);
+}
 
 double AadResult::gradient(const std::string& inputName) const {
   for (size_t i = 0; i < input_names_.size(); ++i) {
@@ -35,18 +55,29 @@ std::string AadResult::toString() const {
 }
 
 // mean, stderr = sqrt(max(0, (sum y^2 - n mean^2) / (n - 1)) / n), mean adjoints.
-AadResult AadResult::fromSums(const std::vector<double>& sums, const std::vector<std::string>& inputNames,
-                              long long paths, double seconds, double kernelSeconds) {
+AadResult AadResult::fromSums(const std::vector<double>& sums, const std::vector<std::string>& outputNames,
+                              const std::vector<std::string>& inputNames, long long paths, double seconds,
+                              double kernelSeconds) {
   const double n = static_cast<double>(paths);
-  const double mean = sums.at(0) / n;
-  double se = std::nan("");
-  if (paths > 1) {
-    const double variance = (sums.at(1) - n * mean * mean) / (n - 1.0);
-    se = std::sqrt(std::max(0.0, variance) / n);
+  const size_t ni = inputNames.size();
+  const size_t no = std::max<size_t>(1, outputNames.size());
+  std::vector<double> means(no), ses(no);
+  std::vector<std::vector<double>> rows(no, std::vector<double>(ni));
+  for (size_t o = 0; o < no; ++o) {
+    const size_t b = o * (2 + ni);
+    means[o] = sums.at(b) / n;
+    ses[o] = std::nan("");
+    if (paths > 1) {
+      const double variance = (sums.at(b + 1) - n * means[o] * means[o]) / (n - 1.0);
+      ses[o] = std::sqrt(std::max(0.0, variance) / n);
+    }
+    for (size_t j = 0; j < ni; ++j) rows[o][j] = sums.at(b + 2 + j) / n;
   }
-  std::vector<double> g(inputNames.size());
-  for (size_t j = 0; j < g.size(); ++j) g[j] = sums.at(2 + j) / n;
-  AadResult r(mean, se, g, inputNames, paths, seconds);
+  AadResult r(means[0], ses[0], rows[0], inputNames, paths, seconds);
+  if (!outputNames.empty()) r.output_names_ = outputNames;
+  r.values_ = means;
+  r.stderrs_ = ses;
+  r.jacobian_ = rows;
   r.raw_ = sums;
   r.kernel_seconds_ = kernelSeconds;
   return r;
@@ -104,11 +135,31 @@ double AadExecutable::calibrate(long long seed) {
 // Chunks of rate * budget paths. Dispatches that carry raw sums are combined
 // exactly; otherwise the reference's mean * n recombination
 // (AadResultAccumulator.java:52-96) is used.
+std::vector<AadResult> AadExecutable::replayMany(const std::vector<std::vector<double>>& inputSets, long long paths,
+                                                long long pathOffset, long long seed) {
+  checkOpen();
+  if (inputSets.empty()) throw std::invalid_argument("at least one input set is required");
+  const std::vector<double> saved = inputs_;
+  const auto& names = tape().inputNames();
+  std::vector<AadResult> out;
+  for (size_t m = 0; m < inputSets.size(); ++m) {
+    if (inputSets[m].size() != names.size()) {
+      throw std::invalid_argument("input set " + std::to_string(m) + " has " + std::to_string(inputSets[m].size()) +
+                                  " values; the tape has " + std::to_string(names.size()) + " inputs");
+    }
+    for (size_t j = 0; j < names.size(); ++j) setInput(names[j], inputSets[m][j]);
+    out.push_back(replay(paths, pathOffset, seed));
+  }
+  for (size_t j = 0; j < names.size(); ++j) setInput(names[j], saved[j]);
+  return out;
+}
+
 AadResult AadExecutable::replaySafe(long long totalPaths, long long seed) {
   if (totalPaths <= 0) throw std::invalid_argument("paths must be positive");
   if (paths_per_second_ <= 0.0) calibrate(seed);
   const size_t ni = tape_->inputNames().size();
-  std::vector<double> sums(2 + ni, 0.0);
+  const size_t no = static_cast<size_t>(tape_->outputCount());
+  std::vector<double> sums(no * (2 + ni), 0.0);
   bool exact = true;
   double seconds = 0.0, kernel = 0.0;
   long long done = 0;
@@ -120,19 +171,25 @@ AadResult AadExecutable::replaySafe(long long totalPaths, long long seed) {
     if (exact && part.rawSums().size() == sums.size()) {
       for (size_t c = 0; c < sums.size(); ++c) sums[c] += part.rawSums()[c];
     } else {
+      // AadResultAccumulator's mean * n reconstruction (AadResultAccumulator.java:52-96)
       exact = false;
       const double n = static_cast<double>(chunk);
-      sums[0] += part.value() * n;
-      const double se = part.standardError();
-      const double variance = se * se * n;
-      const double denom = chunk > 1 ? n - 1.0 : n;
-      sums[1] += std::isnan(se) ? std::nan("") : denom * variance + n * part.value() * part.value();
-      for (size_t j = 0; j < ni; ++j) sums[2 + j] += part.gradients()[j] * n;
+      const auto& names = part.outputNames();
+      for (size_t o = 0; o < no && o < names.size(); ++o) {
+        const size_t b = o * (2 + ni);
+        const double v = part.value(names[o]);
+        sums[b] += v * n;
+        const double se = part.standardError(names[o]);
+        const double variance = se * se * n;
+        const double denom = chunk > 1 ? n - 1.0 : n;
+        sums[b + 1] += std::isnan(se) ? std::nan("") : denom * variance + n * v * v;
+        for (size_t j = 0; j < ni; ++j) sums[b + 2 + j] += part.gradients(names[o])[j] * n;
+      }
     }
     observe(chunk, part.seconds());
     done += chunk;
   }
-  return AadResult::fromSums(sums, tape_->inputNames(), totalPaths, seconds, kernel);
+  return AadResult::fromSums(sums, tape_->outputNames(), tape_->inputNames(), totalPaths, seconds, kernel);
 }
 
 // ---- engine selection (AadEngine.java:56-86, AadEngines.java:41-110) ----------------
@@ -240,6 +297,7 @@ struct RocmAbi {
   decltype(&nt_exec_create) create = nullptr;
   decltype(&nt_exec_set_inputs) set_inputs = nullptr;
   decltype(&nt_exec_replay) replay = nullptr;
+  decltype(&nt_exec_replay_many) replay_many = nullptr;
   decltype(&nt_exec_info_get) info = nullptr;
   decltype(&nt_exec_source) source = nullptr;
   decltype(&nt_exec_destroy) destroy = nullptr;
@@ -279,6 +337,7 @@ const RocmAbi& abi() {
     a.create = reinterpret_cast<decltype(a.create)>(sym("nt_exec_create"));
     a.set_inputs = reinterpret_cast<decltype(a.set_inputs)>(sym("nt_exec_set_inputs"));
     a.replay = reinterpret_cast<decltype(a.replay)>(sym("nt_exec_replay"));
+    a.replay_many = reinterpret_cast<decltype(a.replay_many)>(sym("nt_exec_replay_many"));
     a.info = reinterpret_cast<decltype(a.info)>(sym("nt_exec_info_get"));
     a.source = reinterpret_cast<decltype(a.source)>(sym("nt_exec_source"));
     a.destroy = reinterpret_cast<decltype(a.destroy)>(sym("nt_exec_destroy"));
@@ -328,15 +387,44 @@ class RocmAadExecutable : public AadExecutable {
       if (rc != NT_OK) raise(rc, "nt_exec_set_inputs");
       dirty_ = false;
     }
-    std::vector<double> sums(2 + inputs_.size());
+    std::vector<double> sums(static_cast<size_t>(tape().outputCount()) * (2 + inputs_.size()));
     double timing[3] = {0, 0, 0};
     int rc = a.replay(exec_, static_cast<uint64_t>(paths), static_cast<uint64_t>(pathOffset),
                       static_cast<uint64_t>(seed), sums.data(), static_cast<int32_t>(sums.size()), timing);
     if (rc != NT_OK) raise(rc, "nt_exec_replay");
-    if (!options_.adjoints()) {
-      for (size_t j = 2; j < sums.size(); ++j) sums[j] = 0.0;
+    return AadResult::fromSums(sums, tape().outputNames(), tape().inputNames(), paths, timing[1] / 1e3,
+                               timing[0] / 1e3);
+  }
+  std::vector<AadResult> replayMany(const std::vector<std::vector<double>>& inputSets, long long paths,
+                                    long long pathOffset, long long seed) override {
+    checkOpen();
+    if (paths <= 0) throw std::invalid_argument("paths must be positive");
+    if (inputSets.empty()) throw std::invalid_argument("at least one input set is required");
+    const size_t nin = inputs_.size();
+    std::vector<double> flat;
+    flat.reserve(inputSets.size() * nin);
+    for (size_t m = 0; m < inputSets.size(); ++m) {
+      if (inputSets[m].size() != nin) {
+        throw std::invalid_argument("input set " + std::to_string(m) + " has " + std::to_string(inputSets[m].size()) +
+                                    " values; the tape has " + std::to_string(nin) + " inputs");
+      }
+      flat.insert(flat.end(), inputSets[m].begin(), inputSets[m].end());
     }
-    return AadResult::fromSums(sums, tape().inputNames(), paths, timing[1] / 1e3, timing[0] / 1e3);
+    const int32_t markets = static_cast<int32_t>(inputSets.size());
+    const size_t one = static_cast<size_t>(tape().outputCount()) * (2 + nin);
+    std::vector<double> sums(one * inputSets.size());
+    double timing[3] = {0, 0, 0};
+    int rc = abi().replay_many(exec_, flat.data(), markets, static_cast<uint64_t>(paths),
+                               static_cast<uint64_t>(pathOffset), static_cast<uint64_t>(seed), sums.data(),
+                               static_cast<int32_t>(sums.size()), timing);
+    if (rc != NT_OK) raise(rc, "nt_exec_replay_many");
+    std::vector<AadResult> out;
+    for (int32_t m = 0; m < markets; ++m) {
+      std::vector<double> part(sums.begin() + m * one, sums.begin() + (m + 1) * one);
+      out.push_back(AadResult::fromSums(part, tape().outputNames(), tape().inputNames(), paths, timing[1] / 1e3,
+                                        timing[0] / 1e3));
+    }
+    return out;
   }
   void close() override {
     if (exec_) {
@@ -383,7 +471,8 @@ std::string RocmAadEngine::describe() const {
 }
 
 std::unique_ptr<AadExecutable> RocmAadEngine::compile(TapePtr tape, const AadOptions& options) const {
-  requireSupportedTape(*tape);
+  // Multi-output tapes, uniforms and named streams lower natively here (the
+  // reference's device engines decline them with requireSupportedTape).
   const RocmAbi& a = abi();
   if (!a.loaded) throw std::logic_error("no ROCm/HIP device available for the AAD replay kernel (" + a.error + ")");
   const AadTape& t = *tape;

@@ -70,6 +70,16 @@ class AadResult {
   const std::vector<double>& gradients() const { return gradients_; }
   double gradient(const std::string& inputName) const;
   const std::vector<std::string>& inputNames() const { return input_names_; }
+  // Every recorded output (AadResult.java:88-151); output 0 is the one the
+  // accessors above report.
+  const std::vector<std::string>& outputNames() const { return output_names_; }
+  int outputCount() const { return static_cast<int>(output_names_.size()); }
+  double value(const std::string& outputName) const { return values_.at(outputIndex(outputName)); }
+  double standardError(const std::string& outputName) const { return stderrs_.at(outputIndex(outputName)); }
+  double gradient(const std::string& outputName, const std::string& inputName) const;
+  const std::vector<double>& gradients(const std::string& outputName) const {
+    return jacobian_.at(outputIndex(outputName));
+  }
   long long paths() const { return paths_; }
   double seconds() const { return seconds_; }
   double pathsPerSecond() const { return paths_ / seconds_; }
@@ -77,10 +87,16 @@ class AadResult {
   // raw sums (sum y, sum y^2, sum adjoint_j); empty when built from means only
   const std::vector<double>& rawSums() const { return raw_; }
   double kernelSeconds() const { return kernel_seconds_; }
-  static AadResult fromSums(const std::vector<double>& sums, const std::vector<std::string>& inputNames,
-                            long long paths, double seconds, double kernelSeconds);
+  // sums: per output, [sum y, sum y^2, sum dy/dx_j] (AadTotals.toResult, AadTotals.java:68-89)
+  static AadResult fromSums(const std::vector<double>& sums, const std::vector<std::string>& outputNames,
+                            const std::vector<std::string>& inputNames, long long paths, double seconds,
+                            double kernelSeconds);
  private:
+  int outputIndex(const std::string& outputName) const;
   double value_, stderr_;
+  std::vector<std::string> output_names_;
+  std::vector<double> values_, stderrs_;
+  std::vector<std::vector<double>> jacobian_;
   std::vector<double> gradients_;
   std::vector<std::string> input_names_;
   long long paths_;
@@ -98,6 +114,13 @@ class AadExecutable {
   TapePtr tapePtr() const { return tape_; }
   virtual void setInput(const std::string& name, double value);
   virtual AadResult replay(long long paths, long long pathOffset, long long seed) = 0;
+  // Prices every input set (each in tape().inputNames() order) over the same
+  // paths and seed; results equal one replay per set with those inputs. The
+  // bound inputs are left unchanged. Engines that can share each path's draws
+  // across the sets override it (VulkanAadKernel.replayMany,
+  // nablatensor-engine-vulkan/.../VulkanAadKernel.java:162-238).
+  virtual std::vector<AadResult> replayMany(const std::vector<std::vector<double>>& inputSets, long long paths,
+                                            long long pathOffset, long long seed);
   virtual void close() { closed_ = true; }
   virtual double compileSeconds() const { return 0.0; }
   AadResult replaySafe(long long totalPaths, long long seed);

@@ -164,6 +164,7 @@ class Executable:
         t = arrays.struct()
         self.options = opts or options()
         self.n_inputs = len(arrays.input_node)
+        self.n_outputs = len(arrays.output_node)
         h = C.c_void_p()
         _check(lib().nt_exec_create(C.byref(t), C.byref(self.options), C.byref(h)))
         self._h = h
@@ -173,8 +174,9 @@ class Executable:
         _check(lib().nt_exec_set_inputs(self._h, v.ctypes.data_as(C.POINTER(C.c_double)), len(v)))
 
     def replay(self, paths: int, offset: int = 0, seed: int = 42):
-        """Raw sums [sum y, sum y^2, sum adjoints...] and timing {kernel_ms, wall_ms, replay_ms}."""
-        sums = np.zeros(2 + self.n_inputs, dtype=np.float64)
+        """Raw sums [sum y, sum y^2, sum adjoints...] (one such row per output,
+        concatenated) and timing {kernel_ms, wall_ms, replay_ms}."""
+        sums = np.zeros(self.n_outputs * (2 + self.n_inputs), dtype=np.float64)
         timing = np.zeros(3, dtype=np.float64)
         _check(lib().nt_exec_replay(self._h, paths, offset & 0xFFFFFFFFFFFFFFFF, seed & 0xFFFFFFFFFFFFFFFF,
                                     sums.ctypes.data_as(C.POINTER(C.c_double)), len(sums),
@@ -188,7 +190,7 @@ class Executable:
         markets = x.shape[0] if x.ndim == 2 else 1
         if x.size != markets * self.n_inputs:
             raise ValueError(f"expected {markets} x {self.n_inputs} input values, got shape {x.shape}")
-        sums = np.zeros((markets, 2 + self.n_inputs), dtype=np.float64)
+        sums = np.zeros((markets, self.n_outputs * (2 + self.n_inputs)), dtype=np.float64)
         timing = np.zeros(3, dtype=np.float64)
         _check(lib().nt_exec_replay_many(self._h, x.ctypes.data_as(C.POINTER(C.c_double)), markets, paths,
                                          offset & 0xFFFFFFFFFFFFFFFF, seed & 0xFFFFFFFFFFFFFFFF,
@@ -197,12 +199,18 @@ class Executable:
         return sums, {"kernel_ms": timing[0], "wall_ms": timing[1], "replay_ms": timing[2]}
 
     def replay_paths(self, paths: int, offset: int = 0, seed: int = 42):
-        values = np.zeros(paths, dtype=np.float64)
-        grads = np.zeros((paths, max(1, self.n_inputs)), dtype=np.float64)
+        """Per-path values (paths,) and derivatives (paths, inputs); with
+        several outputs (paths, outputs) and (paths, outputs, inputs)."""
+        no = self.n_outputs
+        values = np.zeros(paths * no, dtype=np.float64)
+        grads = np.zeros((paths * no, max(1, self.n_inputs)), dtype=np.float64)
         _check(lib().nt_exec_replay_paths(self._h, paths, offset & 0xFFFFFFFFFFFFFFFF, seed & 0xFFFFFFFFFFFFFFFF,
                                           values.ctypes.data_as(C.POINTER(C.c_double)),
                                           grads.ctypes.data_as(C.POINTER(C.c_double))))
-        return values, grads[:, :self.n_inputs]
+        grads = grads[:, :self.n_inputs]
+        if no == 1:
+            return values, grads
+        return values.reshape(paths, no), grads.reshape(paths, no, self.n_inputs)
 
     def info(self) -> dict:
         i = NtExecInfo()

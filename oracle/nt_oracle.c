@@ -151,8 +151,8 @@ static inline void adj_add(double *d, int32_t node, double contribution, int f32
 }
 
 /* Per-worker sweep over [from, from+count): ScalarReplay.run, ScalarReplay.java:78-172.
- * When rows != NULL the per-path value and adjoints of output 0 are written there
- * (row p - row_base) instead of only being summed. */
+ * When rows != NULL the per-path value and adjoints of every output are written
+ * there (row (p - row_base) * n_outputs + o) instead of only being summed. */
 static void run_range(const nto_tape *t, const uint8_t *active, const double *in,
                       uint64_t from, uint64_t count, uint64_t seed, int f32, int adjoints,
                       double *value, double *sumsq, double *gradient,
@@ -201,7 +201,9 @@ static void run_range(const nto_tape *t, const uint8_t *active, const double *in
       sumsq[o] += y * y;
     }
     if (row_values) {
-      row_values[path - row_base] = v[t->output_node[0]];
+      for (int32_t o = 0; o < t->n_outputs; o++) {
+        row_values[(path - row_base) * (uint64_t)t->n_outputs + (uint64_t)o] = v[t->output_node[o]];
+      }
     }
     if (!adjoints) {
       continue;
@@ -236,9 +238,10 @@ static void run_range(const nto_tape *t, const uint8_t *active, const double *in
       for (int32_t j = 0; j < t->n_inputs; j++) {
         gradient[(size_t)o * (size_t)t->n_inputs + (size_t)j] += d[t->input_node[j]];
       }
-      if (row_grads && o == 0) {
+      if (row_grads) {
         for (int32_t j = 0; j < t->n_inputs; j++) {
-          row_grads[(path - row_base) * (uint64_t)t->n_inputs + (uint64_t)j] = d[t->input_node[j]];
+          row_grads[((path - row_base) * (uint64_t)t->n_outputs + (uint64_t)o) * (uint64_t)t->n_inputs + (uint64_t)j] =
+              d[t->input_node[j]];
         }
       }
     }

@@ -72,7 +72,8 @@ void nto_mark_active(const nto_tape *t, uint8_t *active);
 int nto_replay(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                uint64_t seed, int f32, int adjoints, int threads, nto_totals *out);
 
-/* Per-path rows for output 0: values[p] and grads[p * n_inputs + j]. */
+/* Per-path rows for every output: values[p * n_outputs + o] and
+ * grads[(p * n_outputs + o) * n_inputs + j]. */
 int nto_replay_paths(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                      uint64_t seed, int f32, int threads, double *values, double *grads);
 

@@ -89,6 +89,10 @@ def normal(path: int, seed: int, k: int, stream: int = 0) -> float:
     return lib().nto_normal(path & (2**64 - 1), seed & (2**64 - 1), stream, k)
 
 
+def uniform(path: int, seed: int, k: int, stream: int = 0) -> float:
+    return lib().nto_uniform(path & (2**64 - 1), seed & (2**64 - 1), stream, k)
+
+
 def active(flat: dict) -> np.ndarray:
     t = Tape(flat)
     out = np.zeros(len(t.op), dtype=np.uint8)
@@ -97,8 +101,9 @@ def active(flat: dict) -> np.ndarray:
 
 
 def replay_sums(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, f32: bool = False,
-                adjoints: bool = True, threads: int = 0) -> np.ndarray:
-    """Raw sums [sum y, sum y^2, sum adjoint_j...] for output 0 (AadTotals fields)."""
+                adjoints: bool = True, threads: int = 0, all_outputs: bool = False) -> np.ndarray:
+    """Raw sums [sum y, sum y^2, sum adjoint_j...] for output 0 (AadTotals
+    fields); with all_outputs, one such row per output, concatenated."""
     t = Tape(flat)
     x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
     no = len(t.output_node)
@@ -111,22 +116,30 @@ def replay_sums(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=
                           offset & (2**64 - 1), seed & (2**64 - 1), int(f32), int(adjoints), threads, C.byref(tot))
     if rc != 0:
         raise ValueError(f"oracle rejected the tape ({rc})")
-    return np.concatenate([[val[0], sq[0]], gr[:t.n_inputs]])
+    ni = t.n_inputs
+    rows = [np.concatenate([[val[o], sq[o]], gr[o * ni:(o + 1) * ni]]) for o in range(no if all_outputs else 1)]
+    return np.concatenate(rows)
 
 
 def replay_paths(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, f32: bool = False,
-                 threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+                 threads: int = 0, output=0) -> tuple[np.ndarray, np.ndarray]:
+    """Per-path value and adjoints of output `output` (None: every output,
+    shapes (paths, outputs) and (paths, outputs, inputs))."""
     t = Tape(flat)
     x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
-    values = np.zeros(paths)
-    grads = np.zeros((paths, max(1, t.n_inputs)))
+    no = len(t.output_node)
+    values = np.zeros((paths, no))
+    grads = np.zeros((paths, no, max(1, t.n_inputs)))
     rc = lib().nto_replay_paths(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
                                 offset & (2**64 - 1), seed & (2**64 - 1), int(f32), threads,
                                 values.ctypes.data_as(C.POINTER(C.c_double)),
                                 grads.ctypes.data_as(C.POINTER(C.c_double)))
     if rc != 0:
         raise ValueError(f"oracle rejected the tape ({rc})")
-    return values, grads[:, :t.n_inputs]
+    grads = grads[:, :, :t.n_inputs]
+    if output is None:
+        return values, grads
+    return values[:, output].copy(), grads[:, output, :].copy()
 
 
 def to_result(sums: np.ndarray, paths: int) -> dict:

@@ -107,3 +107,43 @@ def check_per_path(values, grads, flat, paths, offset, seed, tol=1e-12, min_stri
     assert out["violations"] == 0, out
     assert strict.mean() >= min_strict, out
     return out
+
+
+def jump_clock_tape(nt, steps=16):
+    """The reference's RandomStreamsTest body (RandomStreamsTest.java:70-84): a
+    normal on the default stream and a uniform on a named stream per step; the
+    smooth jump indicator 1 / (1 + exp(-(u - 0.97) / 0.01)) stands in for
+    Smooth.gt."""
+    def body(rec):
+        s0 = rec.input("S0", 100.0)
+        vol = rec.input("sigma", 0.2)
+        jumps = rec.stream("jump-clock")
+        acc = s0
+        for _ in range(steps):
+            z = rec.randn()
+            u = jumps.randu()
+            jump = u.sub(0.97).mul(-100.0).exp().add(1.0)
+            jump = rec.constant(1.0).div(jump)
+            acc = acc.mul(vol.mul(z).mul(0.05).add(1.0)).add(jump.mul(2.0))
+        rec.output(acc)
+    return nt.AadRecorder.record(body)
+
+
+def two_output_tape(nt, steps=40):
+    """Two outputs of one GBM path with a uniform-driven barrier shift: the
+    terminal spot and the running maximum (MultiOutput-style measures)."""
+    def body(rec):
+        s0 = rec.input("S0", 100.0)
+        vol = rec.input("sigma", 0.25)
+        r = rec.input("r", 0.03)
+        dt = 1.0 / steps
+        drift = r.sub(vol.mul(vol).mul(0.5)).mul(dt)
+        sd = vol.mul(dt ** 0.5)
+        s = s0
+        hi = s0
+        for _ in range(steps):
+            s = s.mul(drift.add(sd.mul(rec.randn())).exp())
+            hi = hi.max(s.mul(rec.stream("shift").randu().mul(0.01).add(0.995)))
+        rec.output("spot", s)
+        rec.output("max", hi)
+    return nt.AadRecorder.record(body)

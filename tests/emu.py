@@ -45,18 +45,26 @@ class EmulatedKernel:
         self.slots = tape_slots
 
     def run(self, inputs, paths: int, offset: int = 0, seed: int = 42, grid: int = 4, block: int = 64,
-            markets: int = 1):
+            markets: int = 1, outputs: int = 1):
         """One emulated dispatch. With markets > 1, `inputs` holds one row per
-        market and every result gains a leading market axis."""
+        market and every result gains a leading market axis; with outputs > 1,
+        per-path rows gain an output axis after the path and sums hold one
+        row per output."""
         x = np.ascontiguousarray(inputs, dtype=np.float64).reshape(-1)
-        sums = np.zeros(markets * (2 + self.n_inputs))
-        values = np.zeros(markets * paths)
-        grads = np.zeros((markets * paths, max(1, self.n_inputs)))
+        ni = self.n_inputs
+        sums = np.zeros(markets * outputs * (2 + ni))
+        values = np.zeros(markets * paths * outputs)
+        grads = np.zeros((markets * paths * outputs, max(1, ni)))
         p = lambda a: a.ctypes.data_as(C.POINTER(C.c_double))
         self.lib.emu_run(paths, offset & (2**64 - 1), seed & (2**64 - 1), p(x), p(sums), p(values), p(grads),
                          grid, block, self.slots)
-        grads = grads[:, :self.n_inputs]
+        grads = grads[:, :ni]
+        if outputs > 1:
+            sums = sums.reshape(markets, outputs, 2 + ni)
+            values = values.reshape(markets, paths, outputs)
+            grads = grads.reshape(markets, paths, outputs, ni)
+            return (sums[0], values[0], grads[0]) if markets == 1 else (sums, values, grads)
         if markets == 1:
             return sums, values, grads
-        return (sums.reshape(markets, 2 + self.n_inputs), values.reshape(markets, paths),
-                grads.reshape(markets, paths, self.n_inputs))
+        return (sums.reshape(markets, 2 + ni), values.reshape(markets, paths),
+                grads.reshape(markets, paths, ni))

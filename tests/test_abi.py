@@ -48,21 +48,28 @@ def _mutated(flat, **kw):
     return out
 
 
-def test_unsupported_tapes_are_declined(rocm, tapes):
+def test_extended_tapes_lower_and_bad_draws_are_rejected(rocm, tapes):
+    """Multi-output tapes, uniforms and named streams lower (the reference's
+    device engines decline them, AadEngine.java:56-86; this one takes them);
+    a multi-output tape refuses a forced reverse sweep; draws naming a stream
+    the tape does not have are malformed."""
     flat = tapes["C1"]
     two_outputs = _mutated(flat, output_node=np.array([25, 24], dtype=np.int32))
+    assert "mode=tangent" in rocm.lower(two_outputs)
     with pytest.raises(rocm.NtError) as e:
-        rocm.lower(two_outputs)
-    assert e.value.status == rocm.NT_E_UNSUPPORTED and "multi-output" in str(e.value)
+        rocm.lower(two_outputs, rocm.options(mode=rocm.NT_MODE_REVERSE))
+    assert e.value.status == rocm.NT_E_UNSUPPORTED and "one output" in str(e.value)
     uniform = _mutated(flat)
     uniform["op"][14] = 3  # RANDU
-    with pytest.raises(rocm.NtError) as e:
-        rocm.lower(uniform)
-    assert e.value.status == rocm.NT_E_UNSUPPORTED and "randu" in str(e.value)
+    assert "nt_uniform(" in rocm.lower(uniform)
     streams = _mutated(flat, n_streams=2)
+    streams["arg_b"][14] = 1
+    assert "rhi1 = rhi ^ 0x9E3779B1u" in rocm.lower(streams)
+    bad = _mutated(flat)
+    bad["arg_b"][14] = 1  # stream 1 of a one-stream tape
     with pytest.raises(rocm.NtError) as e:
-        rocm.lower(streams)
-    assert e.value.status == rocm.NT_E_UNSUPPORTED
+        rocm.lower(bad)
+    assert e.value.status == rocm.NT_E_INVALID
 
 
 def test_malformed_tapes_are_rejected(rocm, tapes):

@@ -84,7 +84,41 @@ def test_fp32_monte_carlo(nt, tapes):
     mc.close()
 
 
-def test_engine_declines_extended_tapes_on_device(nt):
-    t = nt.AadRecorder.record(lambda rec: rec.output(rec.input("x", 1.0).mul(rec.stream("s").randn())))
-    with pytest.raises(NotImplementedError):
-        nt.AadEngines.require("rocm", nt.AadOptions.defaults()).compile(t, nt.AadOptions.defaults())
+def test_extended_tapes_run_on_device(nt):
+    """Named streams, uniforms and two outputs through the engine: every
+    output's value, standard error and Jacobian row against the oracle."""
+    from conftest import two_output_tape
+    t = two_output_tape(nt)
+    fp64 = nt.AadOptions.defaults().withPrecision(nt.AadOptions.PrecisionEnum.FLOAT64)  # defaults are fp32
+    exe = nt.AadEngines.require("rocm", fp64).compile(t, fp64)
+    r = exe.replay(100_000, 0, 42)
+    assert r.outputNames() == ["spot", "max"] and r.outputCount() == 2
+    ref = oracle.replay_sums(t.flat(), 100_000, 0, 42, all_outputs=True).reshape(2, -1)
+    for o, name in enumerate(["spot", "max"]):
+        got = oracle.to_result(np.array(r.rawSums()).reshape(2, -1)[o], 100_000)
+        want = oracle.to_result(ref[o], 100_000)
+        assert abs(r.valueOf(name) - want["price"]) <= 1e-10 * abs(want["price"])
+        assert abs(got["price"] - want["price"]) <= 1e-10 * abs(want["price"])
+        for j, inp in enumerate(r.inputNames()):
+            assert abs(r.gradient(name, inp) - want["gradient"][j]) <= 1e-10 * max(1.0, abs(want["gradient"][j]))
+    exe.close()
+
+
+def test_replay_many_spot_ladder_shares_draws(nt):
+    """A spot ladder priced in one call: each rung equals a separate replay with
+    that spot (bit for bit on the raw sums), prices increase along the ladder."""
+    mc = (nt.MonteCarlo.of(nt.Products.asianCall()).market(nt.EquityMarket.atmOneYear())
+          .steps(252).greeks().fp64().on("rocm").build())
+    exe = mc.executable()
+    base = [100.0, 100.0, 0.2, 0.03, 1.0]
+    sets = [[s] + base[1:] for s in (90.0, 95.0, 100.0, 105.0, 110.0)]
+    many = exe.replayMany(sets, 100_000, 0, 42)
+    assert len(many) == 5
+    prices = [r.value() for r in many]
+    assert all(b > a for a, b in zip(prices, prices[1:]))
+    for s, r in zip(sets, many):
+        for name, v in zip(exe.tape().inputNames(), s):
+            exe.setInput(name, v)
+        one = exe.replay(100_000, 0, 42)
+        assert np.array_equal(np.array(r.rawSums()), np.array(one.rawSums()))
+    mc.close()

@@ -185,3 +185,38 @@ def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
         assert np.array_equal(many[0], one)
         with pytest.raises(ValueError):
             x.replay_many(np.zeros((2, 3)), 10_000, 0, 7)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_uniforms_and_named_streams_per_path(rocm, nt, mode):
+    """The reference's random-streams body rolled over 64 steps: per path
+    against the oracle (reverse sweep and tangent mode)."""
+    from conftest import jump_clock_tape
+    flat = jump_clock_tape(nt, 64).flat()
+    print(f"case jump-clock mode={mode}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+        v, g = x.replay_paths(2048, OFFSET, 42)
+        sums, _ = x.replay(200_000, 0, 42)
+    print(check_per_path(v, g, flat, 2048, OFFSET, 42))
+    ref = oracle.replay_sums(flat, 200_000, 0, 42)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-10
+
+
+def test_multi_output_per_path_and_sums(rocm, nt):
+    from conftest import two_output_tape
+    flat = two_output_tape(nt).flat()
+    print("case two outputs", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64")) as x:
+        assert x.info()["mode"] == 2
+        v, g = x.replay_paths(2048, OFFSET, 42)
+        sums, _ = x.replay(200_000, 0, 42)
+        many, _ = x.replay_many(np.stack([flat["recorded_inputs"], np.array(flat["recorded_inputs"]) * 1.1]),
+                                200_000, 0, 42)
+    assert v.shape == (2048, 2) and g.shape == (2048, 2, 3)
+    ov, og = oracle.replay_paths(flat, 2048, OFFSET, 42, output=None)
+    for o in range(2):
+        ev, eg = oracle.path_errors(v[:, o], g[:, o, :], ov[:, o], og[:, o, :])
+        assert ev.max() <= 1e-12 and eg.max() <= 1e-12, o
+    ref = oracle.replay_sums(flat, 200_000, 0, 42, all_outputs=True)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-10
+    assert np.array_equal(many[0], sums)

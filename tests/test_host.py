@@ -96,7 +96,11 @@ def test_selection_without_a_device(nt):
         nt.MonteCarlo.of(nt.Products.asianCall()).market(nt.EquityMarket.atmOneYear()).steps(8).on("rocm").build()
 
 
-def test_engine_declines_extended_tapes(nt):
+@pytest.mark.skipif(gpu_available(), reason="checks the decline path without a device")
+def test_engine_takes_extended_tapes(nt):
+    """The rocm engine no longer declines uniforms, named streams or several
+    outputs (the reference's device engines do, AadEngine.java:56-86): without
+    a device the only refusal left is the missing device."""
     t = nt.AadRecorder.record(lambda rec: rec.output(rec.input("x", 1.0).add(rec.randu())))
-    with pytest.raises(NotImplementedError, match="randu"):
+    with pytest.raises(RuntimeError, match="no ROCm/HIP gfx950 device"):
         nt.RocmAadEngine().compile(t, nt.AadOptions.defaults())

@@ -148,7 +148,7 @@ def test_loop_plan_of_the_workloads(rocm, tapes):
 def test_draw_pairs_share_one_philox_block(rocm, tapes):
     for mode in (1, 2):
         src = rocm.lower(tapes["C2"], rocm.options("fp64", checkpoint=1, seg_len=14, mode=mode))
-        fwd = src.split("for (nt_u32 sg = 0;")[1].split("nt_y = ")[0]
+        fwd = src.split("for (nt_u32 sg = 0;")[1].split("nt_y[")[0]
         assert fwd.count("nt_normal_pair(") == 7  # 14 draws per segment, two legs per block
 
 
@@ -237,3 +237,40 @@ def test_markets_share_draws_and_match_single_market_bit_for_bit(rocm, tapes, na
         s1, v1, g1 = run_emulated(flat, rocm.options("fp64", mode=2), paths, inputs=sets[m], rocm=rocm)
         assert np.array_equal(v[m], v1) and np.array_equal(g[m], g1), m
         assert np.array_equal(sums[m], s1), m
+
+
+def test_uniforms_and_named_streams_match_oracle(nt, rocm):
+    """The reference's random-streams body (a named-stream uniform beside the
+    default-stream normal each step): the reverse sweep equals the oracle bit
+    for bit with libm Box-Muller, tangent mode in values bit for bit and in
+    derivatives to the per-path bar, for a straight-line and a rolled tape."""
+    from conftest import jump_clock_tape
+    for steps, rolled in ((3, False), (64, True)):
+        flat = jump_clock_tape(nt, steps).flat()
+        src = rocm.lower(flat, rocm.options("fp64", mode=1, libm=1))
+        assert ("rolled loop" in src) == rolled
+        assert "rhi1 = rhi ^ 0x9E3779B1u" in src
+        ov, og = oracle.replay_paths(flat, 300, OFFSET, 42, threads=1)
+        _, v, g = run_emulated(flat, rocm.options("fp64", mode=1, libm=1), 300, rocm=rocm)
+        assert np.array_equal(v, ov) and np.array_equal(g, og), steps
+        _, v, g = run_emulated(flat, rocm.options("fp64", mode=2, libm=1), 300, rocm=rocm)
+        assert np.array_equal(v, ov), steps
+        check_per_path(v, g, flat, 300, OFFSET, 42)
+
+
+def test_multi_output_rows_match_oracle(nt, rocm):
+    """Two outputs: every output's per-path value and Jacobian row, and its
+    sums, against the oracle's (which sweeps the outputs one by one)."""
+    from conftest import two_output_tape
+    flat = two_output_tape(nt).flat()
+    src = rocm.lower(flat, rocm.options("fp64", libm=1))
+    assert "mode=tangent" in src and "rolled loop" in src
+    k = emu.EmulatedKernel(src, 3, tape_slots(src))
+    sums, v, g = k.run(flat["recorded_inputs"], 200, OFFSET, 42, grid=3, block=64, outputs=2)
+    ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, threads=1, output=None)
+    assert np.array_equal(v, ov)
+    for o in range(2):
+        ev, eg = oracle.path_errors(v[:, o], g[:, o, :], ov[:, o], og[:, o, :])
+        assert ev.max() == 0.0 and eg.max() <= 1e-12, o
+    ref = oracle.replay_sums(flat, 200, OFFSET, 42, threads=1, all_outputs=True).reshape(2, -1)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-12

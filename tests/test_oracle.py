@@ -11,6 +11,9 @@
   price = price-only price (ModelsTest.java:67-68), additivity of path ranges,
   thread-count independence.
 * Brute force: central differences with common random numbers on small tapes.
+* Uniforms and named streams: the keying restated in numpy, and the reference's
+  own statistical checks (RandomStreamsTest.java: E[U] = 1/2, E[U^4] = 1/5,
+  independent streams); several outputs: sums that follow from a scaled copy.
 A planted mistake in the oracle (sign of a reverse rule, a leg swap, an input
 order slip) fails at least one of these.
 """
@@ -213,3 +216,58 @@ def test_fp32_mode_rounds_every_node(tapes):
     assert rel_err(v32, v64) < 1e-4
     assert not np.array_equal(v32, v64)
     assert np.all(v32.astype(np.float32) == v32)  # stored values are floats
+
+
+# ---- uniforms and named streams -------------------------------------------------------
+
+@pytest.mark.parametrize("stream,k", [(0, 0), (0, 5), (1, 0), (3, 7)])
+def test_uniform_and_stream_keying(stream, k):
+    """Uniform k of stream s: counter (lo, hi ^ s*0x9E3779B1 ^ (k | 2^30)),
+    u = (c0 + 0.5) 2^-32 (Philox.java:44-52,81-94); normals of stream s use the
+    same hi word."""
+    path, seed = 0x100000003, 42
+    lo = (path & 0xFFFFFFFF) ^ (seed & 0xFFFFFFFF)
+    hi = ((path >> 32) ^ (seed >> 32)) ^ ((stream * 0x9E3779B1) & 0xFFFFFFFF)
+    c0, _ = _philox_np(lo, hi ^ (k | 0x40000000), 0x1BD11BDA)
+    assert oracle.uniform(path, seed, k, stream) == (c0 + 0.5) * 2.0 ** -32
+    c0, c1 = _philox_np(lo, hi ^ (k >> 1), 0x1BD11BDA)
+    r = math.sqrt(-2.0 * math.log((c0 + 0.5) * 2.0 ** -32))
+    th = 6.283185307179586 * ((c1 + 0.5) * 2.0 ** -32)
+    want = r * (math.cos(th) if k % 2 == 0 else math.sin(th))
+    assert oracle.normal(path, seed, k, stream) == pytest.approx(want, rel=1e-15, abs=1e-15)
+
+
+def test_uniforms_are_a_unit_interval_sample():
+    """RandomStreamsTest.uniformDrawHasTheRightMeanAndRange: E[U] = 1/2,
+    E[U^4] = 1/5, every draw in (0, 1)."""
+    u = np.array([oracle.uniform(p, 0xC0FFEE, 0) for p in range(60_000)])
+    assert abs(u.mean() - 0.5) < 5e-3 and abs(np.mean(u ** 4) - 0.2) < 5e-3
+    assert u.min() > 0.0 and u.max() < 1.0
+
+
+def test_named_streams_are_independent():
+    """RandomStreamsTest.namedStreamsAreIndependent: E[z_a z_b] ~ 0 across
+    streams; stream 0 is the default stream, and uniforms never reuse a
+    normal's Philox block."""
+    za = np.array([oracle.normal(p, 0xC0FFEE, 0, 1) for p in range(40_000)])
+    zb = np.array([oracle.normal(p, 0xC0FFEE, 0, 2) for p in range(40_000)])
+    assert abs(np.mean(za * zb)) < 2e-2
+    assert not np.array_equal(za, zb)
+    u0 = np.array([oracle.uniform(p, 7, 0) for p in range(2000)])
+    z0 = np.array([oracle.normal(p, 7, 0) for p in range(2000)])
+    assert abs(np.corrcoef(u0, z0)[0, 1]) < 0.1
+
+
+def test_multi_output_sums_are_one_sweep_per_output(nt):
+    """A tape whose second output is twice the first: its sums (values,
+    squares x4, adjoints) follow exactly from the first output's."""
+    def body(rec):
+        x = rec.input("x", 1.5)
+        y = x.mul(rec.randn()).exp()
+        rec.output("y", y)
+        rec.output("2y", y.mul(2.0))
+    flat = nt.AadRecorder.record(body).flat()
+    s = oracle.replay_sums(flat, 5000, 0, 3, all_outputs=True).reshape(2, -1)
+    assert s[1][0] == 2 * s[0][0] and s[1][1] == 4 * s[0][1] and s[1][2] == 2 * s[0][2]
+    v, g = oracle.replay_paths(flat, 50, 0, 3, output=None)
+    assert np.array_equal(v[:, 1], 2 * v[:, 0]) and np.array_equal(g[:, 1, :], 2 * g[:, 0, :])
