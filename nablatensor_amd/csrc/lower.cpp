@@ -618,13 +618,14 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.n_stored = 0;
   p.ck_slots = p.tape_slots = 0;
   if (!L.found) return;
-  // Iterations per loop trip: up to four when the registers the carried
-  // state and its tangents hold leave room (and always an even count when a
-  // step draws an odd number of normals, so both Box-Muller legs stay in one
-  // trip). Longer trips let the scheduler overlap one step's Philox and
-  // transcendental latency with its neighbour's arithmetic and cut the
-  // register moves at the loop edge; measured on the Asian tape, 4 beats 2 by
-  // 16% with fewer VGPRs.
+  // Iterations per loop trip, by the registers the carried state and its
+  // tangents hold (always an even count when a step draws an odd number of
+  // normals, so both Box-Muller legs stay in one trip). Longer trips let the
+  // scheduler overlap one step's Philox and transcendental latency with its
+  // neighbour's arithmetic; shorter ones keep occupancy when the state is
+  // large. Measured on MI355X: Asian fp32 (10 registers of state) 4 steps
+  // beat 8; barrier fp64 (20) 2 beat 4 by 6%; the 16-asset worst-of fp32
+  // (65) 1 beat 2 by 16% (238 VGPRs, two waves per SIMD, instead of 260).
   const int W = p.n_words;
   int live = 0;
   for (int j = 0; j < L.period; ++j) {
@@ -632,7 +633,7 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   }
   const int w = p.precision == NT_FP64 ? 2 : 1;
   const int regs = live * w * p.markets;
-  int seg = o.seg_len > 0 ? o.seg_len : (regs <= 32 ? 4 : regs <= 64 ? 2 : 1);
+  int seg = o.seg_len > 0 ? o.seg_len : (regs <= 16 ? 4 : regs <= 48 ? 2 : 1);
   if (L.need_even && (seg & 1)) seg += 1;
   seg = std::max(1, std::min(seg, L.iters));
   p.seg = seg;
