@@ -799,6 +799,21 @@ class Emitter {
     return d;
   }
   std::string tname(int node, int j) const;  // straight-line node or loop live-out
+  // A MUL whose other operand is exp(x) used nowhere else: its tangent is
+  // (tc + c tx) exp(x) per input, two operations instead of three (tx exp(x)
+  // then the product rule); set by the caller of tangent() for one MUL.
+  struct ExpFactor {
+    bool on = false;
+    int side = 1;                                  // operand holding exp(x): 0 = a, 1 = b
+    std::function<std::string(int)> tx;            // tangent of x
+  } xe_;
+  std::vector<int> uses_;       // per node: operand references + outputs
+  std::vector<int> body_uses_;  // per loop position: references within and across iterations, + live-out
+  void count_uses();
+  bool single_exp(int node) const { return t_.op[node] == NT_OP_EXP && uses_[node] == 1; }
+  bool single_body_exp(int pos) const {
+    return t_.op[L_.start + pos] == NT_OP_EXP && body_uses_[pos] == 1 && !L_.is_liveout[pos] && !L_.is_carry[pos];
+  }
   void tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx, const std::vector<int>& D,
                const std::string& Vi, const std::string& Va, const std::string& Vb,
                const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb);
@@ -1098,6 +1113,15 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
         e = A.empty() ? (B.empty() ? "" : "-" + val(B)) : (B.empty() ? val(A) : val(A) + " - " + val(B));
         break;
       case NT_OP_MUL:
+        if (xe_.on) {
+          // c * exp(x): (tc + c tx) exp(x)
+          const std::string C = xe_.side == 1 ? A : B, X = xe_.tx(j);
+          const std::string cv = xe_.side == 1 ? Va : Vb, ev = xe_.side == 1 ? Vb : Va;
+          if (!C.empty() && !X.empty()) e = "(" + FMA + "(" + val(X) + ", " + cv + ", " + val(C) + ") * " + ev + ")";
+          else if (!C.empty()) e = mulv(C, ev);
+          else if (!X.empty()) e = "(" + mulv(X, cv) + " * " + ev + ")";
+          break;
+        }
         if (!A.empty() && !B.empty()) {
           e = A == "#1" ? FMA + "(" + Va + ", " + val(B) + ", " + Vb + ")"
                         : FMA + "(" + A + ", " + Vb + ", " + mulv(B, Va) + ")";
@@ -1142,8 +1166,16 @@ void Emitter::tline(int lo, int hi) {
       o_ << "    const real v" << i << ms(act) << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
       if (!act || ar == 0 || !p_.adjoints) continue;
       const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
+      xe_ = ExpFactor();
+      if (op == NT_OP_MUL && a != b && (single_exp(b) || single_exp(a))) {
+        xe_.on = true;
+        xe_.side = single_exp(b) ? 1 : 0;
+        const int x_node = t_.a[xe_.side == 1 ? b : a];
+        xe_.tx = [this, x_node](int j) { return tname(x_node, j); };
+      }
       tangent("    ", op, "t" + std::to_string(i) + "_", ms(true), deplist(i), "v" + std::to_string(i) + ms(true), x, y,
               [&](int j) { return tname(a, j); }, [&](int j) { return b >= 0 ? tname(b, j) : std::string(); });
+      xe_ = ExpFactor();
     }
   }
 }
@@ -1199,8 +1231,20 @@ void Emitter::tsegment(int U, const std::string& sg) {
         std::function<std::string(int)> ta, tb;
         body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
         body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
+        xe_ = ExpFactor();
+        if (op == NT_OP_MUL) {
+          const bool bx = L_.kind_b[j] == ARG_BODY && single_body_exp(L_.ref_b[j]);
+          const bool ax = L_.kind_a[j] == ARG_BODY && single_body_exp(L_.ref_a[j]);
+          if ((bx || ax) && !(L_.kind_a[j] == L_.kind_b[j] && L_.ref_a[j] == L_.ref_b[j])) {
+            xe_.on = true;
+            xe_.side = bx ? 1 : 0;
+            const int ep = bx ? L_.ref_b[j] : L_.ref_a[j];
+            body_tangent_operand(u, L_.kind_a[ep], L_.ref_a[ep], xe_.tx);
+          }
+        }
         tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", ms(true), posdeplist(j),
                 name + ms(true), x, y, ta, tb);
+        xe_ = ExpFactor();
       }
     }
   }
@@ -1218,6 +1262,28 @@ void Emitter::tsegment(int U, const std::string& sg) {
     }
   }
   o_ << "    }\n";
+}
+
+void Emitter::count_uses() {
+  uses_.assign(t_.n, 0);
+  for (int i = 0; i < t_.n; ++i) {
+    const int ar = arity(t_.op[i]);
+    if (ar >= 1) ++uses_[t_.a[i]];
+    if (ar >= 2) ++uses_[t_.b[i]];
+  }
+  for (int out : t_.outputs) ++uses_[out];
+  body_uses_.clear();
+  if (!L_.found) return;
+  body_uses_.assign(L_.period, 0);
+  for (int j = 0; j < L_.period; ++j) {
+    const int ar = arity(t_.op[L_.start + j]);
+    for (int slot = 0; slot < ar; ++slot) {
+      const int kind = slot == 0 ? L_.kind_a[j] : L_.kind_b[j];
+      const int ref = slot == 0 ? L_.ref_a[j] : L_.ref_b[j];
+      if (kind == ARG_BODY || kind == ARG_CARRY) ++body_uses_[ref];
+    }
+    if (L_.is_liveout[j]) ++body_uses_[j];
+  }
 }
 
 void Emitter::header() {
@@ -1386,6 +1452,7 @@ void Emitter::body_reverse() {
 }
 
 std::string Emitter::run() {
+  count_uses();
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;
   const bool tangent = p_.mode == NT_MODE_TANGENT;
