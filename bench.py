@@ -58,7 +58,7 @@ def measured_traffic(precision: str, info: dict) -> dict | None:
     return None
 
 
-def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5):
+def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2"):
     from nablatensor_amd import flops
 
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode)) as x:
@@ -80,7 +80,8 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
         wall = time.perf_counter() - t0
     fl = flops.flops_per_scenario(flat, precision)
     avg_replay_s = sum(replay_ms) / len(replay_ms) / 1e3
-    traffic = measured_traffic(precision, info) if paths == 2_000_000 else None
+    # The committed counter summaries cover the Asian 252-fixing tape at 2,000,000 scenarios.
+    traffic = measured_traffic(precision, info) if workload == "C2" and paths == 2_000_000 else None
     achieved = fl * paths / avg_replay_s / 1e12
     peak = flops.PEAK_TFLOPS[precision]
     return {
@@ -178,7 +179,8 @@ def other_workload(rocm, args) -> int:
                "speedup_vs_separate": m["speedup_vs_separate"], "mode": m["mode"]}
         print(json.dumps(out), flush=True)
         return 0
-    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp)
+    m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp,
+                args.workload)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

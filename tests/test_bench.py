@@ -13,7 +13,7 @@ sys.path.insert(0, str(conftest.ROOT))
 import bench  # noqa: E402
 
 
-def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5):
+def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2"):
     ms = 2.0 if precision == "fp64" else 1.0
     resolved = "reverse" if mode == 1 else "tangent"
     return {"value": paths / (ms / 1e3), "ms_per_step": ms, "kernel_ms": ms, "replay_kernel_ms": ms,
@@ -77,3 +77,23 @@ def test_markets_line(patched, monkeypatch, capsys):
         "mode": "tangent", "speedup_vs_separate": 2.0})
     out = run_main(monkeypatch, capsys, ["--workload", "C2", "--markets", "4", "--steps", "1", "--warmup", "0"])
     assert out["unit"] == "market-scenarios/s" and out["config"]["markets"] == 4
+
+
+def plan_of(source: str) -> dict:
+    line = next(ln for ln in source.splitlines() if ln.startswith("// nt-plan:"))
+    return dict(kv.split("=") for kv in line.split()[2:])
+
+
+@pytest.mark.parametrize("precision,mode", [("fp64", 0), ("fp64", 1), ("fp32", 0)])
+def test_committed_counters_cover_the_planned_headline_kernels(tapes, precision, mode):
+    """The traffic figure bench.py reports comes from the committed rocprofv3
+    summary of the exact kernel configuration the engine plans today; a change
+    of plan that leaves it unmeasured fails here rather than printing null."""
+    from nablatensor_amd import rocm
+
+    plan = plan_of(rocm.lower(tapes["C2"], rocm.options(precision, mode=mode)))
+    info = {"mode": 2 if plan["mode"] == "tangent" else 1, "checkpoint": int(plan["ckpt"]),
+            "seg_len": int(plan["seg"])}
+    traffic = bench.measured_traffic(precision, info)
+    assert traffic is not None, (precision, plan)
+    assert traffic["bytes"] > 0
