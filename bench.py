@@ -195,6 +195,82 @@ def other_workload(rocm, args) -> int:
     return 0
 
 
+def host_overheads(rocm, args) -> int:
+    """Host-path costs around the replay kernel on the Asian 252 tape, fp64:
+    building an executable (lowering + hipRTC compile, or a code-object cache
+    hit), the host time each dispatch adds to its kernels, and a chunked
+    replaySafe request through the engine layer against the kernel-only rate.
+    The reference's counterparts: the 0.5 s chunking with calibration probes
+    (AbstractAadExecutable.java:100-159, RocmAadEngine.java:85) and
+    synchronous null-stream dispatches (HipRuntime.java:40-43)."""
+    import tempfile
+
+    import nablatensor_amd as nt
+
+    flat = workload_tape("C2")
+    opts = rocm.options("fp64")
+    saved = os.environ.get("NABLATENSOR_ROCM_CACHE")
+    compile_s = {}
+    try:
+        with tempfile.TemporaryDirectory() as d:
+            for label, cache in (("uncached", "off"), ("cache_miss", d), ("cache_hit", d)):
+                os.environ["NABLATENSOR_ROCM_CACHE"] = cache
+                t0 = time.perf_counter()
+                with rocm.Executable(flat, opts) as x:
+                    compile_s[label] = {"create_s": time.perf_counter() - t0,
+                                        "compile_s": x.info()["compile_seconds"]}
+    finally:
+        if saved is None:
+            os.environ.pop("NABLATENSOR_ROCM_CACHE", None)
+        else:
+            os.environ["NABLATENSOR_ROCM_CACHE"] = saved
+    print(f"[bench] create: {compile_s}", file=sys.stderr, flush=True)
+
+    dispatch = {}
+    for name, paths in (("C1", 1_000_000), ("C2", 2_000_000)):
+        with rocm.Executable(workload_tape(name), opts) as x:
+            t_ramp = time.perf_counter()
+            while time.perf_counter() - t_ramp < args.ramp:
+                x.replay(paths, 0, args.seed)
+            rows = []
+            for k in range(max(args.steps, 5)):
+                t0 = time.perf_counter()
+                _, tm = x.replay(paths, k * paths, args.seed)
+                rows.append((time.perf_counter() - t0, tm["kernel_ms"] / 1e3, tm["replay_ms"] / 1e3))
+        n = len(rows)
+        wall = sum(r[0] for r in rows) / n
+        kernels = sum(r[1] for r in rows) / n
+        dispatch[name] = {"paths": paths, "wall_ms": wall * 1e3, "kernels_ms": kernels * 1e3,
+                          "replay_kernel_ms": sum(r[2] for r in rows) / n * 1e3,
+                          "host_overhead_us": (wall - kernels) * 1e6}
+        print(f"[bench] dispatch {name}: {dispatch[name]}", file=sys.stderr, flush=True)
+
+    total = args.host_paths
+    mc = (nt.MonteCarlo.of(nt.Products.asianCall()).market(nt.EquityMarket.atmOneYear())
+          .steps(252).greeks().fp64().on("rocm").build())
+    exe = mc.executable()
+    t0 = time.perf_counter()
+    exe.calibrate(args.seed)
+    calib = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    res = exe.replaySafe(total, args.seed)
+    safe = time.perf_counter() - t0
+    chunk = exe.measuredPathsPerSecond() * exe.maxChunkSeconds()
+    mc.close()
+    kernel_rate = dispatch["C2"]["paths"] / (dispatch["C2"]["kernels_ms"] / 1e3)
+    out = {"metric": "scenarios/sec of a chunked replaySafe request (fp64), end to end on the host",
+           "value": total / safe, "unit": "scenarios/s", "n_gpus": 1, "steps": 1, "warmup": 0,
+           "ms_per_step": safe * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f64", "data": f"synthetic (Philox2x32-10 normals, seed {args.seed})",
+           "config": {"workload": f"{WORKLOAD}, replaySafe over {total:,} scenarios (0.5 s chunks)"},
+           "replay_safe": {"paths": total, "seconds": safe, "chunk_paths_at_end": int(chunk),
+                           "calibration_s": calib,
+                           "vs_kernel_rate": total / safe / kernel_rate, "price": res.value()},
+           "create": compile_s, "dispatch": dispatch}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,6 +297,11 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
+    ap.add_argument("--host", action="store_true",
+                    help="only measure the host path around the kernel (executable creation with and without the "
+                         "code-object cache, per-dispatch host time, a chunked replaySafe request) and print its line")
+    ap.add_argument("--host-paths", type=int, default=4_000_000_000,
+                    help="scenarios in the --host replaySafe request")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
@@ -235,6 +316,8 @@ def main() -> int:
     if rocm.probe() < 1:
         print("no gfx950 device visible", file=sys.stderr)
         return 1
+    if args.host:
+        return host_overheads(rocm, args)
     if args.workload != "C2" or args.precision or args.markets > 1:
         return other_workload(rocm, args)
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()

@@ -55,8 +55,9 @@ typedef struct nt_tape {
   const int32_t *input_node;
   int32_t n_outputs;
   const int32_t *output_node;
-  int32_t n_streams;        /* random streams; this engine supports 1 */
-  int32_t n_uniforms;       /* RANDU draws; this engine supports 0 */
+  int32_t n_streams;        /* random streams (AadTape.randStreamCount), at least 1; stream 0 is the default */
+  int32_t n_uniforms;       /* RANDU draws on the default stream (AadTape.randUniformCount(0)); informational,
+                               the lowering reads every draw from its node */
 } nt_tape;
 
 enum { NT_FP64 = 0, NT_FP32 = 1 };

@@ -282,7 +282,6 @@ struct MarketVariant {
   hipFunction_t fn = nullptr, fn_finish = nullptr;
   double* d_inputs = nullptr;
   double* d_partials = nullptr;
-  double* d_sums = nullptr;
 };
 
 struct nt_exec {
@@ -296,7 +295,8 @@ struct nt_exec {
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   double* d_inputs = nullptr;
   double* d_partials = nullptr;
-  double* d_sums = nullptr;
+  double* h_sums = nullptr;  // pinned host rows the finishing kernels write the sums to
+  size_t h_cap = 0;          // doubles in h_sums
   void* d_scratch = nullptr;
   int dev = 0;
   int grid_cap = 1;
@@ -398,7 +398,9 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   const int nch = x->low.plan.n_channels;
   NT_HIP(hipMalloc(&x->d_inputs, sizeof(double) * std::max(1, x->low.ir.n_in)), "hipMalloc(inputs)");
   NT_HIP(hipMalloc(&x->d_partials, sizeof(double) * static_cast<size_t>(x->grid_cap) * nch), "hipMalloc(partials)");
-  NT_HIP(hipMalloc(&x->d_sums, sizeof(double) * nch), "hipMalloc(sums)");
+  NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_sums), sizeof(double) * nch, hipHostMallocDefault),
+         "hipHostMalloc(sums)");
+  x->h_cap = static_cast<size_t>(nch);
   const size_t elem = x->low.plan.precision == NT_FP32 ? sizeof(float) : sizeof(double);
   const size_t scratch = static_cast<size_t>(x->low.plan.tape_slots) * x->grid_cap * x->low.plan.block * elem;
   if (scratch > 0) NT_HIP(hipMalloc(&x->d_scratch, scratch), "hipMalloc(scratch)");
@@ -456,6 +458,17 @@ static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t 
   return NT_OK;
 }
 
+// Finishing pass over the `grid` partial rows of one replay launch: `nch` sums
+// written to host memory `out` (pinned, read after the stream drains).
+static int launch_finish(nt_exec* x, hipFunction_t fn, double* d_partials, int grid, int nch, double* out) {
+  unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
+  const unsigned threads = 64u * static_cast<unsigned>(std::min(std::max(nch, 1), 16));
+  void* args[] = {&d_partials, &blocks, &nchu, &out};
+  NT_HIP(hipModuleLaunchKernel(fn, 1, 1, 1, threads, 1, 1, 0, x->stream, args, nullptr),
+         "hipModuleLaunchKernel(nt_finish)");
+  return NT_OK;
+}
+
 int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, double* sums, int32_t n_sums,
                    double* timing) {
   if (!x) return fail(NT_E_CLOSED, "executable is closed");
@@ -469,13 +482,11 @@ int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, d
   int rc = launch_replay(x, x->fn, paths, offset, seed, nullptr, nullptr, grid);
   if (rc != NT_OK) return rc;
   NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
-  unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
-  void* fargs[] = {&x->d_partials, &blocks, &nchu, &x->d_sums};
-  NT_HIP(hipModuleLaunchKernel(x->fn_finish, 1, 1, 1, 256, 1, 1, 0, x->stream, fargs, nullptr),
-         "hipModuleLaunchKernel(nt_finish)");
+  rc = launch_finish(x, x->fn_finish, x->d_partials, grid, nch, x->h_sums);
+  if (rc != NT_OK) return rc;
   NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
-  NT_HIP(hipMemcpyAsync(sums, x->d_sums, sizeof(double) * nch, hipMemcpyDeviceToHost, x->stream), "hipMemcpyAsync(sums)");
   NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  std::memcpy(sums, x->h_sums, sizeof(double) * nch);
   if (timing) {
     float all = 0, rep = 0;
     NT_HIP(hipEventElapsedTime(&all, x->ev[0], x->ev[2]), "hipEventElapsedTime");
@@ -517,9 +528,7 @@ static int market_variant(nt_exec* x, int markets, MarketVariant*& out) {
   if (e == hipSuccess) e = hipModuleGetFunction(&v.fn_finish, v.mod, "nt_finish");
   if (e == hipSuccess) e = hipMalloc(&v.d_inputs, sizeof(double) * std::max<size_t>(1, static_cast<size_t>(nin) * markets));
   if (e == hipSuccess) e = hipMalloc(&v.d_partials, sizeof(double) * static_cast<size_t>(x->grid_cap) * nch);
-  if (e == hipSuccess) e = hipMalloc(&v.d_sums, sizeof(double) * nch);
   if (e != hipSuccess) {
-    if (v.d_sums) (void)hipFree(v.d_sums);
     if (v.d_partials) (void)hipFree(v.d_partials);
     if (v.d_inputs) (void)hipFree(v.d_inputs);
     (void)hipModuleUnload(v.mod);
@@ -572,6 +581,17 @@ int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, u
   const auto t0 = std::chrono::steady_clock::now();
   NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
   const bool shared = x->low.plan.mode == NT_MODE_TANGENT;
+  const size_t need = static_cast<size_t>(nch) * markets;
+  if (x->h_cap < need) {
+    // Every launch below writes its own rows; the stream is idle between calls, so the old rows are free.
+    NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+    double* grown = nullptr;
+    NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&grown), sizeof(double) * need, hipHostMallocDefault),
+           "hipHostMalloc(sums)");
+    (void)hipHostFree(x->h_sums);
+    x->h_sums = grown;
+    x->h_cap = need;
+  }
   NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");
   int grid = 0;
   if (shared) {
@@ -591,16 +611,10 @@ int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, u
       }
       rc = launch_kernel(x, v->fn, v->d_inputs, v->d_partials, paths, offset, seed, nullptr, nullptr, grid);
       if (rc != NT_OK) return rc;
-      unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch * k);
-      void* fargs[] = {&v->d_partials, &blocks, &nchu, &v->d_sums};
-      NT_HIP(hipModuleLaunchKernel(v->fn_finish, 1, 1, 1, 256, 1, 1, 0, x->stream, fargs, nullptr),
-             "hipModuleLaunchKernel(nt_finish)");
-      NT_HIP(hipMemcpyAsync(sums + static_cast<size_t>(m0) * nch, v->d_sums, sizeof(double) * nch * k,
-                            hipMemcpyDeviceToHost, x->stream),
-             "hipMemcpyAsync(sums)");
+      rc = launch_finish(x, v->fn_finish, v->d_partials, grid, nch * k, x->h_sums + static_cast<size_t>(m0) * nch);
+      if (rc != NT_OK) return rc;
     }
     NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
-    NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
   } else {
     // The reverse sweep keeps one set's state per lane: replay the sets in turn.
     if (!x->d_set_inputs) NT_HIP(hipMalloc(&x->d_set_inputs, sizeof(double) * std::max(1, nin)), "hipMalloc(set inputs)");
@@ -612,25 +626,19 @@ int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, u
       }
       int rc = launch_kernel(x, x->fn, x->d_set_inputs, x->d_partials, paths, offset, seed, nullptr, nullptr, grid);
       if (rc != NT_OK) return rc;
-      unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
-      void* fargs[] = {&x->d_partials, &blocks, &nchu, &x->d_sums};
-      NT_HIP(hipModuleLaunchKernel(x->fn_finish, 1, 1, 1, 256, 1, 1, 0, x->stream, fargs, nullptr),
-             "hipModuleLaunchKernel(nt_finish)");
-      NT_HIP(hipMemcpyAsync(sums + static_cast<size_t>(m) * nch, x->d_sums, sizeof(double) * nch, hipMemcpyDeviceToHost,
-                            x->stream),
-             "hipMemcpyAsync(sums)");
+      rc = launch_finish(x, x->fn_finish, x->d_partials, grid, nch, x->h_sums + static_cast<size_t>(m) * nch);
+      if (rc != NT_OK) return rc;
     }
     NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
-    NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
   }
   NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  std::memcpy(sums, x->h_sums, sizeof(double) * need);
   if (timing) {
-    float all = 0, rep = 0;
-    NT_HIP(hipEventElapsedTime(&all, x->ev[0], x->ev[2]), "hipEventElapsedTime");
-    NT_HIP(hipEventElapsedTime(&rep, x->ev[0], x->ev[1]), "hipEventElapsedTime");
-    timing[0] = all;
+    float ms = 0;
+    NT_HIP(hipEventElapsedTime(&ms, x->ev[0], x->ev[1]), "hipEventElapsedTime");
+    timing[0] = ms;
     timing[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    timing[2] = rep;
+    timing[2] = ms;
   }
   return NT_OK;
 }
@@ -694,12 +702,11 @@ int nt_exec_destroy(nt_exec* x) {
   }
   if (x->stream) (void)hipStreamDestroy(x->stream);
   if (x->d_scratch) (void)hipFree(x->d_scratch);
-  if (x->d_sums) (void)hipFree(x->d_sums);
+  if (x->h_sums) (void)hipHostFree(x->h_sums);
   if (x->d_partials) (void)hipFree(x->d_partials);
   if (x->d_inputs) (void)hipFree(x->d_inputs);
   for (auto& kv : x->markets) {
     MarketVariant& v = kv.second;
-    if (v.d_sums) (void)hipFree(v.d_sums);
     if (v.d_partials) (void)hipFree(v.d_partials);
     if (v.d_inputs) (void)hipFree(v.d_inputs);
     if (v.mod) (void)hipModuleUnload(v.mod);

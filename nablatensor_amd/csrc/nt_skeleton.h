@@ -270,30 +270,29 @@ __device__ __forceinline__ void nt_block_store(const double (&acc)[NCH], double*
     if (lane == 0) lds[c * waves + wave] = w;
   }
   __syncthreads();
-  if (threadIdx.x < NCH) {
-    const int c = threadIdx.x;
+  for (int c = threadIdx.x; c < NCH; c += blockDim.x) {
     double s = 0.0;
     for (int w = 0; w < waves; ++w) s += lds[c * waves + w];
     partials[static_cast<nt_u64>(blockIdx.x) * NCH + c] = s;
   }
 }
 
-// Second pass: out[c] = sum over blocks of partials[b * nch + c], one block of
-// 256 threads, fixed assignment and fixed tree order (deterministic).
-extern "C" __global__ __launch_bounds__(256) void nt_finish(const double* __restrict__ partials, nt_u32 blocks,
-                                                          nt_u32 nch, double* __restrict__ out) {
-  __shared__ double red[256];
-  for (nt_u32 c = 0; c < nch; ++c) {
+// Second pass: out[c] = sum over blocks b of partials[b * nch + c], launched as
+// one block of 64 * min(nch, 16) threads. Wave w takes channels w, w + waves,
+// ...; lane l adds blocks l, l + 64, ... in order and the wave adds its 64 lane
+// sums by the fixed butterfly, with no block barrier. The order depends only on
+// the block count, so a channel's result is bitwise the same whatever nch is (a
+// market's sums do not change with the markets priced beside it) and run to
+// run. `out` is host memory the caller reads after the stream has drained.
+extern "C" __global__ __launch_bounds__(1024) void nt_finish(const double* __restrict__ partials, nt_u32 blocks,
+                                                           nt_u32 nch, double* __restrict__ out) {
+  const nt_u32 lane = threadIdx.x & 63;
+  const nt_u32 waves = blockDim.x >> 6;
+  for (nt_u32 c = threadIdx.x >> 6; c < nch; c += waves) {
     double s = 0.0;
-    for (nt_u32 b = threadIdx.x; b < blocks; b += 256) s += partials[static_cast<nt_u64>(b) * nch + c];
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-      if (static_cast<int>(threadIdx.x) < w) red[threadIdx.x] += red[threadIdx.x + w];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) out[c] = red[0];
-    __syncthreads();
+    for (nt_u32 b = lane; b < blocks; b += 64) s += partials[static_cast<nt_u64>(b) * nch + c];
+    s = nt_wave_sum(s);
+    if (lane == 0) out[c] = s;
   }
 }
 

@@ -108,12 +108,34 @@ class TapeArrays:
         self.n_streams = int(flat.get("n_streams", 1))
         self.n_uniforms = int(flat.get("n_uniforms", 0))
 
+    def wire_bytes(self) -> bytes:
+        """The tape's canonical byte form: the nt_tape fields in struct order,
+        little-endian (int32 counts and indices, IEEE-754 binary64 constants):
+        n_nodes, op, arg_a, arg_b, constant, n_inputs, input_node, n_outputs,
+        output_node, n_streams, n_uniforms. These are FlatTape's arrays
+        (FlatTape.java:37-79) minus `active`, which the engine derives itself;
+        a foreign-function adapter hashes the same bytes of what it marshals."""
+        i32 = lambda v: np.asarray(v, dtype="<i4").tobytes()
+        n = len(self.op)
+        return b"".join([i32([n]), i32(self.op), i32(self.arg_a), i32(self.arg_b),
+                         np.asarray(self.constant, dtype="<f8").tobytes(), i32([len(self.input_node)]),
+                         i32(self.input_node), i32([len(self.output_node)]), i32(self.output_node),
+                         i32([self.n_streams, self.n_uniforms])])
+
     def struct(self) -> NtTape:
         p32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
         return NtTape(len(self.op), p32(self.op), p32(self.arg_a), p32(self.arg_b),
                       self.constant.ctypes.data_as(C.POINTER(C.c_double)), len(self.input_node),
                       p32(self.input_node), len(self.output_node), p32(self.output_node),
                       self.n_streams, self.n_uniforms)
+
+
+def wire_digest(flat: dict) -> str:
+    """SHA-256 (hex) of TapeArrays.wire_bytes: the identity of a tape as it
+    crosses the C ABI."""
+    import hashlib
+
+    return hashlib.sha256(TapeArrays(flat).wire_bytes()).hexdigest()
 
 
 def options(precision: str = "fp64", adjoints: bool = True, block: int = 0, max_blocks: int = 0,
