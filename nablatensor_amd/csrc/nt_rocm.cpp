@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 #include <sys/stat.h>
+#include <utime.h>
 
 #include <algorithm>
 #include <chrono>
@@ -129,6 +130,7 @@ int compile_hiprtc(const std::string& src, bool dump, std::vector<char>& code, d
   const std::string dir = cache_dir();
   const std::string path = dir.empty() ? "" : dir + "/" + hex + ".co";
   if (!path.empty() && read_file(path, code)) {
+    (void)utime(path.c_str(), nullptr);  // marks the entry as in use (build() prunes entries it did not touch)
     seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     return NT_OK;
   }
