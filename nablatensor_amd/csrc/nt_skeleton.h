@@ -79,11 +79,12 @@ __device__ __forceinline__ void nt_tables_load() {
   __syncthreads();
 }
 
-// exp(x) by Tang's table-driven method: x = (64 m + j) ln2/64 + r with
-// |r| <= ln2/128 (ln2/64 split in a 32-bit head and a tail, so the reduction
+// exp(x) by Tang's table-driven method: x = (256 m + j) ln2/256 + r with
+// |r| <= ln2/512 (ln2/256 split in a 32-bit head and a tail, so the reduction
 // keeps r to one rounding), exp(x) = 2^m (T_j + T_j p(r)) with T_j =
-// 2^(j/64) as head + tail and p(r) = exp(r) - 1 through r^6. Below 1 ulp.
-// k = 64 m + j comes out of the low word of x 64/ln2 + 1.5 * 2^52 (rounded
+// 2^(j/256) as head + tail and p(r) = exp(r) - 1 through r^4 (truncation
+// r^5/120 < 4e-17 relative). Below 1 ulp.
+// k = 256 m + j comes out of the low word of x 256/ln2 + 1.5 * 2^52 (rounded
 // to an integer by that addition), so no float-to-int conversion is needed.
 // The result is exact only for |x| <= 708 (results in the normal range);
 // outside it (and for infinities and NaN) it is garbage but harmless (the
@@ -95,11 +96,9 @@ __device__ __forceinline__ double nt_exp_fast(double x, bool& bad) {
   const int k = static_cast<int>(nt_lo(t));
   double r = fma(-kd, NT_EXP_L_HI, x);
   r = fma(-kd, NT_EXP_L_LO, r);
-  const int j = k & 63;
-  const int m = k >> 6;
-  double q = fma(r, NT_EXP_C6, NT_EXP_C5);
-  q = fma(r, q, NT_EXP_C4);
-  q = fma(r, q, NT_EXP_C3);
+  const int j = k & 255;
+  const int m = k >> 8;
+  double q = fma(r, NT_EXP_C4, NT_EXP_C3);
   q = fma(r, q, NT_EXP_C2);
   const double p = fma(r * r, q, r);
   const double th = nt_tables.ex.t[2 * j];
