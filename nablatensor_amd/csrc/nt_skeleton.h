@@ -115,10 +115,10 @@ __device__ __forceinline__ double nt_exp(double x) {
 }
 
 // -2 ln(u) for u = (c + 0.5) * 2^-32, by Tang's table-driven method: u = 2^e x
-// with x in [sqrt(1/2), sqrt(2)), F = x rounded to 7 fractional bits of its
-// binade (rounding the high word at bit 13 moves F = 2 - 2^-7 up to the next
+// with x in [sqrt(1/2), sqrt(2)), F = x rounded to 8 fractional bits of its
+// binade (rounding the high word at bit 12 moves F = 2 - 2^-8 up to the next
 // binade exactly), ln u = e ln2 + ln F + ln(1 + r), r = (x - F) / F,
-// |r| <= 2^-8. x - F is exact and F = 1 near u = 1, so ln u keeps full
+// |r| <= 2^-9. x - F is exact and F = 1 near u = 1, so ln u keeps full
 // relative accuracy there. Tables and constants carry the factor -2 (exact).
 __device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
   const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
@@ -126,11 +126,10 @@ __device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
   const int e = static_cast<int>(hx >> 20) - 0x3FF;
   hx = (hx & 0x000FFFFFu) + 0x3FE6A09Eu;
   const double x = nt_mk(hx, nt_lo(u));
-  const nt_u32 fhi = (hx + 0x1000u) & 0xFFFFE000u;
-  const nt_u32 idx = (fhi - 0x3FE6A000u) >> 13;
+  const nt_u32 fhi = (hx + 0x800u) & 0xFFFFF000u;
+  const nt_u32 idx = (fhi - 0x3FE6A000u) >> 12;
   const double r = (x - nt_mk(fhi, 0u)) * nt_tables.lg.inv[idx];  // r' = -2 (x - F) / F
-  double q = fma(r, NT_LOGQ_5, NT_LOGQ_4);
-  q = fma(r, q, NT_LOGQ_3);
+  double q = fma(r, NT_LOGQ_4, NT_LOGQ_3);
   q = fma(r, q, NT_LOGQ_2);
   q = fma(r, q, NT_LOGQ_1);
   q = fma(r, q, NT_LOGQ_0);
@@ -156,24 +155,22 @@ __device__ __forceinline__ double nt_sqrt_pos(double a) {
 
 // sin and cos of theta = fl(6.283185307179586 * u) for u = (c + 0.5) * 2^-32.
 // The reference rounds its angle once, and so does this (theta is that
-// rounded product). The circle is cut in 256 sectors: c = j 2^24 + d with d
-// the sign-extended low 24 bits, so u = j/256 + f exactly, f = (d + 0.5)
-// 2^-32, |f| <= 2^-9 turns. With (S, C) = (sin, cos)(2 pi j/256) from the
+// rounded product). The circle is cut in 512 sectors: c = j 2^23 + d with d
+// the sign-extended low 23 bits, so u = j/512 + f exactly, f = (d + 0.5)
+// 2^-32, |f| <= 2^-10 turns. With (S, C) = (sin, cos)(2 pi j/512) from the
 // table, sin(2 pi u) = S cos(2 pi f) + C sin(2 pi f) and cos(2 pi u) =
 // C cos(2 pi f) - S sin(2 pi f), the small-angle parts being polynomials in
 // f. The rounding of theta, eps = theta - 2 pi u, is known exactly (two FMAs)
 // and enters as sin(2 pi f + eps) = sin(2 pi f) + eps to first order (the
 // second-order terms are below 1e-17).
 __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& co) {
-  const int d = static_cast<int>(c << 8) >> 8;
-  const nt_u32 j = (c - static_cast<nt_u32>(d)) >> 24;
+  const int d = static_cast<int>(c << 9) >> 9;
+  const nt_u32 j = (c - static_cast<nt_u32>(d)) >> 23;
   const double f = fma(static_cast<double>(d), 0x1p-32, 0x1p-33);
   const double t = f * f;
-  double ps = fma(t, NT_SC_S7, NT_SC_S5);
-  ps = fma(t, ps, NT_SC_S3);
+  double ps = fma(t, NT_SC_S5, NT_SC_S3);
   ps = fma(t, ps, NT_SC_S1);
-  double cq = fma(t, NT_SC_C6, NT_SC_C4);
-  cq = fma(t, cq, NT_SC_C2);
+  const double cq = fma(t, NT_SC_C4, NT_SC_C2);
   const double cm = t * cq;  // cos(2 pi f) - 1
   const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
   const double theta = NT_TWO_PI_D * u;

@@ -55,8 +55,8 @@ def sample_u32(n: int, seed: int) -> np.ndarray:
     rng = np.random.default_rng(seed)
     edges = [0, 1, 2, 3, 2**29 - 1, 2**29, 2**29 + 1, 2**30 - 1, 2**30, 2**31 - 1, 2**31, 3 * 2**30 - 1,
              3 * 2**30, 2**32 - 2**29 - 1, 2**32 - 2**29, 2**32 - 3, 2**32 - 2, 2**32 - 1]
-    # both sides of the sine/cosine table's sector boundaries (j 2^24 +- 2^23)
-    sectors = [j * 2**24 + 2**23 + o for j in range(0, 256, 17) for o in (-1, 0, 1)]
+    # both sides of the sine/cosine table's sector boundaries (j 2^23 +- 2^22)
+    sectors = [j * 2**23 + 2**22 + o for j in range(0, 512, 17) for o in (-1, 0, 1)]
     sectors = [v % 2**32 for v in sectors]
     return _u32(np.concatenate([edges, sectors, rng.integers(0, 2**32, n, dtype=np.uint64)]))
 
