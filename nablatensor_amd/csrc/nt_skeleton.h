@@ -233,8 +233,10 @@ __device__ __forceinline__ void nt_normal_pair(nt_u32 lo, nt_u32 hi, nt_u32 ctr,
 __device__ __forceinline__ void nt_normal_pair(nt_u32 lo, nt_u32 hi, nt_u32 ctr, float& zc, float& zs) {
   nt_u32 c0, c1;
   nt_philox(lo, hi ^ ctr, c0, c1);
-  const float u1 = (static_cast<float>(c0) + 0.5f) * 2.3283064365386963e-10f;
-  const float u2 = (static_cast<float>(c1) + 0.5f) * 2.3283064365386963e-10f;
+  // (float(c) + 0.5f) * 2^-32 in one rounding: the same float for every c
+  // (exact below 2^24; above, both round the same tie or sub-half-ulp term).
+  const float u1 = fmaf(static_cast<float>(c0), 0x1p-32f, 0x1p-33f);
+  const float u2 = fmaf(static_cast<float>(c1), 0x1p-32f, 0x1p-33f);
   const float r = nt_hw_sqrtf(-1.38629436111989061f * nt_hw_log2f(u1));  // -2 ln 2 * log2(u1)
   zc = r * nt_hw_cos2pif(u2);
   zs = r * nt_hw_sin2pif(u2);

@@ -161,7 +161,10 @@ static void run_range(const nto_tape *t, const uint8_t *active, const double *in
   double *v = (double *)malloc(sizeof(double) * (size_t)n);
   double *d = (double *)malloc(sizeof(double) * (size_t)n);
   stream_state *rng = (stream_state *)malloc(sizeof(stream_state) * (size_t)t->n_streams);
-  for (uint64_t path = from; path < from + count; path++) {
+  /* Path indices wrap modulo 2^64, as the reference's long arithmetic does
+   * (offset + i); counting by i keeps a range that crosses 2^64 whole. */
+  for (uint64_t i = 0; i < count; i++) {
+    const uint64_t path = from + i;
     for (int32_t s = 0; s < t->n_streams; s++) {
       stream_init(&rng[s], path, seed, s);
     }

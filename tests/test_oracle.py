@@ -271,3 +271,15 @@ def test_multi_output_sums_are_one_sweep_per_output(nt):
     assert s[1][0] == 2 * s[0][0] and s[1][1] == 4 * s[0][1] and s[1][2] == 2 * s[0][2]
     v, g = oracle.replay_paths(flat, 50, 0, 3, output=None)
     assert np.array_equal(v[:, 1], 2 * v[:, 0]) and np.array_equal(g[:, 1, :], 2 * g[:, 0, :])
+
+
+def test_path_ranges_wrap_modulo_two_to_the_64(tapes):
+    """Path indices are offset + i modulo 2^64 (the reference's long
+    arithmetic): a range that crosses 2^64 is the range up to it plus the
+    range from 0, whichever worker thread's chunk holds the crossing."""
+    t = tapes["C2"]
+    for threads in (1, 16):
+        whole = oracle.replay_sums(t, 4000, 2**64 - 1500, 11, threads=threads)
+        head = oracle.replay_sums(t, 1500, 2**64 - 1500, 11, threads=threads)
+        tail = oracle.replay_sums(t, 2500, 0, 11, threads=threads)
+        assert np.allclose(whole, head + tail, rtol=1e-12, atol=0.0)
