@@ -623,9 +623,10 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   // normals, so both Box-Muller legs stay in one trip). Longer trips let the
   // scheduler overlap one step's Philox and transcendental latency with its
   // neighbour's arithmetic; shorter ones keep occupancy when the state is
-  // large. Measured on MI355X: Asian fp32 (10 registers of state) 4 steps
-  // beat 8; barrier fp64 (20) 2 beat 4 by 6%; the 16-asset worst-of fp32
-  // (65) 1 beat 2 by 16% (238 VGPRs, two waves per SIMD, instead of 260).
+  // large. Measured on MI355X: Asian fp32 (10 registers of state) 2 and 4
+  // steps tie and 8 is 7% slower; barrier fp32 2 beat 4 by 2%; Asian fp64
+  // (20) 2 beat 4 by 2.5%; barrier fp64 2 beat 4 by 5%; the 16-asset
+  // worst-of (65 fp32, 130 fp64) 1 beat 2 by 9% (fp32) and 5% (fp64).
   const int W = p.n_words;
   int live = 0;
   for (int j = 0; j < L.period; ++j) {
@@ -633,7 +634,7 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   }
   const int w = p.precision == NT_FP64 ? 2 : 1;
   const int regs = live * w * p.markets;
-  int seg = o.seg_len > 0 ? o.seg_len : (regs <= 16 ? 4 : regs <= 48 ? 2 : 1);
+  int seg = o.seg_len > 0 ? o.seg_len : (regs <= 8 ? 4 : regs <= 48 ? 2 : 1);
   if (L.need_even && (seg & 1)) seg += 1;
   seg = std::max(1, std::min(seg, L.iters));
   p.seg = seg;
