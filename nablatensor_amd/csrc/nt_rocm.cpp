@@ -307,6 +307,31 @@ struct nt_exec {
   std::map<int, MarketVariant> markets;  // by set count
   int market_chunk = 0;                  // input sets per multi-market dispatch, 0 until chosen
   double* d_set_inputs = nullptr;        // one input set at a time (reverse-sweep executables)
+
+  nt_exec() = default;
+  nt_exec(const nt_exec&) = delete;
+  nt_exec& operator=(const nt_exec&) = delete;
+  // Releases whatever was acquired, so a create that fails part way frees it too.
+  ~nt_exec() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& e : ev) {
+      if (e) (void)hipEventDestroy(e);
+    }
+    if (stream) (void)hipStreamDestroy(stream);
+    if (d_scratch) (void)hipFree(d_scratch);
+    if (h_sums) (void)hipHostFree(h_sums);
+    if (d_partials) (void)hipFree(d_partials);
+    if (d_inputs) (void)hipFree(d_inputs);
+    for (auto& kv : markets) {
+      MarketVariant& v = kv.second;
+      if (v.d_partials) (void)hipFree(v.d_partials);
+      if (v.d_inputs) (void)hipFree(v.d_inputs);
+      if (v.mod) (void)hipModuleUnload(v.mod);
+    }
+    if (d_set_inputs) (void)hipFree(d_set_inputs);
+    if (mod_dump) (void)hipModuleUnload(mod_dump);
+    if (mod) (void)hipModuleUnload(mod);
+  }
 };
 
 extern "C" {
@@ -697,26 +722,7 @@ int nt_exec_source(const nt_exec* x, char* source, int64_t* len) {
 }
 
 int nt_exec_destroy(nt_exec* x) {
-  if (!x) return NT_OK;
-  if (x->stream) (void)hipStreamSynchronize(x->stream);
-  for (auto& e : x->ev) {
-    if (e) (void)hipEventDestroy(e);
-  }
-  if (x->stream) (void)hipStreamDestroy(x->stream);
-  if (x->d_scratch) (void)hipFree(x->d_scratch);
-  if (x->h_sums) (void)hipHostFree(x->h_sums);
-  if (x->d_partials) (void)hipFree(x->d_partials);
-  if (x->d_inputs) (void)hipFree(x->d_inputs);
-  for (auto& kv : x->markets) {
-    MarketVariant& v = kv.second;
-    if (v.d_partials) (void)hipFree(v.d_partials);
-    if (v.d_inputs) (void)hipFree(v.d_inputs);
-    if (v.mod) (void)hipModuleUnload(v.mod);
-  }
-  if (x->d_set_inputs) (void)hipFree(x->d_set_inputs);
-  if (x->mod_dump) (void)hipModuleUnload(x->mod_dump);
-  if (x->mod) (void)hipModuleUnload(x->mod);
-  delete x;
+  delete x;  // ~nt_exec releases the device resources
   return NT_OK;
 }
 
