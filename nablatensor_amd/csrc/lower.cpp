@@ -8,6 +8,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <set>
 #include <sstream>
 
 namespace ntl {
@@ -815,6 +816,18 @@ class Emitter {
   bool single_body_exp(int pos) const {
     return t_.op[L_.start + pos] == NT_OP_EXP && body_uses_[pos] == 1 && !L_.is_liveout[pos] && !L_.is_carry[pos];
   }
+  // fp32 tangent loops: exp(p + r s) (or exp(r s)) with p and r loop-invariant
+  // and the sum and product used nowhere else becomes exp2(p' + r' s) with
+  // p' = p log2(e) and r' = r log2(e) computed once per path, dropping the
+  // per-step multiply by log2(e) that the hardware exp2 otherwise needs.
+  struct Exp2Fold {
+    bool on = false;
+    int p = -1, r = -1;          // invariant nodes (p = -1: no sum)
+    int s_kind = ARG_NONE, s_ref = -1;
+  };
+  std::vector<Exp2Fold> fold_;  // per loop position
+  void plan_exp2_folds();
+  std::string l2e_name(int node) const { return "v" + std::to_string(node) + "_l2e" + ms(t_.active[node]); }
   void tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx, const std::vector<int>& D,
                const std::string& Vi, const std::string& Va, const std::string& Vb,
                const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb);
@@ -1227,7 +1240,14 @@ void Emitter::tsegment(int U, const std::string& sg) {
         exp_active_ = act;
         const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], false) : "";
         const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], false) : "";
-        o_ << ind << "const real " << name << ms(act) << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+        std::string val = expr(op, x, y, t_.c[i], t_.a[i]);
+        if (op == NT_OP_EXP && fold_[j].on) {
+          const Exp2Fold& f = fold_[j];
+          const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
+          val = "nt_hw_exp2f(" + (f.p >= 0 ? "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")"
+                                           : l2e_name(f.r) + " * " + sv) + ")";
+        }
+        o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
         if (!act || ar == 0 || !p_.adjoints) continue;
         std::function<std::string(int)> ta, tb;
         body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
@@ -1263,6 +1283,40 @@ void Emitter::tsegment(int U, const std::string& sg) {
     }
   }
   o_ << "    }\n";
+}
+
+void Emitter::plan_exp2_folds() {
+  fold_.assign(L_.found ? L_.period : 0, Exp2Fold());
+  if (!f32_ || !L_.found || p_.mode != NT_MODE_TANGENT) return;
+  auto body_only = [&](int pos) { return body_uses_[pos] == 1 && !L_.is_liveout[pos] && !L_.is_carry[pos]; };
+  for (int j = 0; j < L_.period; ++j) {
+    if (t_.op[L_.start + j] != NT_OP_EXP || L_.kind_a[j] != ARG_BODY || !body_only(L_.ref_a[j])) continue;
+    const int a = L_.ref_a[j];
+    Exp2Fold f;
+    int mul = -1;
+    if (t_.op[L_.start + a] == NT_OP_ADD) {
+      for (int side = 0; side < 2 && mul < 0; ++side) {
+        const int ik = side ? L_.kind_b[a] : L_.kind_a[a], ir = side ? L_.ref_b[a] : L_.ref_a[a];
+        const int mk = side ? L_.kind_a[a] : L_.kind_b[a], mr = side ? L_.ref_a[a] : L_.ref_b[a];
+        if (ik == ARG_INV && mk == ARG_BODY && t_.op[L_.start + mr] == NT_OP_MUL && body_only(mr)) {
+          f.p = ir;
+          mul = mr;
+        }
+      }
+    } else if (t_.op[L_.start + a] == NT_OP_MUL) {
+      mul = a;
+    }
+    if (mul < 0) continue;
+    for (int side = 0; side < 2 && !f.on; ++side) {
+      const int ik = side ? L_.kind_b[mul] : L_.kind_a[mul], ir = side ? L_.ref_b[mul] : L_.ref_a[mul];
+      if (ik != ARG_INV) continue;
+      f.r = ir;
+      f.s_kind = side ? L_.kind_a[mul] : L_.kind_b[mul];
+      f.s_ref = side ? L_.ref_a[mul] : L_.ref_b[mul];
+      f.on = true;
+    }
+    if (f.on) fold_[j] = f;
+  }
 }
 
 void Emitter::count_uses() {
@@ -1356,6 +1410,19 @@ void Emitter::body_tangent() {
   const std::string one = f32_ ? "1.0f" : "1.0";
   tline(0, ls);
   if (loop) {
+    std::set<int> scaled;
+    for (const auto& f : fold_) {
+      if (!f.on) continue;
+      if (f.p >= 0) scaled.insert(f.p);
+      scaled.insert(f.r);
+    }
+    for (int node : scaled) {
+      const bool act = t_.active[node] != 0;
+      for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+        m_ = m;
+        o_ << "    const real " << l2e_name(node) << " = " << vname(node) << " * 1.44269504088896341f;\n";
+      }
+    }
     for (int j = 0; j < L_.period; ++j) {
       if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
       const int init = L_.is_carry[j] ? L_.carry_init[j] : -1;
@@ -1454,6 +1521,7 @@ void Emitter::body_reverse() {
 
 std::string Emitter::run() {
   count_uses();
+  plan_exp2_folds();
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;
   const bool tangent = p_.mode == NT_MODE_TANGENT;
