@@ -809,6 +809,26 @@ class Emitter {
     int side = 1;                                  // operand holding exp(x): 0 = a, 1 = b
     std::function<std::string(int)> tx;            // tangent of x
   } xe_;
+  // Tangents that are a plain product of two factors, by the name (or
+  // expression) that stands for them: a sum or difference with one of them
+  // becomes one fma instead of a multiply and an add.
+  mutable std::map<std::string, std::pair<std::string, std::string>> prod_;
+  // "(a * b)", recorded as a product for the fma peephole
+  std::string product(const std::string& a, const std::string& b) const {
+    const std::string e = "(" + a + " * " + b + ")";
+    prod_[e] = {a, b};
+    return e;
+  }
+  // Multiplicative carries (tangent loops): a carried value updated as
+  // c <- c exp(x), the exponential used nowhere else, keeps G = the product of
+  // the exp(x) since the loop began and sigma_k = t_k(loop start) + c0 sum tx_k,
+  // c0 its value at the loop start; its tangent is G sigma_k (exact: c = c0 G).
+  // Per step that is one fma per input and one multiply per carry, instead of
+  // an fma and a multiply per input, and a consumer's sum of G sigma_k is one
+  // fma. Tangents return to absolute form after the loop.
+  std::vector<char> geo_;  // per loop position
+  void plan_geo_carries();
+  bool geo(int pos) const { return pos >= 0 && pos < static_cast<int>(geo_.size()) && geo_[pos]; }
   std::vector<int> uses_;       // per node: operand references + outputs
   std::vector<int> body_uses_;  // per loop position: references within and across iterations, + live-out
   void count_uses();
@@ -1094,6 +1114,16 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
   const std::string FMA = f("fma");
   auto val = [&](const std::string& T) { return T == "#1" ? one : T; };
   auto mulv = [&](const std::string& T, const std::string& v) { return T == "#1" ? v : "(" + T + " * " + v + ")"; };
+  // a product P * Q in tangent j (recorded for the fma peephole below)
+  std::pair<std::string, std::string> pq;
+  auto prod = [&](const std::string& T, const std::string& v) {
+    if (T != "#1") pq = {T, v};
+    return mulv(T, v);
+  };
+  auto product_of = [&](const std::string& T) -> const std::pair<std::string, std::string>* {
+    auto it = prod_.find(T);
+    return it == prod_.end() ? nullptr : &it->second;
+  };
   bool needB = false;
   for (int j : D) needB |= !tb(j).empty();
   const std::string q = tn + "q" + sfx, r = tn + "r" + sfx, c = tn + "c" + sfx;
@@ -1119,12 +1149,25 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
   for (int j : D) {
     const std::string A = ta(j), B = tb(j);
     std::string e;
+    pq = {};
     switch (op) {
       case NT_OP_ADD:
-        e = A.empty() ? (B.empty() ? "" : val(B)) : (B.empty() ? val(A) : val(A) + " + " + val(B));
+        if (!A.empty() && !B.empty()) {
+          if (const auto* m = product_of(B)) e = FMA + "(" + m->first + ", " + m->second + ", " + val(A) + ")";
+          else if (const auto* n = product_of(A)) e = FMA + "(" + n->first + ", " + n->second + ", " + val(B) + ")";
+          else e = val(A) + " + " + val(B);
+        } else {
+          e = A.empty() ? (B.empty() ? "" : val(B)) : val(A);
+        }
         break;
       case NT_OP_SUB:
-        e = A.empty() ? (B.empty() ? "" : "-" + val(B)) : (B.empty() ? val(A) : val(A) + " - " + val(B));
+        if (!A.empty() && !B.empty()) {
+          if (const auto* m = product_of(B)) e = FMA + "(-" + m->first + ", " + m->second + ", " + val(A) + ")";
+          else if (const auto* n = product_of(A)) e = FMA + "(" + n->first + ", " + n->second + ", -" + val(B) + ")";
+          else e = val(A) + " - " + val(B);
+        } else {
+          e = A.empty() ? (B.empty() ? "" : "-" + val(B)) : val(A);
+        }
         break;
       case NT_OP_MUL:
         if (xe_.on) {
@@ -1140,9 +1183,9 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
           e = A == "#1" ? FMA + "(" + Va + ", " + val(B) + ", " + Vb + ")"
                         : FMA + "(" + A + ", " + Vb + ", " + mulv(B, Va) + ")";
         } else if (!A.empty()) {
-          e = mulv(A, Vb);
+          e = prod(A, Vb);
         } else if (!B.empty()) {
-          e = mulv(B, Va);
+          e = prod(B, Va);
         }
         break;
       case NT_OP_DIV:
@@ -1151,14 +1194,16 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
         else if (!B.empty()) e = "-" + mulv(B, r);
         break;
       case NT_OP_NEG: if (!A.empty()) e = "-" + val(A); break;
-      case NT_OP_EXP: if (!A.empty()) e = mulv(A, Vi); break;
-      case NT_OP_LOG: case NT_OP_SQRT: case NT_OP_ABS: if (!A.empty()) e = mulv(A, q); break;
+      case NT_OP_EXP: if (!A.empty()) e = prod(A, Vi); break;
+      case NT_OP_LOG: case NT_OP_SQRT: case NT_OP_ABS: if (!A.empty()) e = prod(A, q); break;
       case NT_OP_MAX: case NT_OP_MIN:
         if (!A.empty() || !B.empty()) e = c + " ? " + (A.empty() ? zero : val(A)) + " : " + (B.empty() ? zero : val(B));
         break;
       default: break;
     }
-    o_ << ind << "const real " << tn << j << sfx << " = " << (e.empty() ? zero : e) << ";\n";
+    const std::string name = tn + std::to_string(j) + sfx;
+    if (!pq.first.empty()) prod_[name] = pq;
+    o_ << ind << "const real " << name << " = " << (e.empty() ? zero : e) << ";\n";
   }
 }
 
@@ -1196,6 +1241,18 @@ void Emitter::tline(int lo, int hi) {
 
 void Emitter::body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const {
   const std::string m = ms(true);
+  if ((kind == ARG_BODY || kind == ARG_CARRY) && geo(ref)) {
+    // a multiplicative carry's tangent is G sigma
+    const int v = kind == ARG_BODY ? u : u - 1;  // iteration whose value is read; -1: the state before the trip
+    fn = [this, v, ref, m](int j) {
+      if (!poshas(ref, j)) return std::string();
+      const std::string r = std::to_string(ref), k = std::to_string(j);
+      if (v < 0) return product("gs" + r + m, "ts" + r + "_" + k + m);
+      const std::string it = std::to_string(v);
+      return product("gq" + it + "_" + r + m, "tr" + it + "_" + r + "_" + k + m);
+    };
+    return;
+  }
   if (kind == ARG_BODY) {
     fn = [this, u, ref, m](int j) {
       return poshas(ref, j) ? "tr" + std::to_string(u) + "_" + std::to_string(ref) + "_" + std::to_string(j) + m
@@ -1249,6 +1306,28 @@ void Emitter::tsegment(int U, const std::string& sg) {
         }
         o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
         if (!act || ar == 0 || !p_.adjoints) continue;
+        if (geo(j)) {
+          const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+          const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
+          const std::string m = ms(true), sj = std::to_string(j), su = std::to_string(u);
+          const std::string prev = u > 0 ? std::to_string(u - 1) : "";
+          o_ << ind << "const real gq" << su << "_" << sj << m << " = "
+             << (u > 0 ? "gq" + prev + "_" + sj + m : "gs" + sj + m) << " * " << body_value(u, ARG_BODY, e, false)
+             << ";\n";
+          std::function<std::string(int)> tx;
+          body_tangent_operand(u, L_.kind_a[e], L_.ref_a[e], tx);
+          for (int k : posdeplist(j)) {
+            const std::string sk = std::to_string(k);
+            const std::string sp = u > 0 ? "tr" + prev + "_" + sj + "_" + sk + m : "ts" + sj + "_" + sk + m;
+            const std::string X = tx(k);
+            o_ << ind << "const real tr" << su << "_" << sj << "_" << sk << m << " = "
+               << (X.empty() ? sp
+                             : f("fma") + "(c0_" + sj + m + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) + ", " + sp +
+                                   ")")
+               << ";\n";
+          }
+          continue;
+        }
         std::function<std::string(int)> ta, tb;
         body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
         body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
@@ -1277,12 +1356,53 @@ void Emitter::tsegment(int U, const std::string& sg) {
       const std::string sm = ms(act);
       o_ << ind << "st" << j << sm << " = r" << (U - 1) << "_" << j << sm << ";\n";
       if (!act || !p_.adjoints) continue;
+      if (geo(j)) o_ << ind << "gs" << j << sm << " = gq" << (U - 1) << "_" << j << sm << ";\n";
       for (int k : posdeplist(j)) {
         o_ << ind << "ts" << j << "_" << k << sm << " = tr" << (U - 1) << "_" << j << "_" << k << sm << ";\n";
       }
     }
   }
   o_ << "    }\n";
+}
+
+void Emitter::plan_geo_carries() {
+  geo_.assign(L_.found ? L_.period : 0, 0);
+  if (!L_.found || p_.mode != NT_MODE_TANGENT || !p_.adjoints) return;
+  for (int j = 0; j < L_.period; ++j) {
+    if (!L_.is_carry[j] || !t_.active[L_.start + j] || t_.op[L_.start + j] != NT_OP_MUL) continue;
+    const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+    const bool b_self = L_.kind_b[j] == ARG_CARRY && L_.ref_b[j] == j;
+    if (a_self == b_self) continue;
+    const int ek = a_self ? L_.kind_b[j] : L_.kind_a[j], er = a_self ? L_.ref_b[j] : L_.ref_a[j];
+    if (ek != ARG_BODY || !single_body_exp(er)) continue;
+    // Worth it when the saving (one operation per input of the carry's
+    // tangent) beats the multiply for G plus one multiply per input that some
+    // consumer needs as an absolute tangent G sigma_k. A sum or difference
+    // with an operand whose tangent also has input k takes G sigma_k as one
+    // fma and needs none.
+    const std::vector<int> D = posdeplist(j);
+    std::vector<char> need(static_cast<size_t>(t_.n_in), 0);
+    for (int q = 0; q < L_.period; ++q) {
+      const int oq = t_.op[L_.start + q];
+      const int ar = arity(oq);
+      for (int slot = 0; slot < ar; ++slot) {
+        const int kind = slot ? L_.kind_b[q] : L_.kind_a[q], ref = slot ? L_.ref_b[q] : L_.ref_a[q];
+        if (!((kind == ARG_BODY || kind == ARG_CARRY) && ref == j) || (q == j && kind == ARG_CARRY)) continue;
+        const int okind = slot ? L_.kind_a[q] : L_.kind_b[q], oref = slot ? L_.ref_a[q] : L_.ref_b[q];
+        for (int k : D) {
+          bool fused = false;
+          if ((oq == NT_OP_ADD || oq == NT_OP_SUB) && ar == 2) {
+            if (okind == ARG_BODY || okind == ARG_CARRY) fused = poshas(oref, k) && !geo(oref) && oref != j;
+            else if (okind == ARG_INV) fused = has(oref, k);
+          }
+          if (!fused) need[k] = 1;
+        }
+      }
+    }
+    int materialised = 0;
+    for (int k : D) materialised += need[k];
+    if (static_cast<int>(D.size()) - 1 - materialised > 0) geo_[j] = 1;
+  }
 }
 
 void Emitter::plan_exp2_folds() {
@@ -1436,6 +1556,10 @@ void Emitter::body_tangent() {
           o_ << "    real ts" << j << "_" << k << ms(true) << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin)
              << ";\n";
         }
+        if (geo(j)) {
+          o_ << "    real gs" << j << ms(true) << " = " << one << ";\n";
+          o_ << "    const real c0_" << j << ms(true) << " = st" << j << ms(true) << ";\n";
+        }
       }
     }
     if (p_.nseg_full > 0) {
@@ -1443,6 +1567,16 @@ void Emitter::body_tangent() {
       tsegment(p_.seg, "sg");
     }
     if (p_.tail) tsegment(p_.tail, std::to_string(p_.nseg_full) + "u");
+    for (int j = 0; j < L_.period; ++j) {
+      if (!geo(j)) continue;
+      for (int m = mlo_; m < mhi_; ++m) {
+        m_ = m;
+        for (int k : posdeplist(j)) {
+          o_ << "    ts" << j << "_" << k << ms(true) << " = gs" << j << ms(true) << " * ts" << j << "_" << k << ms(true)
+             << ";\n";
+        }
+      }
+    }
     tline(le, n);
   }
   const int nin = t_.n_in;
@@ -1522,6 +1656,7 @@ void Emitter::body_reverse() {
 std::string Emitter::run() {
   count_uses();
   plan_exp2_folds();
+  plan_geo_carries();
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;
   const bool tangent = p_.mode == NT_MODE_TANGENT;

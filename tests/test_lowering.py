@@ -274,3 +274,48 @@ def test_multi_output_rows_match_oracle(nt, rocm):
         assert ev.max() == 0.0 and eg.max() <= 1e-12, o
     ref = oracle.replay_sums(flat, 200, OFFSET, 42, threads=1, all_outputs=True).reshape(2, -1)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-12
+
+
+def _growth_tape(nt, steps=24):
+    """S <- S exp(0.2 vol z - 0.01) per step and a running sum of S: a carried
+    value updated by a single-use exponential, read by a sum."""
+    def body(rec):
+        s0 = rec.input("S0", 100.0)
+        vol = rec.input("vol", 0.3)
+        s = s0
+        acc = rec.constant(0.0)
+        for _ in range(steps):
+            s = s.mul(vol.mul(rec.randn()).mul(0.2).sub(0.01).exp())
+            acc = acc.add(s)
+        rec.output(acc.mul(0.5).add(s))
+    return nt.AadRecorder.record(body).flat()
+
+
+@pytest.mark.parametrize("precision", ["fp64", "fp32"])
+def test_multiplicative_carry_tangents(nt, rocm, precision):
+    """Tangent mode carries such a value's tangent as G sigma (G the product of
+    the exponentials since the loop began, sigma = t(start) + c0 sum tx): no
+    division, so a start value of zero (where the tangent is still G t(start),
+    not zero) is exact too."""
+    flat = _growth_tape(nt)
+    src = rocm.lower(flat, rocm.options(precision, mode=2))
+    assert "real gs" in src and "c0_" in src
+    for s0 in (100.0, 0.0):
+        x = [s0, 0.3]
+        ov, og = oracle.replay_paths(flat, 64, OFFSET, 9, inputs=x, threads=1)
+        _, v, g = run_emulated(flat, rocm.options(precision, mode=2, libm=1), 64, seed=9, inputs=x, rocm=rocm)
+        if precision == "fp64":
+            ev, eg = oracle.path_errors(v, g, ov, og)
+            assert ev.max() <= 1e-13 and eg.max() <= 1e-12, s0
+        else:
+            assert rel_err(g, og) <= 1e-4, s0
+        if s0 == 0.0:
+            assert np.all(v == 0.0) and np.all(np.abs(og[:, 0]) > 0.1) and np.all(og[:, 1] == 0.0)
+
+
+def test_multiplicative_carries_only_where_they_pay(rocm, tapes):
+    """The Asian spot (read by a sum), the Heston spot and the 16 worst-of
+    spots (read only after the loop) take G sigma; the barrier spot, read by
+    the smoothed barrier test through a product, keeps the product rule."""
+    gs = {k: rocm.lower(tapes[k], rocm.options("fp32", mode=2)).count("real gs") for k in ("C2", "C3", "C4", "C5")}
+    assert gs == {"C2": 1, "C3": 0, "C4": 1, "C5": 16}
