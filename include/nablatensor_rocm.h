@@ -93,7 +93,9 @@ typedef struct nt_options {
   int32_t mode;             /* NT_MODE_* */
   int32_t markets;          /* nt_lower / nt_compile_check only: lower the kernel that prices this many input
                                sets from each path's draws (what nt_exec_replay_many compiles); 0 or 1 = one */
-  int32_t reserved[5];
+  int32_t waves;            /* replay kernel: ask the compiler for at least this many waves per SIMD (a register
+                               budget; it may fail to meet it or spill); 0 = the engine's choice */
+  int32_t reserved[4];
 } nt_options;
 
 typedef struct nt_exec nt_exec;

@@ -343,6 +343,8 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   if (o.mode < NT_MODE_AUTO || o.mode > NT_MODE_TANGENT) { err = "unknown derivative mode"; return NT_E_INVALID; }
   if (o.markets < 0 || o.markets > 64) { err = "markets must be between 1 and 64"; return NT_E_INVALID; }
   p.markets = std::max(1, o.markets);
+  if (o.waves < 0 || o.waves > 8) { err = "waves must be between 0 and 8"; return NT_E_INVALID; }
+  p.waves = o.waves;
   if (p.markets > 1 && o.mode == NT_MODE_REVERSE) {
     err = "several markets per dispatch share draws in tangent mode only";
     return NT_E_INVALID;
@@ -1491,7 +1493,9 @@ void Emitter::header() {
   if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";
   o_ << "#include \"nt_skeleton.h\"\n";
   o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
-  o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block << ") void nt_replay(\n"
+  o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block;
+  if (p_.waves > 0) o_ << ", " << p_.waves;
+  o_ << ") void nt_replay(\n"
      << "    const double* __restrict__ inputs, nt_u64 n_paths, nt_u64 path_offset, nt_u64 seed,\n"
      << "    double* __restrict__ partials, real* __restrict__ scratch,\n"
      << "    double* __restrict__ out_v, double* __restrict__ out_g) {\n";

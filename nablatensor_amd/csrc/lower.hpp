@@ -66,6 +66,7 @@ struct Plan {
   int precision = NT_FP64;
   int mode = NT_MODE_REVERSE;             // resolved NT_MODE_REVERSE or NT_MODE_TANGENT
   int markets = 1;                        // input sets per dispatch sharing each path's draws (tangent mode)
+  int waves = 0;                          // launch-bound hint: minimum waves per SIMD (0: none)
   int n_words = 0;                        // 64-bit words per dependency set
   std::vector<uint64_t> deps;             // node -> inputs it depends on (bitset), tangent mode
   std::vector<uint64_t> posdeps;          // loop position -> union over the iterations

@@ -13,7 +13,8 @@ sys.path.insert(0, str(conftest.ROOT))
 import bench  # noqa: E402
 
 
-def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2"):
+def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
+                 waves=0):
     ms = 2.0 if precision == "fp64" else 1.0
     resolved = "reverse" if mode == 1 else "tangent"
     return {"value": paths / (ms / 1e3), "ms_per_step": ms, "kernel_ms": ms, "replay_kernel_ms": ms,
