@@ -288,6 +288,9 @@ extern "C" __global__ __launch_bounds__(1024) void nt_finish(const double* __res
   const nt_u32 waves = blockDim.x >> 6;
   for (nt_u32 c = threadIdx.x >> 6; c < nch; c += waves) {
     double s = 0.0;
+    // unrolled so the loads of several rows are in flight at once; the adds
+    // keep their order
+#pragma unroll 8
     for (nt_u32 b = lane; b < blocks; b += 64) s += partials[static_cast<nt_u64>(b) * nch + c];
     s = nt_wave_sum(s);
     if (lane == 0) out[c] = s;
