@@ -59,10 +59,11 @@ def measured_traffic(precision: str, info: dict) -> dict | None:
 
 
 def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
-            waves=0):
+            waves=0, max_blocks=0):
     from nablatensor_amd import flops
 
-    with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves)) as x:
+    with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves,
+                                                max_blocks=max_blocks)) as x:
         info = x.info()
         # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
         # (untimed) before the warmup steps, so a short --warmup does not time
@@ -181,7 +182,7 @@ def other_workload(rocm, args) -> int:
         print(json.dumps(out), flush=True)
         return 0
     m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp,
-                args.workload, args.waves)
+                args.workload, args.waves, args.max_blocks)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -284,6 +285,8 @@ def main() -> int:
     ap.add_argument("--policy", type=int, default=0, help="checkpoint policy (0 auto, 1 recompute, 2 store draws, 3 store all)")
     ap.add_argument("--seg", type=int, default=0, help="loop iterations per checkpoint segment (0 auto)")
     ap.add_argument("--mode", type=int, default=0, help="derivative mode (0 cost model, 1 reverse sweep, 2 tangent)")
+    ap.add_argument("--max-blocks", type=int, default=0,
+                    help="cap on the replay grid in blocks (0: one resident wave of blocks)")
     ap.add_argument("--waves", type=int, default=0,
                     help="with --workload/--precision: minimum waves per SIMD asked of the compiler (0: the engine's choice)")
     ap.add_argument("--no-reverse", action="store_true", help="skip the reverse-sweep comparison run")

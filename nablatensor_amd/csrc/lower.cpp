@@ -705,7 +705,7 @@ class Emitter {
       case NT_OP_ADD: return x + " + " + y;
       case NT_OP_SUB: return x + " - " + y;
       case NT_OP_MUL: return x + " * " + y;
-      case NT_OP_DIV: return x + " / " + y;
+      case NT_OP_DIV: return f32_ ? x + " * nt_rcpf(" + y + ")" : x + " / " + y;
       case NT_OP_NEG: return "-" + x;
       case NT_OP_EXP:
         if (f32_) return "nt_expf(" + x + ")";
@@ -803,24 +803,40 @@ class Emitter {
     return d;
   }
   std::string tname(int node, int j) const;  // straight-line node or loop live-out
-  // A MUL whose other operand is exp(x) used nowhere else: its tangent is
-  // (tc + c tx) exp(x) per input, two operations instead of three (tx exp(x)
-  // then the product rule); set by the caller of tangent() for one MUL.
-  struct ExpFactor {
-    bool on = false;
-    int side = 1;                                  // operand holding exp(x): 0 = a, 1 = b
-    std::function<std::string(int)> tx;            // tangent of x
-  } xe_;
-  // Tangents that are a plain product of two factors, by the name (or
-  // expression) that stands for them: a sum or difference with one of them
-  // becomes one fma instead of a multiply and an add.
-  mutable std::map<std::string, std::pair<std::string, std::string>> prod_;
-  // "(a * b)", recorded as a product for the fma peephole
-  std::string product(const std::string& a, const std::string& b) const {
-    const std::string e = "(" + a + " * " + b + ")";
-    prod_[e] = {a, b};
+  // Scaled tangents. A node whose tangent is its operand's tangent times a
+  // local factor (EXP, LOG, SQRT, ABS, NEG, a product or quotient with a value
+  // that has no tangent, a max/min that follows one operand) keeps, per input,
+  // the pair (base, scale): the tangent is base * scale, base a tangent that
+  // was formed as a variable and scale a scalar of the node, the same for
+  // every input. A chain of such rules multiplies scalars only; the product
+  // per input is formed where a consumer needs it, and a sum or a product
+  // rule takes it as one fma. lazy_ maps the name (or expression) that stands
+  // for a tangent to its pair.
+  mutable std::map<std::string, std::pair<std::string, std::string>> lazy_;
+  // "(base * scale)", recorded as a scaled tangent
+  std::string product(const std::string& scale, const std::string& base) const {
+    const std::string e = "(" + base + " * " + scale + ")";
+    lazy_[e] = {base, scale};
     return e;
   }
+  // Scalar factors of scaled tangents: expression -> variable, for the scope
+  // being emitted (a trip's block restores the set it found).
+  std::map<std::string, std::string> scal_;
+  int nscal_ = 0;
+  std::string scalar(const std::string& ind, const std::string& e);
+  // One tangent of one input: expr is its value; when base is set, the
+  // tangent is base * scale and expr is that product.
+  struct Term {
+    std::string expr, base, scale;
+    bool empty() const { return expr.empty(); }
+  };
+  Term lazy_term(const std::string& base, const std::string& scale) const {
+    if (scale.empty()) return Term{base, "", ""};
+    return Term{"(" + base + " * " + scale + ")", base, scale};
+  }
+  std::string smul(const std::string& ind, const std::string& s1, const std::string& s2);
+  Term scaled(const std::string& ind, const std::string& T, const std::string& s, bool unwrap);
+  Term sum(const Term& x, const Term& y) const;
   // Multiplicative carries (tangent loops): a carried value updated as
   // c <- c exp(x), the exponential used nowhere else, keeps G = the product of
   // the exp(x) since the loop began and sigma_k = t_k(loop start) + c0 sum tx_k,
@@ -834,7 +850,6 @@ class Emitter {
   std::vector<int> uses_;       // per node: operand references + outputs
   std::vector<int> body_uses_;  // per loop position: references within and across iterations, + live-out
   void count_uses();
-  bool single_exp(int node) const { return t_.op[node] == NT_OP_EXP && uses_[node] == 1; }
   bool single_body_exp(int pos) const {
     return t_.op[L_.start + pos] == NT_OP_EXP && body_uses_[pos] == 1 && !L_.is_liveout[pos] && !L_.is_carry[pos];
   }
@@ -1103,109 +1118,175 @@ std::string Emitter::tname(int node, int j) const {
   return "t" + std::to_string(node) + "_" + std::to_string(j) + ms(true);
 }
 
+std::string Emitter::scalar(const std::string& ind, const std::string& e) {
+  auto it = scal_.find(e);
+  if (it != scal_.end()) return it->second;
+  const std::string name = "ls" + std::to_string(nscal_++);
+  o_ << ind << "const real " << name << " = " << e << ";\n";
+  scal_[e] = name;
+  return name;
+}
+
+// s1 * s2 for scale factors ("" stands for 1)
+std::string Emitter::smul(const std::string& ind, const std::string& s1, const std::string& s2) {
+  if (s1.empty()) return s2;
+  if (s2.empty()) return s1;
+  return scalar(ind, "(" + s1 + " * " + s2 + ")");
+}
+
+// The tangent T ("#1" the seed of an input, a variable, or a scaled tangent)
+// times the scalar s. A scaled T is taken apart (its scale times s, one
+// scalar operation) only when `unwrap` says that scalar is shared; otherwise
+// T's own variable is the base.
+Emitter::Term Emitter::scaled(const std::string& ind, const std::string& T, const std::string& s, bool unwrap) {
+  if (T == "#1") return Term{s.empty() ? std::string(f32_ ? "1.0f" : "1.0") : s, "", ""};
+  auto it = lazy_.find(T);
+  if (it != lazy_.end() && (s.empty() || unwrap)) return lazy_term(it->second.first, smul(ind, it->second.second, s));
+  return lazy_term(T, s);
+}
+
+// x + y, with a scaled term taken as one fma and a term scaled by -1 as a
+// subtraction.
+Emitter::Term Emitter::sum(const Term& x, const Term& y) const {
+  if (x.empty()) return y;
+  if (y.empty()) return x;
+  const std::string mone = f32_ ? "(-1.0f)" : "(-1.0)";
+  if (y.scale == mone) return Term{"(" + x.expr + " - " + y.base + ")", "", ""};
+  if (x.scale == mone) return Term{"(" + y.expr + " - " + x.base + ")", "", ""};
+  if (!y.base.empty()) return Term{f("fma") + "(" + y.base + ", " + y.scale + ", " + x.expr + ")", "", ""};
+  if (!x.base.empty()) return Term{f("fma") + "(" + x.base + ", " + x.scale + ", " + y.expr + ")", "", ""};
+  return Term{"(" + x.expr + " + " + y.expr + ")", "", ""};
+}
+
 // Tangent of one active node for each input j in D, named tn + j, from the
 // operand tangents ta(j), tb(j). The local derivatives are those of the
 // reverse rules in rev(): d/da and d/db of ADD SUB MUL DIV NEG EXP LOG SQRT
-// ABS, and MAX/MIN following operand a when a >= b (a <= b), else b.
+// ABS, and MAX/MIN following operand a when a >= b (a <= b), else b. Every
+// rule is A qa + B qb with scalar factors qa, qb (a max/min selects), so a
+// node's tangent stays scaled (base * scale) wherever one operand has a
+// tangent for that input. A new scalar (a scale times a factor, a selected
+// scale, the sum of two scales of one base) is formed only when at least two
+// inputs of the node share it: for a single input it costs what the product
+// per input costs.
 void Emitter::tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx,
                       const std::vector<int>& D, const std::string& Vi, const std::string& Va, const std::string& Vb,
                       const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb) {
   if (D.empty()) return;
   const std::string one = f32_ ? "1.0f" : "1.0";
   const std::string zero = f32_ ? "0.0f" : "0.0";
-  const std::string FMA = f("fma");
-  auto val = [&](const std::string& T) { return T == "#1" ? one : T; };
-  auto mulv = [&](const std::string& T, const std::string& v) { return T == "#1" ? v : "(" + T + " * " + v + ")"; };
-  // a product P * Q in tangent j (recorded for the fma peephole below)
-  std::pair<std::string, std::string> pq;
-  auto prod = [&](const std::string& T, const std::string& v) {
-    if (T != "#1") pq = {T, v};
-    return mulv(T, v);
-  };
-  auto product_of = [&](const std::string& T) -> const std::pair<std::string, std::string>* {
-    auto it = prod_.find(T);
-    return it == prod_.end() ? nullptr : &it->second;
-  };
+  const std::string mone = f32_ ? "(-1.0f)" : "(-1.0)";
   bool needB = false;
   for (int j : D) needB |= !tb(j).empty();
   const std::string q = tn + "q" + sfx, r = tn + "r" + sfx, c = tn + "c" + sfx;
+  const std::string rcp_one = f32_ ? "nt_rcpf(" : "1.0 / (";
   switch (op) {
     case NT_OP_DIV:
-      o_ << ind << "const real " << q << " = " << one << " / " << Vb << ";\n";
+      o_ << ind << "const real " << q << " = " << rcp_one << Vb << ");\n";
       if (needB) o_ << ind << "const real " << r << " = " << Vi << " * " << q << ";\n";
       break;
-    case NT_OP_LOG: o_ << ind << "const real " << q << " = " << one << " / " << Va << ";\n"; break;
+    case NT_OP_LOG: o_ << ind << "const real " << q << " = " << rcp_one << Va << ");\n"; break;
     case NT_OP_SQRT:
       // sqrt(0) = 0 has an infinite local derivative. The reverse sweep never
       // multiplies it by a zero adjoint (zero adjoints are skipped), so the
       // factor is capped at a finite 2^(max exponent) here: a zero tangent
       // (e.g. a full-truncation max(v, 0) that chose the constant) stays zero.
-      o_ << ind << "const real " << q << " = " << f("fmin") << "(" << (f32_ ? "0.5f" : "0.5") << " / " << Vi << ", "
-         << (f32_ ? "0x1p127f" : "0x1p1023") << ");\n";
+      o_ << ind << "const real " << q << " = " << f("fmin") << "("
+         << (f32_ ? "0.5f * nt_rcpf(" + Vi + ")" : "0.5 / " + Vi) << ", " << (f32_ ? "0x1p127f" : "0x1p1023") << ");\n";
       break;
     case NT_OP_ABS: o_ << ind << "const real " << q << " = " << Va << " < " << zero << " ? -" << one << " : " << one << ";\n"; break;
     case NT_OP_MAX: o_ << ind << "const bool " << c << " = " << Va << " >= " << Vb << ";\n"; break;
     case NT_OP_MIN: o_ << ind << "const bool " << c << " = " << Va << " <= " << Vb << ";\n"; break;
     default: break;
   }
+  std::string qa, qb;  // local factors ("" stands for 1)
+  switch (op) {
+    case NT_OP_SUB: qb = mone; break;
+    case NT_OP_MUL: qa = Vb; qb = Va; break;
+    case NT_OP_DIV: qa = q; if (needB) qb = "(-" + r + ")"; break;
+    case NT_OP_NEG: qa = mone; break;
+    case NT_OP_EXP: qa = Vi; break;
+    case NT_OP_LOG: case NT_OP_SQRT: case NT_OP_ABS: qa = q; break;
+    default: break;
+  }
+  // How many inputs would share each new scalar.
+  auto scale_of = [&](const std::string& T) -> std::string {
+    auto it = lazy_.find(T);
+    return it == lazy_.end() ? std::string("=") + T : it->second.second;  // "=" marks an unscaled tangent
+  };
+  std::map<std::string, int> share;
   for (int j : D) {
     const std::string A = ta(j), B = tb(j);
-    std::string e;
-    pq = {};
-    switch (op) {
-      case NT_OP_ADD:
-        if (!A.empty() && !B.empty()) {
-          if (const auto* m = product_of(B)) e = FMA + "(" + m->first + ", " + m->second + ", " + val(A) + ")";
-          else if (const auto* n = product_of(A)) e = FMA + "(" + n->first + ", " + n->second + ", " + val(B) + ")";
-          else e = val(A) + " + " + val(B);
-        } else {
-          e = A.empty() ? (B.empty() ? "" : val(B)) : val(A);
-        }
-        break;
-      case NT_OP_SUB:
-        if (!A.empty() && !B.empty()) {
-          if (const auto* m = product_of(B)) e = FMA + "(-" + m->first + ", " + m->second + ", " + val(A) + ")";
-          else if (const auto* n = product_of(A)) e = FMA + "(" + n->first + ", " + n->second + ", -" + val(B) + ")";
-          else e = val(A) + " - " + val(B);
-        } else {
-          e = A.empty() ? (B.empty() ? "" : "-" + val(B)) : val(A);
-        }
-        break;
-      case NT_OP_MUL:
-        if (xe_.on) {
-          // c * exp(x): (tc + c tx) exp(x)
-          const std::string C = xe_.side == 1 ? A : B, X = xe_.tx(j);
-          const std::string cv = xe_.side == 1 ? Va : Vb, ev = xe_.side == 1 ? Vb : Va;
-          if (!C.empty() && !X.empty()) e = "(" + FMA + "(" + val(X) + ", " + cv + ", " + val(C) + ") * " + ev + ")";
-          else if (!C.empty()) e = mulv(C, ev);
-          else if (!X.empty()) e = "(" + mulv(X, cv) + " * " + ev + ")";
+    if (!A.empty() && A != "#1") ++share["a" + scale_of(A)];
+    if (!B.empty() && B != "#1") ++share["b" + scale_of(B)];
+  }
+  auto shared = [&](const std::string& key) { return share[key] >= 2; };
+  const size_t nD = D.size();
+  std::vector<Term> x(nD), y(nD);
+  for (size_t i = 0; i < nD; ++i) {
+    const std::string A = ta(D[i]), B = tb(D[i]);
+    if (!A.empty()) x[i] = scaled(ind, A, qa, shared("a" + scale_of(A)));
+    if (!B.empty()) y[i] = scaled(ind, B, qb, shared("b" + scale_of(B)));
+  }
+  std::vector<Term> t(nD);
+  if (op == NT_OP_MAX || op == NT_OP_MIN) {
+    // c ? A : B: with one side, or both sides scalings of one base, the
+    // selection moves to the scale when that selection is shared.
+    auto base_of = [](const Term& u) { return u.base.empty() ? u.expr : u.base; };
+    auto scale_or_one = [&](const Term& u) { return u.scale.empty() ? one : u.scale; };
+    std::vector<std::string> key(nD);
+    std::map<std::string, int> nsel;
+    for (size_t i = 0; i < nD; ++i) {
+      const std::string A = ta(D[i]), B = tb(D[i]);
+      const bool ax = !x[i].empty() && A != "#1", by = !y[i].empty() && B != "#1";
+      if (ax && by && base_of(x[i]) == base_of(y[i])) key[i] = "(" + c + " ? " + scale_or_one(x[i]) + " : " + scale_or_one(y[i]) + ")";
+      else if (ax && y[i].empty()) key[i] = "(" + c + " ? " + scale_or_one(x[i]) + " : " + zero + ")";
+      else if (by && x[i].empty()) key[i] = "(" + c + " ? " + zero + " : " + scale_or_one(y[i]) + ")";
+      if (!key[i].empty()) ++nsel[key[i]];
+    }
+    for (size_t i = 0; i < nD; ++i) {
+      if (!key[i].empty() && (nsel[key[i]] >= 2 || scal_.count(key[i]))) {
+        t[i] = lazy_term(base_of(x[i].empty() ? y[i] : x[i]), scalar(ind, key[i]));
+      } else if (!x[i].empty() || !y[i].empty()) {
+        t[i] = Term{"(" + c + " ? " + (x[i].empty() ? zero : x[i].expr) + " : " + (y[i].empty() ? zero : y[i].expr) + ")", "", ""};
+      }
+    }
+  } else {
+    // Two scalings of one base add their scales when that sum is shared.
+    std::map<std::string, int> nadd;
+    std::vector<std::string> key(nD);
+    for (size_t i = 0; i < nD; ++i) {
+      if (!x[i].base.empty() && x[i].base == y[i].base) {
+        key[i] = "(" + x[i].scale + " + " + y[i].scale + ")";
+        ++nadd[key[i]];
+      }
+    }
+    for (size_t i = 0; i < nD; ++i) {
+      if (!key[i].empty() && (nadd[key[i]] >= 2 || scal_.count(key[i]))) t[i] = lazy_term(x[i].base, scalar(ind, key[i]));
+      else t[i] = sum(x[i], y[i]);
+    }
+    // a * b with b = exp(x): the tangent of b is tx b, and A b + a tx b is
+    // (A + a tx) b, an fma and a multiply per input with no scalar.
+    if (op == NT_OP_MUL) {
+      for (size_t i = 0; i < nD; ++i) {
+        for (int side = 0; side < 2; ++side) {
+          const std::string C = side ? ta(D[i]) : tb(D[i]), E = side ? tb(D[i]) : ta(D[i]);
+          const std::string& cv = side ? Va : Vb;  // value of the other factor
+          const std::string& ev = side ? Vb : Va;  // value of the exponential
+          if (C.empty() || E.empty() || C == "#1" || E == "#1" || lazy_.count(C) || lazy_.count(E) == 0) continue;
+          const auto& le = lazy_.at(E);
+          // (a scaled tx is used as its variable: free outside the loop body)
+          if (le.second != ev || (lazy_.count(le.first) && le.first.rfind("tr", 0) == 0)) continue;
+          t[i] = Term{"(" + f("fma") + "(" + le.first + ", " + cv + ", " + C + ") * " + ev + ")", "", ""};
           break;
         }
-        if (!A.empty() && !B.empty()) {
-          e = A == "#1" ? FMA + "(" + Va + ", " + val(B) + ", " + Vb + ")"
-                        : FMA + "(" + A + ", " + Vb + ", " + mulv(B, Va) + ")";
-        } else if (!A.empty()) {
-          e = prod(A, Vb);
-        } else if (!B.empty()) {
-          e = prod(B, Va);
-        }
-        break;
-      case NT_OP_DIV:
-        if (!A.empty() && !B.empty()) e = FMA + "(" + val(A) + ", " + q + ", -" + mulv(B, r) + ")";
-        else if (!A.empty()) e = mulv(A, q);
-        else if (!B.empty()) e = "-" + mulv(B, r);
-        break;
-      case NT_OP_NEG: if (!A.empty()) e = "-" + val(A); break;
-      case NT_OP_EXP: if (!A.empty()) e = prod(A, Vi); break;
-      case NT_OP_LOG: case NT_OP_SQRT: case NT_OP_ABS: if (!A.empty()) e = prod(A, q); break;
-      case NT_OP_MAX: case NT_OP_MIN:
-        if (!A.empty() || !B.empty()) e = c + " ? " + (A.empty() ? zero : val(A)) + " : " + (B.empty() ? zero : val(B));
-        break;
-      default: break;
+      }
     }
-    const std::string name = tn + std::to_string(j) + sfx;
-    if (!pq.first.empty()) prod_[name] = pq;
-    o_ << ind << "const real " << name << " = " << (e.empty() ? zero : e) << ";\n";
+  }
+  for (size_t i = 0; i < nD; ++i) {
+    const std::string name = tn + std::to_string(D[i]) + sfx;
+    if (!t[i].base.empty()) lazy_[name] = {t[i].base, t[i].scale};
+    else lazy_.erase(name);
+    o_ << ind << "const real " << name << " = " << (t[i].empty() ? zero : t[i].expr) << ";\n";
   }
 }
 
@@ -1227,16 +1308,8 @@ void Emitter::tline(int lo, int hi) {
       o_ << "    const real v" << i << ms(act) << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
       if (!act || ar == 0 || !p_.adjoints) continue;
       const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
-      xe_ = ExpFactor();
-      if (op == NT_OP_MUL && a != b && (single_exp(b) || single_exp(a))) {
-        xe_.on = true;
-        xe_.side = single_exp(b) ? 1 : 0;
-        const int x_node = t_.a[xe_.side == 1 ? b : a];
-        xe_.tx = [this, x_node](int j) { return tname(x_node, j); };
-      }
       tangent("    ", op, "t" + std::to_string(i) + "_", ms(true), deplist(i), "v" + std::to_string(i) + ms(true), x, y,
               [&](int j) { return tname(a, j); }, [&](int j) { return b >= 0 ? tname(b, j) : std::string(); });
-      xe_ = ExpFactor();
     }
   }
 }
@@ -1278,6 +1351,7 @@ void Emitter::body_tangent_operand(int u, int kind, int ref, std::function<std::
 void Emitter::tsegment(int U, const std::string& sg) {
   const int P = L_.period, s = L_.start;
   const std::string ind = "      ";
+  const auto outer_scalars = scal_;  // scalars declared in this block end with it
   o_ << "    {\n";
   o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << p_.seg << "u;\n";
   trip_counters(ind);
@@ -1322,31 +1396,18 @@ void Emitter::tsegment(int U, const std::string& sg) {
             const std::string sk = std::to_string(k);
             const std::string sp = u > 0 ? "tr" + prev + "_" + sj + "_" + sk + m : "ts" + sj + "_" + sk + m;
             const std::string X = tx(k);
-            o_ << ind << "const real tr" << su << "_" << sj << "_" << sk << m << " = "
-               << (X.empty() ? sp
-                             : f("fma") + "(c0_" + sj + m + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) + ", " + sp +
-                                   ")")
-               << ";\n";
+            const std::string name_k = "tr" + su + "_" + sj + "_" + sk + m;
+            lazy_.erase(name_k);
+            const std::string e = X.empty() ? sp : sum(Term{sp, "", ""}, scaled(ind, X, "c0_" + sj + m, false)).expr;
+            o_ << ind << "const real " << name_k << " = " << e << ";\n";
           }
           continue;
         }
         std::function<std::string(int)> ta, tb;
         body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
         body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
-        xe_ = ExpFactor();
-        if (op == NT_OP_MUL) {
-          const bool bx = L_.kind_b[j] == ARG_BODY && single_body_exp(L_.ref_b[j]);
-          const bool ax = L_.kind_a[j] == ARG_BODY && single_body_exp(L_.ref_a[j]);
-          if ((bx || ax) && !(L_.kind_a[j] == L_.kind_b[j] && L_.ref_a[j] == L_.ref_b[j])) {
-            xe_.on = true;
-            xe_.side = bx ? 1 : 0;
-            const int ep = bx ? L_.ref_b[j] : L_.ref_a[j];
-            body_tangent_operand(u, L_.kind_a[ep], L_.ref_a[ep], xe_.tx);
-          }
-        }
         tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", ms(true), posdeplist(j),
                 name + ms(true), x, y, ta, tb);
-        xe_ = ExpFactor();
       }
     }
   }
@@ -1365,6 +1426,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
     }
   }
   o_ << "    }\n";
+  scal_ = outer_scalars;
 }
 
 void Emitter::plan_geo_carries() {
@@ -1684,6 +1746,7 @@ std::string Emitter::run() {
   mlo_ = 0;
   mhi_ = M;
   o_ << "    {\n";
+  scal_.clear();
   if (tangent) body_tangent(); else body_reverse();
   o_ << "    }\n";
   if (fallback) {
@@ -1694,6 +1757,7 @@ std::string Emitter::run() {
       o_ << "    if (nt_slow" << (M > 1 ? " || nt_slow" + msuf(m) : std::string()) << ") {\n";
       mlo_ = m;
       mhi_ = m + 1;
+      scal_.clear();
       if (tangent) body_tangent(); else body_reverse();
       o_ << "    }\n";
     }

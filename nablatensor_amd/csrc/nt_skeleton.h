@@ -58,6 +58,10 @@ __device__ __forceinline__ float nt_hw_log2f(float x) { return __builtin_amdgcn_
 __device__ __forceinline__ float nt_hw_sqrtf(float x) { return __builtin_amdgcn_sqrtf(x); }
 __device__ __forceinline__ float nt_hw_sin2pif(float x) { return __builtin_amdgcn_sinf(x); }
 __device__ __forceinline__ float nt_hw_cos2pif(float x) { return __builtin_amdgcn_cosf(x); }
+// fp32 reciprocal, one v_rcp_f32 (1 ulp): fp32 replay divides as a * (1/b),
+// within 2 ulp of the rounded quotient, where a correctly rounded division
+// takes ten instructions.
+__device__ __forceinline__ float nt_rcpf(float x) { return __builtin_amdgcn_rcpf(x); }
 #endif
 
 // fp32 exp as 2^(x log2 e) on the hardware exp2: the rounding of the product

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import hashlib
+import os
 import subprocess
 import tempfile
 from pathlib import Path
@@ -29,14 +30,17 @@ class EmulatedKernel:
         src = BUILD / f"k_{key}.hip.h"
         so = BUILD / f"k_{key}.so"
         if not so.exists():
-            src.write_text(source)
+            src_tmp = Path(f"{src}.{os.getpid()}")
+            src_tmp.write_text(source)
+            os.replace(src_tmp, src)
+            tmp = f"{so}.{os.getpid()}.tmp"  # test workers may build the same kernel at once
             cmd = ["g++", "-O1", "-std=c++17", "-shared", "-fPIC", "-ffp-contract=off", "-w",
                    f"-I{ROOT / 'nablatensor_amd' / 'csrc'}", f"-I{EMU}", f'-DNT_KERNEL_FILE="{src}"',
-                   str(EMU / "emu_main.cpp"), "-o", str(so) + ".tmp"]
+                   str(EMU / "emu_main.cpp"), "-o", tmp]
             if dump:
                 cmd.insert(1, "-DNT_DUMP_PATHS=1")
             subprocess.run(cmd, check=True)
-            Path(str(so) + ".tmp").rename(so)
+            os.replace(tmp, so)
         self.lib = C.CDLL(str(so))
         self.lib.emu_run.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(C.c_double),
                                      C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double),

@@ -38,6 +38,7 @@ static nt_emu_dim3 gridDim, blockDim, blockIdx, threadIdx;
 inline float nt_hw_exp2f(float x) { return static_cast<float>(::exp2(static_cast<double>(x))); }
 inline float nt_hw_log2f(float x) { return static_cast<float>(::log2(static_cast<double>(x))); }
 inline float nt_hw_sqrtf(float x) { return static_cast<float>(::sqrt(static_cast<double>(x))); }
+inline float nt_rcpf(float x) { return 1.0f / x; }
 inline float nt_hw_sin2pif(float x) { return static_cast<float>(::sin(2.0 * M_PI * static_cast<double>(x))); }
 inline float nt_hw_cos2pif(float x) { return static_cast<float>(::cos(2.0 * M_PI * static_cast<double>(x))); }
 
