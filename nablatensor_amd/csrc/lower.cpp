@@ -711,8 +711,8 @@ class Emitter {
         if (f32_) return "nt_expf(" + x + ")";
         if (p_.libm == 1 || slow_) return "exp(" + x + ")";
         return "nt_exp_fast(" + x + ", nt_slow" + ms(exp_active_) + ")";
-      case NT_OP_LOG: return f("log") + "(" + x + ")";
-      case NT_OP_SQRT: return f("sqrt") + "(" + x + ")";
+      case NT_OP_LOG: return f32_ ? "(nt_hw_log2f(" + x + ") * 0.693147180559945309f)" : "log(" + x + ")";
+      case NT_OP_SQRT: return f32_ ? "nt_hw_sqrtf(" + x + ")" : "sqrt(" + x + ")";
       case NT_OP_ABS: return f("fabs") + "(" + x + ")";
       case NT_OP_MAX: return f("fmax") + "(" + x + ", " + y + ")";
       case NT_OP_MIN: return f("fmin") + "(" + x + ", " + y + ")";
@@ -864,6 +864,18 @@ class Emitter {
   };
   std::vector<Exp2Fold> fold_;  // per loop position
   void plan_exp2_folds();
+  // fp64 loop bodies: an EXP of p + r z, p - r z or r z, with p and r
+  // loop-invariant and z a normal draw, cannot leave the fast exp's range if
+  // |p| + Z_MAX |r| <= 708, |z| <= Z_MAX for every Box-Muller draw (u1 >=
+  // 2^-33, so |z| <= sqrt(66 ln 2) = 6.764). That is checked once per path,
+  // before the loop, and the loop's exponentials skip their own check.
+  struct ExpBound {
+    bool on = false;
+    int p = -1, r = -1;  // invariant nodes (p = -1: no offset)
+  };
+  std::vector<ExpBound> bound_;  // per loop position
+  void plan_exp_bounds();
+  void exp_bound_checks();
   std::string l2e_name(int node) const { return "v" + std::to_string(node) + "_l2e" + ms(t_.active[node]); }
   void tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx, const std::vector<int>& D,
                const std::string& Vi, const std::string& Va, const std::string& Vb,
@@ -885,10 +897,23 @@ class Emitter {
   bool exp_fallback() const {
     if (f32_ || p_.libm == 1) return false;
     for (int i = 0; i < t_.n; ++i) {
-      if (t_.op[i] == NT_OP_EXP) return true;
+      if (t_.op[i] == NT_OP_EXP || (t_.op[i] == NT_OP_SQRT && fast_sqrt())) return true;
     }
     return false;
   }
+  // fp64 tangent kernels with the skeleton's own math take a SQRT node's value
+  // and tangent factor from one nt_sqrt_q (a path whose argument it does not
+  // cover is evaluated again with device libm).
+  bool fast_sqrt() const { return !f32_ && p_.libm == 0 && p_.mode == NT_MODE_TANGENT; }
+  // Forward value of a SQRT node; `q` names its tangent factor when the
+  // tangent rule below should take it from here.
+  std::string sqrt_expr(const std::string& x, const std::string& q, bool act) {
+    if (f32_) return "nt_hw_sqrtf(" + x + ")";
+    if (!fast_sqrt() || slow_) return "sqrt(" + x + ")";
+    sqrt_q_ = q;
+    return "nt_sqrt_q(" + x + ", " + q + ", nt_slow" + ms(act) + ")";
+  }
+  std::string sqrt_q_;  // tangent factor of the SQRT just emitted, if nt_sqrt_q made it
   void header();
   void body_tangent();
   void body_reverse();
@@ -1190,6 +1215,8 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
       // multiplies it by a zero adjoint (zero adjoints are skipped), so the
       // factor is capped at a finite 2^(max exponent) here: a zero tangent
       // (e.g. a full-truncation max(v, 0) that chose the constant) stays zero.
+      // nt_sqrt_q has set it already where it computed the value.
+      if (sqrt_q_ == q) break;
       o_ << ind << "const real " << q << " = " << f("fmin") << "("
          << (f32_ ? "0.5f * nt_rcpf(" + Vi + ")" : "0.5 / " + Vi) << ", " << (f32_ ? "0x1p127f" : "0x1p1023") << ");\n";
       break;
@@ -1305,11 +1332,19 @@ void Emitter::tline(int lo, int hi) {
       exp_active_ = act;
       const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
       const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
-      o_ << "    const real v" << i << ms(act) << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+      std::string val = expr(op, x, y, t_.c[i], t_.a[i]);
+      sqrt_q_.clear();
+      if (op == NT_OP_SQRT && fast_sqrt() && !slow_) {
+        const std::string q = "t" + std::to_string(i) + "_q" + ms(true);
+        o_ << "    real " << q << ";\n";
+        val = sqrt_expr(x, q, act);
+      }
+      o_ << "    const real v" << i << ms(act) << " = " << val << ";\n";
       if (!act || ar == 0 || !p_.adjoints) continue;
       const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
       tangent("    ", op, "t" + std::to_string(i) + "_", ms(true), deplist(i), "v" + std::to_string(i) + ms(true), x, y,
               [&](int j) { return tname(a, j); }, [&](int j) { return b >= 0 ? tname(b, j) : std::string(); });
+      sqrt_q_.clear();
     }
   }
 }
@@ -1380,6 +1415,13 @@ void Emitter::tsegment(int U, const std::string& sg) {
           val = "nt_hw_exp2f(" + (f.p >= 0 ? "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")"
                                            : l2e_name(f.r) + " * " + sv) + ")";
         }
+        sqrt_q_.clear();
+        if (op == NT_OP_SQRT && fast_sqrt() && !slow_) {
+          const std::string q = "tr" + std::to_string(u) + "_" + std::to_string(j) + "_q" + ms(true);
+          o_ << ind << "real " << q << ";\n";
+          val = sqrt_expr(x, q, act);
+        }
+        if (op == NT_OP_EXP && bound_[j].on && !slow_ && !f32_ && p_.libm != 1) val = "nt_exp_core(" + x + ")";
         o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
         if (!act || ar == 0 || !p_.adjoints) continue;
         if (geo(j)) {
@@ -1408,6 +1450,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
         body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
         tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", ms(true), posdeplist(j),
                 name + ms(true), x, y, ta, tb);
+        sqrt_q_.clear();
       }
     }
   }
@@ -1500,6 +1543,59 @@ void Emitter::plan_exp2_folds() {
       f.on = true;
     }
     if (f.on) fold_[j] = f;
+  }
+}
+
+void Emitter::plan_exp_bounds() {
+  bound_.assign(L_.found ? L_.period : 0, ExpBound());
+  if (f32_ || p_.libm == 1 || !L_.found || p_.mode != NT_MODE_TANGENT) return;
+  auto is_normal_draw = [&](int kind, int ref) {
+    return kind == ARG_BODY && t_.op[L_.start + ref] == NT_OP_RANDN;
+  };
+  // r z with r invariant: the node at loop position m; sets r
+  auto scaled_draw = [&](int m, int& r) {
+    if (t_.op[L_.start + m] != NT_OP_MUL) return false;
+    for (int side = 0; side < 2; ++side) {
+      const int ik = side ? L_.kind_b[m] : L_.kind_a[m], ir = side ? L_.ref_b[m] : L_.ref_a[m];
+      const int dk = side ? L_.kind_a[m] : L_.kind_b[m], dr = side ? L_.ref_a[m] : L_.ref_b[m];
+      if (ik == ARG_INV && is_normal_draw(dk, dr)) {
+        r = ir;
+        return true;
+      }
+    }
+    return false;
+  };
+  for (int j = 0; j < L_.period; ++j) {
+    if (t_.op[L_.start + j] != NT_OP_EXP || L_.kind_a[j] != ARG_BODY) continue;
+    const int a = L_.ref_a[j];
+    ExpBound b;
+    if (scaled_draw(a, b.r)) {
+      b.on = true;
+    } else if (t_.op[L_.start + a] == NT_OP_ADD || t_.op[L_.start + a] == NT_OP_SUB) {
+      for (int side = 0; side < 2 && !b.on; ++side) {
+        const int ik = side ? L_.kind_b[a] : L_.kind_a[a], ir = side ? L_.ref_b[a] : L_.ref_a[a];
+        const int mk = side ? L_.kind_a[a] : L_.kind_b[a], mr = side ? L_.ref_a[a] : L_.ref_b[a];
+        if (ik == ARG_INV && mk == ARG_BODY && scaled_draw(mr, b.r)) {
+          b.p = ir;
+          b.on = true;
+        }
+      }
+    }
+    if (b.on) bound_[j] = b;
+  }
+}
+
+void Emitter::exp_bound_checks() {
+  if (slow_) return;
+  for (int j = 0; j < static_cast<int>(bound_.size()); ++j) {
+    const ExpBound& b = bound_[j];
+    if (!b.on) continue;
+    const bool act = t_.active[L_.start + j] != 0;
+    for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+      m_ = m;
+      const std::string off = b.p >= 0 ? "fabs(" + vname(b.p) + ") + " : std::string();
+      o_ << "    nt_slow" << ms(act) << " |= !(" << off << "6.77 * fabs(" << vname(b.r) << ") <= 708.0);\n";
+    }
   }
 }
 
@@ -1628,6 +1724,7 @@ void Emitter::body_tangent() {
         }
       }
     }
+    exp_bound_checks();
     if (p_.nseg_full > 0) {
       o_ << "    for (nt_u32 sg = 0; sg < " << p_.nseg_full << "u; ++sg)\n";
       tsegment(p_.seg, "sg");
@@ -1722,6 +1819,7 @@ void Emitter::body_reverse() {
 std::string Emitter::run() {
   count_uses();
   plan_exp2_folds();
+  plan_exp_bounds();
   plan_geo_carries();
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;

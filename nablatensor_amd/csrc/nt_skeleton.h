@@ -51,6 +51,8 @@ __device__ __forceinline__ double nt_mk(nt_u32 hi, nt_u32 lo) {
   return __hiloint2double(static_cast<int>(hi), static_cast<int>(lo));
 }
 __device__ __forceinline__ double nt_rsq(double x) { return __builtin_amdgcn_rsq(x); }
+// x is -0, +0 or a positive normal number: one v_cmp_class_f64
+__device__ __forceinline__ bool nt_zero_or_pos_normal(double x) { return __builtin_amdgcn_class(x, 0x160); }
 // fp32 hardware transcendentals (quarter-rate VALU): exp2, log2, sqrt, and
 // sin/cos of 2 pi x (the instructions take their argument in revolutions).
 __device__ __forceinline__ float nt_hw_exp2f(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -94,7 +96,7 @@ __device__ __forceinline__ void nt_tables_load() {
 // outside it (and for infinities and NaN) it is garbage but harmless (the
 // table index stays in range) and `bad` is set, so the caller can evaluate
 // the path again with device libm.
-__device__ __forceinline__ double nt_exp_fast(double x, bool& bad) {
+__device__ __forceinline__ double nt_exp_core(double x) {
   const double t = fma(x, NT_EXP_INV_L, 0x1.8p52);
   const double kd = t - 0x1.8p52;
   const int k = static_cast<int>(nt_lo(t));
@@ -107,8 +109,14 @@ __device__ __forceinline__ double nt_exp_fast(double x, bool& bad) {
   const double p = fma(r * r, q, r);
   const double th = nt_tables.ex.t[2 * j];
   const double tl = nt_tables.ex.t[2 * j + 1];
-  bad |= !(fabs(x) <= 708.0);
   return ldexp(th + fma(th, p, tl), m);
+}
+
+// The fast path with its range check; a caller that has bounded |x| <= 708
+// for the whole path beforehand calls nt_exp_core directly.
+__device__ __forceinline__ double nt_exp_fast(double x, bool& bad) {
+  bad |= !(fabs(x) <= 708.0);
+  return nt_exp_core(x);
 }
 
 // exp for any argument: the fast path, device libm where it does not apply.
@@ -127,7 +135,9 @@ __device__ __forceinline__ double nt_exp(double x) {
 __device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
   const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
   nt_u32 hx = nt_hi(u) + (0x3FF00000u - 0x3FE6A09Eu);
-  const int e = static_cast<int>(hx >> 20) - 0x3FF;
+  // e = (hx >> 20) - 1023 as a double: the biased exponent in the low word of
+  // 2^52 + (hx >> 20), less 2^52 + 1023 (exact), instead of a conversion
+  const double ed = nt_mk(0x43300000u, hx >> 20) - 0x1.00000000003ffp52;
   hx = (hx & 0x000FFFFFu) + 0x3FE6A09Eu;
   const double x = nt_mk(hx, nt_lo(u));
   const nt_u32 fhi = (hx + 0x800u) & 0xFFFFF000u;
@@ -138,7 +148,6 @@ __device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
   q = fma(r, q, NT_LOGQ_1);
   q = fma(r, q, NT_LOGQ_0);
   const double p = fma(r * r, q, r);  // -2 ln(1 + (x - F) / F)
-  const double ed = static_cast<double>(e);
   const double hi = fma(ed, NT_M2LN2_HI, nt_tables.lg.hi[idx]);  // exact by the table's layout
   const double lo = fma(ed, NT_M2LN2_LO, nt_tables.lg.lo[idx]) + p;
   return hi + lo;
@@ -159,14 +168,16 @@ __device__ __forceinline__ double nt_sqrt_pos(double a) {
 
 // sin and cos of theta = fl(6.283185307179586 * u) for u = (c + 0.5) * 2^-32.
 // The reference rounds its angle once, and so does this (theta is that
-// rounded product). The circle is cut in 512 sectors: c = j 2^23 + d with d
-// the sign-extended low 23 bits, so u = j/512 + f exactly, f = (d + 0.5)
-// 2^-32, |f| <= 2^-10 turns. With (S, C) = (sin, cos)(2 pi j/512) from the
-// table, sin(2 pi u) = S cos(2 pi f) + C sin(2 pi f) and cos(2 pi u) =
-// C cos(2 pi f) - S sin(2 pi f), the small-angle parts being polynomials in
-// f. The rounding of theta, eps = theta - 2 pi u, is known exactly (two FMAs)
-// and enters as sin(2 pi f + eps) = sin(2 pi f) + eps to first order (the
-// second-order terms are below 1e-17).
+// rounded product): the per-path results of the Heston tape move by a few
+// 1e-12 when the normals lose that rounding (4.7e-15 at most). The circle is
+// cut in 512 sectors: c = j 2^23 + d with d the sign-extended low 23 bits, so
+// u = j/512 + f exactly, f = (d + 0.5) 2^-32, |f| <= 2^-10 turns. With
+// (S, C) = (sin, cos)(2 pi j/512) from the table, sin(2 pi u) = S cos(2 pi f)
+// + C sin(2 pi f) and cos(2 pi u) = C cos(2 pi f) - S sin(2 pi f), the
+// small-angle parts being polynomials in f. The rounding of theta, eps =
+// theta - 2 pi u, is known exactly (two FMAs) and enters as sin(2 pi f + eps)
+// = sin(2 pi f) + eps to first order (the second-order terms are below
+// 1e-17).
 __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& co) {
   const int d = static_cast<int>(c << 9) >> 9;
   const nt_u32 j = (c - static_cast<nt_u32>(d)) >> 23;
@@ -184,6 +195,31 @@ __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& c
   const double C = nt_tables.sc.t[2 * j + 1];
   s = S + fma(C, sn, S * cm);
   co = C + fma(C, cm, -(S * sn));
+}
+
+// sqrt(a) and the tangent factor 1/(2 sqrt(a)) of a SQRT node, for a = +-0 or
+// a positive normal, where a correctly rounded sqrt and a division take two
+// dozen instructions. nt_sqrt_pos's coupled Newton step and residual
+// correction give the root; the factor after that step is low by 1.5 e^2 (e
+// the seed's relative error), the same sign every time, so a second step on
+// it (against the corrected root) brings it to full precision: in a carried
+// tangent (a variance process) a one-sided error would compound over the
+// steps. The seed is taken at max(a, 2^-1022), so a = +-0 gives sqrt = a and
+// a large finite factor (the derivative is infinite there; a zero tangent
+// stays zero, as with the capped factor of the libm path). Any other
+// argument (negative, subnormal, infinite, NaN) sets `bad`, and the caller
+// evaluates the path again with device libm.
+__device__ __forceinline__ double nt_sqrt_q(double a, double& q, bool& bad) {
+  bad |= !nt_zero_or_pos_normal(a);
+  const double y = nt_rsq(fmax(a, 0x1p-1022));
+  double g = a * y;
+  double h = 0.5 * y;
+  const double r = fma(-g, h, 0.5);
+  g = fma(g, r, g);
+  h = fma(h, r, h);
+  const double s = fma(fma(-g, g, a), h, g);
+  q = fma(h, fma(-s, h, 0.5), h);
+  return s;
 }
 #else
 __device__ __forceinline__ void nt_tables_load() {}

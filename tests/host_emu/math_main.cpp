@@ -24,6 +24,13 @@ void emu_exp(const double* x, double* out, long n) {
 void emu_sqrt(const double* a, double* out, long n) {
   for (long i = 0; i < n; ++i) out[i] = nt_sqrt_pos(a[i]);
 }
+void emu_sqrt_q(const double* a, double* out, double* q, int* bad, long n) {
+  for (long i = 0; i < n; ++i) {
+    bool b = false;
+    out[i] = nt_sqrt_q(a[i], q[i], b);
+    bad[i] = b ? 1 : 0;
+  }
+}
 void emu_normal_pair(const nt_u32* lo, const nt_u32* hi, const nt_u32* ctr, double* zc, double* zs, long n) {
   load_tables();
   for (long i = 0; i < n; ++i) nt_normal_pair(lo[i], hi[i], ctr[i], zc[i], zs[i]);

@@ -26,6 +26,10 @@ inline double nt_mk(unsigned hi, unsigned lo) {
   return x;
 }
 inline unsigned nt_xor3(unsigned a, unsigned b, unsigned c) { return a ^ b ^ c; }
+inline bool nt_zero_or_pos_normal(double x) {
+  const int c = std::fpclassify(x);
+  return c == FP_ZERO || (c == FP_NORMAL && !std::signbit(x));
+}
 // correctly rounded stand-in for the device's reciprocal-square-root seed
 inline double nt_rsq(double x) { return 1.0 / std::sqrt(x); }
 

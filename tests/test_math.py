@@ -32,6 +32,7 @@ def lib():
     L.emu_sincos.argtypes = [P(C.c_uint32), P(C.c_double), P(C.c_double), C.c_long]
     L.emu_sqrt.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
     L.emu_exp.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
+    L.emu_sqrt_q.argtypes = [P(C.c_double), P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
     L.emu_normal_pair.argtypes = [P(C.c_uint32)] * 3 + [P(C.c_double)] * 2 + [C.c_long]
     return L
 
@@ -97,6 +98,30 @@ def test_sqrt_within_one_ulp(lib):
     lib.emu_sqrt(_ptr(a, C.c_double), _ptr(out, C.c_double), len(a))
     err = np.abs(out - np.sqrt(a)) / np.spacing(np.sqrt(a))
     assert err.max() <= 1.0
+
+
+def test_sqrt_with_tangent_factor(lib):
+    """nt_sqrt_q: sqrt within 1 ulp and 1/(2 sqrt) within 2 ulp for
+    positive normals; +-0 give +-0 and a finite factor; every other class
+    (subnormal, negative, infinite, NaN) raises the flag."""
+    rng = np.random.default_rng(4)
+    normals = np.exp(rng.uniform(np.log(2.3e-308), np.log(1.7e308), 20000))
+    a = np.ascontiguousarray(np.concatenate([normals, [2.2250738585072014e-308, 1.0, 4.0, 0.25, 1.7976931348623157e308,
+                                                       0.0, -0.0, 5e-324, 1e-310, -1.0, -1e-300, np.inf, -np.inf,
+                                                       np.nan]]))
+    n = len(a)
+    out, q = np.zeros(n), np.zeros(n)
+    bad = np.zeros(n, dtype=np.int32)
+    lib.emu_sqrt_q(_ptr(a, C.c_double), _ptr(out, C.c_double), _ptr(q, C.c_double), _ptr(bad, C.c_int), n)
+    ok = (a > 0) & np.isfinite(a) & (a >= 2.2250738585072014e-308)
+    zero = a == 0.0
+    assert (bad[ok | zero] == 0).all() and (bad[~(ok | zero)] == 1).all()
+    r = np.sqrt(a[ok])
+    assert (np.abs(out[ok] - r) / np.spacing(r)).max() <= 1.0
+    hq = 0.5 / r
+    assert (np.abs(q[ok] - hq) / np.spacing(hq)).max() <= 2.0
+    assert (out[zero] == 0.0).all() and np.array_equal(np.signbit(out[zero]), np.signbit(a[zero]))
+    assert np.isfinite(q[zero]).all() and (q[zero] > 1e150).all()
 
 
 def test_normal_pairs_track_the_reference_formula(lib):
