@@ -1166,7 +1166,9 @@ std::string Emitter::smul(const std::string& ind, const std::string& s1, const s
 Emitter::Term Emitter::scaled(const std::string& ind, const std::string& T, const std::string& s, bool unwrap) {
   if (T == "#1") return Term{s.empty() ? std::string(f32_ ? "1.0f" : "1.0") : s, "", ""};
   auto it = lazy_.find(T);
-  if (it != lazy_.end() && (s.empty() || unwrap)) return lazy_term(it->second.first, smul(ind, it->second.second, s));
+  // T itself, still known as a scaling of its base; its variable is its value
+  if (it != lazy_.end() && s.empty()) return Term{T, it->second.first, it->second.second};
+  if (it != lazy_.end() && unwrap) return lazy_term(it->second.first, smul(ind, it->second.second, s));
   return lazy_term(T, s);
 }
 
@@ -1440,7 +1442,10 @@ void Emitter::tsegment(int U, const std::string& sg) {
             const std::string X = tx(k);
             const std::string name_k = "tr" + su + "_" + sj + "_" + sk + m;
             lazy_.erase(name_k);
-            const std::string e = X.empty() ? sp : sum(Term{sp, "", ""}, scaled(ind, X, "c0_" + sj + m, false)).expr;
+            // sigma_k + c0 tx_k (a scaled tx as its variable)
+            const std::string e = X.empty() ? sp
+                                            : f("fma") + "(c0_" + sj + m + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) +
+                                                  ", " + sp + ")";
             o_ << ind << "const real " << name_k << " = " << e << ";\n";
           }
           continue;
