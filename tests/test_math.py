@@ -5,6 +5,7 @@ formula."""
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 import tempfile
 from pathlib import Path
@@ -22,7 +23,7 @@ EMU = ROOT / "tests" / "host_emu"
 
 @pytest.fixture(scope="module")
 def lib():
-    out = Path(tempfile.gettempdir()) / "nt_math_emu.so"
+    out = Path(tempfile.gettempdir()) / f"nt_math_emu_{os.getpid()}.so"  # one per test worker
     subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-ffp-contract=off", "-w",
                     f"-I{ROOT / 'nablatensor_amd' / 'csrc'}", f"-I{EMU}", str(EMU / "math_main.cpp"),
                     "-o", str(out)], check=True)
