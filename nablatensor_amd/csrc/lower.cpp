@@ -1218,9 +1218,10 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
       // factor is capped at a finite 2^(max exponent) here: a zero tangent
       // (e.g. a full-truncation max(v, 0) that chose the constant) stays zero.
       // nt_sqrt_q has set it already where it computed the value.
+      // (A NaN root keeps a NaN factor, as the reverse rule's 0.5 / v does.)
       if (sqrt_q_ == q) break;
-      o_ << ind << "const real " << q << " = " << f("fmin") << "("
-         << (f32_ ? "0.5f * nt_rcpf(" + Vi + ")" : "0.5 / " + Vi) << ", " << (f32_ ? "0x1p127f" : "0x1p1023") << ");\n";
+      o_ << ind << "const real " << q << " = " << Vi << " == " << zero << " ? " << (f32_ ? "0x1p127f" : "0x1p1023")
+         << " : " << (f32_ ? "0.5f * nt_rcpf(" + Vi + ")" : "0.5 / " + Vi) << ";\n";
       break;
     case NT_OP_ABS: o_ << ind << "const real " << q << " = " << Va << " < " << zero << " ? -" << one << " : " << one << ";\n"; break;
     case NT_OP_MAX: o_ << ind << "const bool " << c << " = " << Va << " >= " << Vb << ";\n"; break;

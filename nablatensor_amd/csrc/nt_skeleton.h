@@ -178,9 +178,14 @@ __device__ __forceinline__ double nt_sqrt_pos(double a) {
 // theta - 2 pi u, is known exactly (two FMAs) and enters as sin(2 pi f + eps)
 // = sin(2 pi f) + eps to first order (the second-order terms are below
 // 1e-17).
+struct __attribute__((aligned(16))) NtPair {
+  double a, b;
+};
 __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& co) {
   const int d = static_cast<int>(c << 9) >> 9;
-  const nt_u32 j = (c - static_cast<nt_u32>(d)) >> 23;
+  // c - d = j 2^23, so its shift by 19 is the byte offset 16 j of the
+  // sector's (sin, cos) pair: one 16-byte load, no masking
+  const nt_u32 off = (c - static_cast<nt_u32>(d)) >> 19;
   const double f = fma(static_cast<double>(d), 0x1p-32, 0x1p-33);
   const double t = f * f;
   double ps = fma(t, NT_SC_S5, NT_SC_S3);
@@ -191,8 +196,9 @@ __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& c
   const double theta = NT_TWO_PI_D * u;
   const double eps = fma(NT_TWO_PI_D_ERR, u, -fma(NT_TWO_PI_D, u, -theta));
   const double sn = fma(f, ps, eps);  // sin(2 pi f) + eps
-  const double S = nt_tables.sc.t[2 * j];
-  const double C = nt_tables.sc.t[2 * j + 1];
+  const NtPair sc = *reinterpret_cast<const NtPair*>(reinterpret_cast<const char*>(nt_tables.sc.t) + off);
+  const double S = sc.a;
+  const double C = sc.b;
   s = S + fma(C, sn, S * cm);
   co = C + fma(C, cm, -(S * sn));
 }

@@ -147,3 +147,34 @@ def two_output_tape(nt, steps=40):
         rec.output("spot", s)
         rec.output("max", hi)
     return nt.AadRecorder.record(body)
+
+
+def scaled_exp_tape(nt, a, steps=16):
+    """s <- s exp(a z) per step: every exponent is a loop-invariant times a
+    normal draw, so the kernel bounds it once per path (6.77 |a| <= 708)
+    instead of checking each exponential; a = 300 fails that bound."""
+    def body(rec):
+        s0 = rec.input("S0", 1.0)
+        k = rec.input("a", a)
+        s = s0
+        for _ in range(steps):
+            s = s.mul(k.mul(rec.randn()).exp())
+        rec.output(s)
+    return nt.AadRecorder.record(body)
+
+
+def sqrt_classes_tape(nt, s_val, floor=True, steps=16):
+    """acc <- acc + w sqrt(x), x = max(z s, 0) (or z s without the floor): x
+    is +0 for z <= 0 (the max follows its constant, so no derivative flows
+    through the infinite factor of sqrt at 0) and subnormal for z > 0 when
+    s = 1e-310; without the floor x < 0 gives a NaN root."""
+    def body(rec):
+        s = rec.input("s", s_val)
+        w = rec.input("w", 1.0)
+        acc = w.mul(0.0)
+        for _ in range(steps):
+            z = rec.randn()
+            x = z.mul(s).max(0.0) if floor else z.mul(s)
+            acc = acc.add(x.sqrt().mul(w))
+        rec.output(acc)
+    return nt.AadRecorder.record(body)

@@ -220,3 +220,41 @@ def test_multi_output_per_path_and_sums(rocm, nt):
     ref = oracle.replay_sums(flat, 200_000, 0, 42, all_outputs=True)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-10
     assert np.array_equal(many[0], sums)
+
+
+@pytest.mark.parametrize("a,tol", [(0.3, 1e-12), (110.0, 1e-10)])
+def test_loop_exponent_bound_on_device(rocm, nt, a, tol):
+    """s exp(a z) over 16 steps, tangent mode: the exponents are bounded once
+    per path before the loop. With a = 0.3 every path stays on the table exp;
+    with a = 110 the bound (6.77 |a| = 745 > 708) sends every path to the
+    device-libm evaluation. The exponent a z multiplies the normals' own
+    difference from the oracle's (a few 1e-15) by a at each step, so a = 110
+    is held to 1e-10 per path."""
+    from conftest import scaled_exp_tape
+    flat = scaled_exp_tape(nt, a).flat()
+    print(f"case scaled exp a={a}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=2)) as x:
+        assert x.info()["mode"] == 2
+        v, g = x.replay_paths(4096, OFFSET, 5)
+    ov, og = oracle.replay_paths(flat, 4096, OFFSET, 5)
+    ev, eg = oracle.path_errors(v, g, ov, og)
+    finite = np.isfinite(ov) & np.isfinite(og).all(axis=1) & (np.abs(og) < 1e300).all(axis=1)
+    assert finite.sum() > 3000
+    assert ev.max() <= tol and eg[finite].max() <= tol, (ev.max(), eg[finite].max())
+
+
+@pytest.mark.parametrize("s_val,floor", [(1e-3, True), (1e-310, True), (1e-3, False)])
+def test_sqrt_routine_and_fallback_on_device(rocm, nt, s_val, floor):
+    """SQRT nodes in a tangent kernel: +0 arguments stay on nt_sqrt_q,
+    subnormal (s = 1e-310) and negative (no floor) arguments send the path to
+    device-libm sqrt; values and derivatives per path against the oracle,
+    NaN for NaN."""
+    from conftest import sqrt_classes_tape
+    flat = sqrt_classes_tape(nt, s_val, floor).flat()
+    print(f"case sqrt classes s={s_val} floor={floor}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=2)) as x:
+        v, g = x.replay_paths(4096, OFFSET, 9)
+    ov, og = oracle.replay_paths(flat, 4096, OFFSET, 9)
+    ev, eg = oracle.path_errors(v, g, ov, og)
+    assert ev.max() <= 1e-12 and eg.max() <= 1e-12, (ev.max(), eg.max())
+    assert np.array_equal(np.isnan(v), np.isnan(ov))

@@ -16,7 +16,7 @@ import pytest
 
 import emu
 import oracle
-from conftest import check_per_path, equity_tape, rel_err, tape_slots
+from conftest import check_per_path, equity_tape, rel_err, scaled_exp_tape, sqrt_classes_tape, tape_slots
 
 OFFSET = 0x100000003
 
@@ -217,6 +217,45 @@ def test_exp_outside_fast_range_falls_back_per_path(rocm):
         assert np.array_equal(np.isinf(v), np.isinf(ov))
         fast = ~beyond & np.isfinite(ov)
         assert ev[fast].max() <= 1e-12
+
+
+@pytest.mark.parametrize("a", [0.3, 300.0])
+def test_loop_exponent_bound_checked_once_per_path(nt, rocm, a):
+    """s exp(a z) per step: the tangent kernel bounds the exponents before the
+    loop (|a| 6.77 <= 708) and the loop's exponentials skip their own check;
+    with a = 300 every path fails the bound and is evaluated again with libm
+    exp (overflow and underflow included), agreeing with the oracle."""
+    flat = scaled_exp_tape(nt, a).flat()
+    src = rocm.lower(flat, rocm.options("fp64", mode=2))
+    assert "6.77 * fabs(" in src and "nt_exp_core(" in src
+    ov, og = oracle.replay_paths(flat, 600, 0, 5, threads=1)
+    if a > 1:
+        assert np.isinf(ov).any() and (ov == 0).any()
+    _, v, g = run_emulated(flat, rocm.options("fp64", mode=2, libm=2), 600, offset=0, seed=5, rocm=rocm)
+    ev, eg = oracle.path_errors(v, g, ov, og)
+    assert ev.max() <= 1e-12  # overflowed values agree as infinities, underflowed ones as zeros
+    # derivatives of overflowing products depend on the order of the products
+    # (reverse against forward accumulation); the finite paths are held to the bar
+    finite = np.isfinite(ov) & np.isfinite(og).all(axis=1) & (np.abs(og) < 1e300).all(axis=1)
+    assert finite.sum() > 100 and eg[finite].max() <= 1e-12
+
+
+@pytest.mark.parametrize("s_val,floor", [(1e-3, True), (1e-310, True), (1e-3, False)])
+def test_sqrt_fast_routine_and_its_fallback(nt, rocm, s_val, floor):
+    """SQRT nodes of tangent kernels take nt_sqrt_q: +0 arguments (z <= 0
+    under the floor) stay on it; subnormal arguments (s = 1e-310) and
+    negative ones (no floor: NaN roots) flag the path, which is evaluated
+    again with libm sqrt. Values and derivatives agree with the oracle,
+    NaN for NaN."""
+    flat = sqrt_classes_tape(nt, s_val, floor).flat()
+    assert "nt_sqrt_q(" in rocm.lower(flat, rocm.options("fp64", mode=2))
+    ov, og = oracle.replay_paths(flat, 300, 0, 9, threads=1)
+    if not floor:
+        assert np.isnan(ov).any()
+    _, v, g = run_emulated(flat, rocm.options("fp64", mode=2), 300, offset=0, seed=9, rocm=rocm)
+    ev, eg = oracle.path_errors(v, g, ov, og)
+    assert ev.max() <= 1e-12 and eg.max() <= 1e-12
+    assert np.array_equal(np.isnan(v), np.isnan(ov))
 
 
 @pytest.mark.parametrize("name,paths", [("C2", 200), ("C4", 64)])
