@@ -897,7 +897,7 @@ class Emitter {
   bool exp_fallback() const {
     if (f32_ || p_.libm == 1) return false;
     for (int i = 0; i < t_.n; ++i) {
-      if (t_.op[i] == NT_OP_EXP || (t_.op[i] == NT_OP_SQRT && fast_sqrt())) return true;
+      if (t_.op[i] == NT_OP_EXP || ((t_.op[i] == NT_OP_SQRT || t_.op[i] == NT_OP_DIV) && fast_sqrt())) return true;
     }
     return false;
   }
@@ -914,6 +914,10 @@ class Emitter {
     return "nt_sqrt_q(" + x + ", " + q + ", nt_slow" + ms(act) + ")";
   }
   std::string sqrt_q_;  // tangent factor of the SQRT just emitted, if nt_sqrt_q made it
+  // A DIV whose numerator is the constant 1 takes nt_recip in the same
+  // kernels; its value is then its own tangent factor 1/b.
+  bool is_one(int node) const { return t_.op[node] == NT_OP_CONST && t_.c[node] == 1.0; }
+  bool recip_ = false;  // the DIV just emitted is a nt_recip
   void header();
   void body_tangent();
   void body_reverse();
@@ -1208,7 +1212,8 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
   const std::string rcp_one = f32_ ? "nt_rcpf(" : "1.0 / (";
   switch (op) {
     case NT_OP_DIV:
-      o_ << ind << "const real " << q << " = " << rcp_one << Vb << ");\n";
+      // (1 / b from nt_recip is its own factor)
+      o_ << ind << "const real " << q << " = " << (recip_ ? Vi : rcp_one + Vb + ")") << ";\n";
       if (needB) o_ << ind << "const real " << r << " = " << Vi << " * " << q << ";\n";
       break;
     case NT_OP_LOG: o_ << ind << "const real " << q << " = " << rcp_one << Va << ");\n"; break;
@@ -1342,6 +1347,8 @@ void Emitter::tline(int lo, int hi) {
         o_ << "    real " << q << ";\n";
         val = sqrt_expr(x, q, act);
       }
+      recip_ = op == NT_OP_DIV && fast_sqrt() && !slow_ && is_one(t_.a[i]);
+      if (recip_) val = "nt_recip(" + y + ", nt_slow" + ms(act) + ")";
       o_ << "    const real v" << i << ms(act) << " = " << val << ";\n";
       if (!act || ar == 0 || !p_.adjoints) continue;
       const int a = t_.a[i], b = ar >= 2 ? t_.b[i] : -1;
@@ -1425,6 +1432,9 @@ void Emitter::tsegment(int U, const std::string& sg) {
           val = sqrt_expr(x, q, act);
         }
         if (op == NT_OP_EXP && bound_[j].on && !slow_ && !f32_ && p_.libm != 1) val = "nt_exp_core(" + x + ")";
+        recip_ = op == NT_OP_DIV && fast_sqrt() && !slow_ &&
+                 ((L_.kind_a[j] == ARG_BODY && is_one(s + L_.ref_a[j])) || (L_.kind_a[j] == ARG_INV && is_one(L_.ref_a[j])));
+        if (recip_) val = "nt_recip(" + y + ", nt_slow" + ms(act) + ")";
         o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
         if (!act || ar == 0 || !p_.adjoints) continue;
         if (geo(j)) {

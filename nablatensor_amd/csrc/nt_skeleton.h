@@ -51,6 +51,7 @@ __device__ __forceinline__ double nt_mk(nt_u32 hi, nt_u32 lo) {
   return __hiloint2double(static_cast<int>(hi), static_cast<int>(lo));
 }
 __device__ __forceinline__ double nt_rsq(double x) { return __builtin_amdgcn_rsq(x); }
+__device__ __forceinline__ double nt_rcp(double x) { return __builtin_amdgcn_rcp(x); }
 // x is -0, +0 or a positive normal number: one v_cmp_class_f64
 __device__ __forceinline__ bool nt_zero_or_pos_normal(double x) { return __builtin_amdgcn_class(x, 0x160); }
 // fp32 hardware transcendentals (quarter-rate VALU): exp2, log2, sqrt, and
@@ -164,6 +165,21 @@ __device__ __forceinline__ double nt_sqrt_pos(double a) {
   h = fma(h, r, h);
   const double d = fma(-g, g, a);
   return fma(d, h, g);
+}
+
+// 1/b for a DIV node whose numerator is the constant 1, in fp64 tangent
+// kernels (the value is also the node's tangent factor): the v_rcp_f64 seed
+// and two Newton steps give it within an ulp, where a correctly rounded
+// division takes eleven instructions. For |b| outside [2^-1022, 2^1022]
+// (zero, subnormal, huge, infinite, NaN) `bad` is set and the caller
+// evaluates the path again with device libm.
+__device__ __forceinline__ double nt_recip(double b, bool& bad) {
+  bad |= !(fabs(b) >= 0x1p-1022 && fabs(b) <= 0x1p1022);
+  double y = nt_rcp(b);
+  double e = fma(-b, y, 1.0);
+  y = fma(y, e, y);
+  e = fma(-b, y, 1.0);
+  return fma(y, e, y);
 }
 
 // sin and cos of theta = fl(6.283185307179586 * u) for u = (c + 0.5) * 2^-32.

@@ -31,6 +31,13 @@ void emu_sqrt_q(const double* a, double* out, double* q, int* bad, long n) {
     bad[i] = b ? 1 : 0;
   }
 }
+void emu_recip(const double* b, double* out, int* bad, long n) {
+  for (long i = 0; i < n; ++i) {
+    bool f = false;
+    out[i] = nt_recip(b[i], f);
+    bad[i] = f ? 1 : 0;
+  }
+}
 void emu_normal_pair(const nt_u32* lo, const nt_u32* hi, const nt_u32* ctr, double* zc, double* zs, long n) {
   load_tables();
   for (long i = 0; i < n; ++i) nt_normal_pair(lo[i], hi[i], ctr[i], zc[i], zs[i]);

@@ -32,6 +32,8 @@ inline bool nt_zero_or_pos_normal(double x) {
 }
 // correctly rounded stand-in for the device's reciprocal-square-root seed
 inline double nt_rsq(double x) { return 1.0 / std::sqrt(x); }
+// correctly rounded stand-in for the device's reciprocal seed
+inline double nt_rcp(double x) { return 1.0 / x; }
 
 struct nt_emu_dim3 {
   unsigned x = 0, y = 1, z = 1;

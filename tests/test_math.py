@@ -34,6 +34,7 @@ def lib():
     L.emu_sqrt.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
     L.emu_exp.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
     L.emu_sqrt_q.argtypes = [P(C.c_double), P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
+    L.emu_recip.argtypes = [P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
     L.emu_normal_pair.argtypes = [P(C.c_uint32)] * 3 + [P(C.c_double)] * 2 + [C.c_long]
     return L
 
@@ -123,6 +124,24 @@ def test_sqrt_with_tangent_factor(lib):
     assert (np.abs(q[ok] - hq) / np.spacing(hq)).max() <= 2.0
     assert (out[zero] == 0.0).all() and np.array_equal(np.signbit(out[zero]), np.signbit(a[zero]))
     assert np.isfinite(q[zero]).all() and (q[zero] > 1e150).all()
+
+
+def test_recip_within_one_ulp_and_its_range(lib):
+    """nt_recip: 1/b within 1 ulp for 2^-1022 <= |b| <= 2^1022, either sign;
+    zero, subnormal, larger, infinite and NaN arguments raise the flag."""
+    rng = np.random.default_rng(5)
+    mags = np.exp(rng.uniform(np.log(2.3e-308), np.log(4.4e307), 20000))
+    b = np.ascontiguousarray(np.concatenate([mags, -mags[:5000], [2.0**-1022, 2.0**1022, 1.0, -3.0, 0.0, -0.0, 1e-310,
+                                                                  2.0**1023, -1.7e308, np.inf, -np.inf, np.nan]]))
+    n = len(b)
+    out = np.zeros(n)
+    bad = np.zeros(n, dtype=np.int32)
+    lib.emu_recip(_ptr(b, C.c_double), _ptr(out, C.c_double), _ptr(bad, C.c_int), n)
+    with np.errstate(invalid="ignore"):
+        ok = (np.abs(b) >= 2.0**-1022) & (np.abs(b) <= 2.0**1022)
+    assert (bad[ok] == 0).all() and (bad[~ok] == 1).all()
+    r = 1.0 / b[ok]
+    assert (np.abs(out[ok] - r) / np.spacing(np.abs(r))).max() <= 1.0
 
 
 def test_normal_pairs_track_the_reference_formula(lib):
