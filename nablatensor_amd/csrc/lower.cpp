@@ -847,6 +847,13 @@ class Emitter {
   std::vector<char> geo_;  // per loop position
   void plan_geo_carries();
   bool geo(int pos) const { return pos >= 0 && pos < static_cast<int>(geo_.size()) && geo_[pos]; }
+  // A multiplicative carry that nothing in the body reads but itself (a
+  // worst-of basket's spots, read by the payoff only) carries G alone; its
+  // value is c0 G after the loop (c0 G, not the product of the roundings of
+  // every step: the same value to a few hundred ulps).
+  bool geo_free(int pos) const {
+    return geo(pos) && body_uses_[pos] == 1 + (L_.is_liveout[pos] ? 1 : 0);
+  }
   std::vector<int> uses_;       // per node: operand references + outputs
   std::vector<int> body_uses_;  // per loop position: references within and across iterations, + live-out
   void count_uses();
@@ -1435,7 +1442,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
         recip_ = op == NT_OP_DIV && fast_sqrt() && !slow_ &&
                  ((L_.kind_a[j] == ARG_BODY && is_one(s + L_.ref_a[j])) || (L_.kind_a[j] == ARG_INV && is_one(L_.ref_a[j])));
         if (recip_) val = "nt_recip(" + y + ", nt_slow" + ms(act) + ")";
-        o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
+        if (!(geo_free(j) && act && p_.adjoints)) o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
         if (!act || ar == 0 || !p_.adjoints) continue;
         if (geo(j)) {
           const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
@@ -1476,7 +1483,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
     for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
       m_ = m;
       const std::string sm = ms(act);
-      o_ << ind << "st" << j << sm << " = r" << (U - 1) << "_" << j << sm << ";\n";
+      if (!(geo_free(j) && act && p_.adjoints)) o_ << ind << "st" << j << sm << " = r" << (U - 1) << "_" << j << sm << ";\n";
       if (!act || !p_.adjoints) continue;
       if (geo(j)) o_ << ind << "gs" << j << sm << " = gq" << (U - 1) << "_" << j << sm << ";\n";
       for (int k : posdeplist(j)) {
@@ -1750,6 +1757,7 @@ void Emitter::body_tangent() {
       if (!geo(j)) continue;
       for (int m = mlo_; m < mhi_; ++m) {
         m_ = m;
+        if (geo_free(j)) o_ << "    st" << j << ms(true) << " = c0_" << j << ms(true) << " * gs" << j << ms(true) << ";\n";
         for (int k : posdeplist(j)) {
           o_ << "    ts" << j << "_" << k << ms(true) << " = gs" << j << ms(true) << " * ts" << j << "_" << k << ms(true)
              << ";\n";

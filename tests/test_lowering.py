@@ -11,6 +11,8 @@ gradients are held to the per-path bar instead.
 """
 from __future__ import annotations
 
+import re
+
 import numpy as np
 import pytest
 
@@ -19,6 +21,21 @@ import oracle
 from conftest import check_per_path, equity_tape, rel_err, scaled_exp_tape, sqrt_classes_tape, tape_slots
 
 OFFSET = 0x100000003
+
+
+def carries_g_alone(src: str) -> bool:
+    """The kernel carries a multiplicative carry as G alone and rebuilds its
+    value as c0 G after the loop: that value then differs from the oracle's
+    step-by-step product by rounding (about sqrt(steps) ulps), and the path
+    values are held to the per-path bar instead of bit equality."""
+    return re.search(r"st\d+ = c0_\d+ \* gs\d+;", src) is not None
+
+
+def assert_values_match(v, ov, src):
+    if carries_g_alone(src):
+        assert rel_err(v, ov) <= 1e-12
+    else:
+        assert np.array_equal(v, ov)
 
 
 def run_emulated(flat, opts, paths, offset=OFFSET, seed=42, grid=3, block=64, inputs=None, rocm=None):
@@ -50,11 +67,13 @@ def test_emulated_fp64_is_bit_exact(rocm, tapes, name, paths, ckpt):
 @pytest.mark.parametrize("name,paths", [("C1", 700), ("C2", 400), ("C3", 300), ("C4", 150), ("C5", 40)])
 def test_emulated_tangent_values_bit_exact_gradients_within_bar(rocm, tapes, name, paths):
     """Tangent mode: same forward arithmetic (values bit for bit with libm
-    Box-Muller); derivatives within the per-path bar."""
+    Box-Muller, but for a carry kept as G alone); derivatives within the
+    per-path bar."""
     flat = tapes[name]
-    sums, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=2), paths, rocm=rocm)
+    opts = rocm.options("fp64", libm=1, mode=2)
+    sums, v, g = run_emulated(flat, opts, paths, rocm=rocm)
     ov, _ = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
-    assert np.array_equal(v, ov)
+    assert_values_match(v, ov, rocm.lower(flat, opts))
     check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
     ref = oracle.replay_sums(flat, paths, OFFSET, 42, threads=1)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-12
@@ -128,8 +147,9 @@ def test_lookback_and_digital_tapes(nt, rocm):
         for ckpt in (1, 2, 3):
             _, v, g = run_emulated(flat, rocm.options("fp64", checkpoint=ckpt, libm=1, mode=1), 96, rocm=rocm)
             assert np.array_equal(v, ov) and np.array_equal(g, og), (product.label, ckpt)
-        _, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=2), 96, rocm=rocm)
-        assert np.array_equal(v, ov), product.label
+        opts = rocm.options("fp64", libm=1, mode=2)
+        _, v, g = run_emulated(flat, opts, 96, rocm=rocm)
+        assert_values_match(v, ov, rocm.lower(flat, opts))
         check_per_path(v, g, flat, 96, OFFSET, 42, min_strict=0.5)
 
 
