@@ -860,6 +860,13 @@ class Emitter {
   bool single_body_exp(int pos) const {
     return t_.op[L_.start + pos] == NT_OP_EXP && body_uses_[pos] == 1 && !L_.is_liveout[pos] && !L_.is_carry[pos];
   }
+  // 1 / b used by nothing else: a multiplicative carry c <- c / b (a survival
+  // probability) has the log-derivative -tb / b = -tb m, no division needed
+  bool single_body_recip(int pos) const {
+    if (t_.op[L_.start + pos] != NT_OP_DIV || body_uses_[pos] != 1 || L_.is_liveout[pos] || L_.is_carry[pos]) return false;
+    const int ka = L_.kind_a[pos], ra = L_.ref_a[pos];
+    return (ka == ARG_BODY && is_one(L_.start + ra)) || (ka == ARG_INV && is_one(ra));
+  }
   // fp32 tangent loops: exp(p + r s) (or exp(r s)) with p and r loop-invariant
   // and the sum and product used nowhere else becomes exp2(p' + r' s) with
   // p' = p log2(e) and r' = r log2(e) computed once per path, dropping the
@@ -1452,19 +1459,36 @@ void Emitter::tsegment(int U, const std::string& sg) {
           o_ << ind << "const real gq" << su << "_" << sj << m << " = "
              << (u > 0 ? "gq" + prev + "_" + sj + m : "gs" + sj + m) << " * " << body_value(u, ARG_BODY, e, false)
              << ";\n";
+          // the factor's log-derivative per input: tx for exp(x), -tb m for m = 1 / b
+          const bool recip = t_.op[s + e] == NT_OP_DIV;
           std::function<std::string(int)> tx;
-          body_tangent_operand(u, L_.kind_a[e], L_.ref_a[e], tx);
-          for (int k : posdeplist(j)) {
+          body_tangent_operand(u, recip ? L_.kind_b[e] : L_.kind_a[e], recip ? L_.ref_b[e] : L_.ref_a[e], tx);
+          const std::vector<int> Dj = posdeplist(j);
+          std::string cs = "c0_" + sj + m;  // sigma_k + cs X_k
+          bool shared = true;
+          if (recip) {
+            cs = scalar(ind, "(-(c0_" + sj + m + " * " + body_value(u, ARG_BODY, e, false) + "))");
+            // the tangents of b are scalings of one base per input: take them apart
+            // when two or more inputs share the scale
+            std::map<std::string, int> n;
+            for (int k : Dj) {
+              auto it = lazy_.find(tx(k));
+              if (it != lazy_.end()) ++n[it->second.second];
+            }
+            shared = false;
+            for (const auto& kv : n) shared |= kv.second >= 2;
+          }
+          for (int k : Dj) {
             const std::string sk = std::to_string(k);
             const std::string sp = u > 0 ? "tr" + prev + "_" + sj + "_" + sk + m : "ts" + sj + "_" + sk + m;
             const std::string X = tx(k);
             const std::string name_k = "tr" + su + "_" + sj + "_" + sk + m;
             lazy_.erase(name_k);
-            // sigma_k + c0 tx_k (a scaled tx as its variable)
-            const std::string e = X.empty() ? sp
-                                            : f("fma") + "(c0_" + sj + m + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) +
-                                                  ", " + sp + ")";
-            o_ << ind << "const real " << name_k << " = " << e << ";\n";
+            std::string ex;
+            if (X.empty()) ex = sp;
+            else if (!recip) ex = f("fma") + "(" + cs + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) + ", " + sp + ")";
+            else ex = sum(Term{sp, "", ""}, scaled(ind, X, cs, shared)).expr;
+            o_ << ind << "const real " << name_k << " = " << ex << ";\n";
           }
           continue;
         }
@@ -1504,7 +1528,7 @@ void Emitter::plan_geo_carries() {
     const bool b_self = L_.kind_b[j] == ARG_CARRY && L_.ref_b[j] == j;
     if (a_self == b_self) continue;
     const int ek = a_self ? L_.kind_b[j] : L_.kind_a[j], er = a_self ? L_.ref_b[j] : L_.ref_a[j];
-    if (ek != ARG_BODY || !single_body_exp(er)) continue;
+    if (ek != ARG_BODY || !(single_body_exp(er) || single_body_recip(er))) continue;
     // Worth it when the saving (one operation per input of the carry's
     // tangent) beats the multiply for G plus one multiply per input that some
     // consumer needs as an absolute tangent G sigma_k. A sum or difference
