@@ -1531,25 +1531,27 @@ void Emitter::plan_geo_carries() {
     if (ek != ARG_BODY || !(single_body_exp(er) || single_body_recip(er))) continue;
     // Worth it when the saving (one operation per input of the carry's
     // tangent) beats the multiply for G plus one multiply per input that some
-    // consumer needs as an absolute tangent G sigma_k. A sum or difference
-    // with an operand whose tangent also has input k takes G sigma_k as one
-    // fma and needs none.
+    // consumer needs as an absolute tangent G sigma_k. The tangent G sigma_k
+    // is a scaled tangent (base sigma_k, scale G): a unary rule, or a binary
+    // one whose other operand has no tangent for input k, scales it further
+    // at no cost per input, and a sum or difference takes it as one fma; a
+    // product, quotient, max or min with an operand that has a tangent for k
+    // as well pays the multiply.
     const std::vector<int> D = posdeplist(j);
     std::vector<char> need(static_cast<size_t>(t_.n_in), 0);
     for (int q = 0; q < L_.period; ++q) {
       const int oq = t_.op[L_.start + q];
       const int ar = arity(oq);
+      if (ar < 2 || oq == NT_OP_ADD || oq == NT_OP_SUB) continue;
       for (int slot = 0; slot < ar; ++slot) {
         const int kind = slot ? L_.kind_b[q] : L_.kind_a[q], ref = slot ? L_.ref_b[q] : L_.ref_a[q];
         if (!((kind == ARG_BODY || kind == ARG_CARRY) && ref == j) || (q == j && kind == ARG_CARRY)) continue;
         const int okind = slot ? L_.kind_a[q] : L_.kind_b[q], oref = slot ? L_.ref_a[q] : L_.ref_b[q];
         for (int k : D) {
-          bool fused = false;
-          if ((oq == NT_OP_ADD || oq == NT_OP_SUB) && ar == 2) {
-            if (okind == ARG_BODY || okind == ARG_CARRY) fused = poshas(oref, k) && !geo(oref) && oref != j;
-            else if (okind == ARG_INV) fused = has(oref, k);
-          }
-          if (!fused) need[k] = 1;
+          bool other = false;
+          if (okind == ARG_BODY || okind == ARG_CARRY) other = poshas(oref, k);
+          else if (okind == ARG_INV) other = has(oref, k);
+          if (other) need[k] = 1;
         }
       }
     }

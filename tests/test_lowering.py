@@ -372,10 +372,22 @@ def test_multiplicative_carry_tangents(nt, rocm, precision):
             assert np.all(v == 0.0) and np.all(np.abs(og[:, 0]) > 0.1) and np.all(og[:, 1] == 0.0)
 
 
-def test_multiplicative_carries_only_where_they_pay(rocm, tapes):
-    """The Asian spot (read by a sum), the Heston spot and the 16 worst-of
-    spots (read only after the loop) take G sigma, and so does the barrier's
-    survival product (a carry times 1 / (1 + e)); the barrier spot, read by
-    the smoothed barrier test through a product, keeps the product rule."""
+def test_multiplicative_carries_only_where_they_pay(nt, rocm, tapes):
+    """The Asian spot (read by a sum), the Heston spot, the 16 worst-of spots
+    (read only after the loop) and both barrier carries (the spot, read by
+    the smoothed barrier test through scalings, and the survival product, a
+    carry times 1 / (1 + e)) take G sigma. A carry multiplied by another
+    value with a tangent keeps the product rule (below)."""
     gs = {k: rocm.lower(tapes[k], rocm.options("fp32", mode=2)).count("real gs") for k in ("C2", "C3", "C4", "C5")}
-    assert gs == {"C2": 1, "C3": 1, "C4": 1, "C5": 16}
+    assert gs == {"C2": 1, "C3": 2, "C4": 1, "C5": 16}
+
+    def body(rec):
+        s = rec.input("S0", 100.0)
+        vol = rec.input("sigma", 0.2)
+        acc = s.mul(0.0)
+        for _ in range(16):
+            s = s.mul(vol.mul(rec.randn()).exp())
+            acc = acc.add(s.mul(vol))  # a product with a value that has a tangent for sigma
+        rec.output(acc)
+    flat = nt.AadRecorder.record(body).flat()
+    assert rocm.lower(flat, rocm.options("fp64", mode=2)).count("real gs") == 0
