@@ -852,7 +852,28 @@ class Emitter {
   // value is c0 G after the loop (c0 G, not the product of the roundings of
   // every step: the same value to a few hundred ulps).
   bool geo_free(int pos) const {
-    return geo(pos) && body_uses_[pos] == 1 + (L_.is_liveout[pos] ? 1 : 0);
+    if (!geo(pos)) return false;
+    const int own = 1 + (L_.is_liveout[pos] ? 1 : 0);
+    return body_uses_[pos] == own || (body_uses_[pos] == own + 1 && gsum_of_[pos] >= 0);
+  }
+  // A running sum A <- A + c of such a carry (the Asian average's sum of
+  // spots), read by nothing but itself, accumulates G instead: A = A0 + c0
+  // sum G after the loop. Per step that drops the carry's own multiply and,
+  // for an input whose sigma is constant 1 (c's own start value), the sum of
+  // tangents is that same sum of G.
+  std::vector<int> gsum_;     // per loop position: the geo carry a sum accumulates, or -1
+  std::vector<int> gsum_of_;  // per loop position: the sum that accumulates this geo carry, or -1
+  void plan_geo_sums();
+  // Inputs k for which the sum's tangent is its own value: the carry's sigma_k
+  // is the constant 1 (k is the carry's start value and no factor depends on
+  // it) and the sum starts with no tangent for k.
+  bool gsum_self(int a, int k) const {
+    const int j = gsum_[a];
+    if (j < 0) return false;
+    const int ij = L_.carry_init[j], ia = L_.carry_init[a];
+    const bool a_row = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+    const int e = a_row ? L_.ref_b[j] : L_.ref_a[j];  // the factor's loop position
+    return ij >= 0 && tname(ij, k) == "#1" && !poshas(e, k) && (ia < 0 || tname(ia, k).empty());
   }
   std::vector<int> uses_;       // per node: operand references + outputs
   std::vector<int> body_uses_;  // per loop position: references within and across iterations, + live-out
@@ -1449,6 +1470,10 @@ void Emitter::tsegment(int U, const std::string& sg) {
         recip_ = op == NT_OP_DIV && fast_sqrt() && !slow_ &&
                  ((L_.kind_a[j] == ARG_BODY && is_one(s + L_.ref_a[j])) || (L_.kind_a[j] == ARG_INV && is_one(L_.ref_a[j])));
         if (recip_) val = "nt_recip(" + y + ", nt_slow" + ms(act) + ")";
+        if (gsum_[j] >= 0 && act && p_.adjoints) {
+          // sum of G (the spots' sum is A0 + c0 sum G)
+          val = body_value(u, ARG_CARRY, j, false) + " + gq" + std::to_string(u) + "_" + std::to_string(gsum_[j]) + ms(true);
+        }
         if (!(geo_free(j) && act && p_.adjoints)) o_ << ind << "const real " << name << ms(act) << " = " << val << ";\n";
         if (!act || ar == 0 || !p_.adjoints) continue;
         if (geo(j)) {
@@ -1495,8 +1520,20 @@ void Emitter::tsegment(int U, const std::string& sg) {
         std::function<std::string(int)> ta, tb;
         body_tangent_operand(u, L_.kind_a[j], L_.ref_a[j], ta);
         body_tangent_operand(u, ar >= 2 ? L_.kind_b[j] : ARG_NONE, ar >= 2 ? L_.ref_b[j] : -1, tb);
-        tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", ms(true), posdeplist(j),
-                name + ms(true), x, y, ta, tb);
+        std::vector<int> Dj = posdeplist(j);
+        std::vector<int> self;  // a running sum of G: its tangent for these inputs is its value
+        if (gsum_[j] >= 0) {
+          std::vector<int> rest;
+          for (int k : Dj) (gsum_self(j, k) ? self : rest).push_back(k);
+          Dj = rest;
+        }
+        tangent(ind, op, "tr" + std::to_string(u) + "_" + std::to_string(j) + "_", ms(true), Dj, name + ms(true), x, y,
+                ta, tb);
+        for (int k : self) {
+          const std::string tk = "tr" + std::to_string(u) + "_" + std::to_string(j) + "_" + std::to_string(k) + ms(true);
+          lazy_.erase(tk);
+          o_ << ind << "const real " << tk << " = " << name << ms(true) << ";\n";
+        }
         sqrt_q_.clear();
       }
     }
@@ -1558,6 +1595,24 @@ void Emitter::plan_geo_carries() {
     int materialised = 0;
     for (int k : D) materialised += need[k];
     if (static_cast<int>(D.size()) - 1 - materialised > 0) geo_[j] = 1;
+  }
+}
+
+void Emitter::plan_geo_sums() {
+  gsum_.assign(L_.found ? L_.period : 0, -1);
+  gsum_of_.assign(L_.found ? L_.period : 0, -1);
+  if (!L_.found) return;
+  for (int a = 0; a < L_.period; ++a) {
+    if (!L_.is_carry[a] || !t_.active[L_.start + a] || t_.op[L_.start + a] != NT_OP_ADD) continue;
+    if (body_uses_[a] != 1 + (L_.is_liveout[a] ? 1 : 0)) continue;
+    const bool a_self = L_.kind_a[a] == ARG_CARRY && L_.ref_a[a] == a;
+    const bool b_self = L_.kind_b[a] == ARG_CARRY && L_.ref_b[a] == a;
+    if (a_self == b_self) continue;
+    const int ok = a_self ? L_.kind_b[a] : L_.kind_a[a], j = a_self ? L_.ref_b[a] : L_.ref_a[a];
+    if (ok != ARG_BODY || !geo(j) || gsum_of_[j] >= 0) continue;
+    if (body_uses_[j] != 2 + (L_.is_liveout[j] ? 1 : 0)) continue;
+    gsum_[a] = j;
+    gsum_of_[j] = a;
   }
 }
 
@@ -1760,7 +1815,8 @@ void Emitter::body_tangent() {
       const bool act = t_.active[L_.start + j] != 0;
       for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
         m_ = m;
-        o_ << "    real st" << j << ms(act) << " = " << (init >= 0 ? vname(init) : zero) << ";\n";
+        const bool gsum = gsum_[j] >= 0 && act && p_.adjoints;
+        o_ << "    real st" << j << ms(act) << " = " << (init >= 0 && !gsum ? vname(init) : zero) << ";\n";
         if (!act || !p_.adjoints) continue;
         for (int k : posdeplist(j)) {
           const std::string tin = init >= 0 ? tname(init, k) : "";
@@ -1784,6 +1840,12 @@ void Emitter::body_tangent() {
       for (int m = mlo_; m < mhi_; ++m) {
         m_ = m;
         if (geo_free(j)) o_ << "    st" << j << ms(true) << " = c0_" << j << ms(true) << " * gs" << j << ms(true) << ";\n";
+        if (gsum_of_[j] >= 0) {
+          const int a = gsum_of_[j];
+          const int init = L_.carry_init[a];
+          const std::string c = "c0_" + std::to_string(j) + ms(true) + " * st" + std::to_string(a) + ms(true);
+          o_ << "    st" << a << ms(true) << " = " << (init >= 0 ? vname(init) + " + " + c : c) << ";\n";
+        }
         for (int k : posdeplist(j)) {
           o_ << "    ts" << j << "_" << k << ms(true) << " = gs" << j << ms(true) << " * ts" << j << "_" << k << ms(true)
              << ";\n";
@@ -1871,6 +1933,7 @@ std::string Emitter::run() {
   plan_exp2_folds();
   plan_exp_bounds();
   plan_geo_carries();
+  plan_geo_sums();
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;
   const bool tangent = p_.mode == NT_MODE_TANGENT;
