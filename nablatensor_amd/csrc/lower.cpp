@@ -1490,19 +1490,16 @@ void Emitter::tsegment(int U, const std::string& sg) {
           body_tangent_operand(u, recip ? L_.kind_b[e] : L_.kind_a[e], recip ? L_.ref_b[e] : L_.ref_a[e], tx);
           const std::vector<int> Dj = posdeplist(j);
           std::string cs = "c0_" + sj + m;  // sigma_k + cs X_k
-          bool shared = true;
-          if (recip) {
-            cs = scalar(ind, "(-(c0_" + sj + m + " * " + body_value(u, ARG_BODY, e, false) + "))");
-            // the tangents of b are scalings of one base per input: take them apart
-            // when two or more inputs share the scale
-            std::map<std::string, int> n;
-            for (int k : Dj) {
-              auto it = lazy_.find(tx(k));
-              if (it != lazy_.end()) ++n[it->second.second];
-            }
-            shared = false;
-            for (const auto& kv : n) shared |= kv.second >= 2;
+          if (recip) cs = scalar(ind, "(-(c0_" + sj + m + " * " + body_value(u, ARG_BODY, e, false) + "))");
+          // X_k scaled (a base per input times a scale of the node): taken apart
+          // when two or more inputs share the scale, one fma per input
+          std::map<std::string, int> n;
+          for (int k : Dj) {
+            auto it = lazy_.find(tx(k));
+            if (it != lazy_.end()) ++n[it->second.second];
           }
+          bool shared = false;
+          for (const auto& kv : n) shared |= kv.second >= 2;
           for (int k : Dj) {
             const std::string sk = std::to_string(k);
             const std::string sp = u > 0 ? "tr" + prev + "_" + sj + "_" + sk + m : "ts" + sj + "_" + sk + m;
@@ -1511,7 +1508,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
             lazy_.erase(name_k);
             std::string ex;
             if (X.empty()) ex = sp;
-            else if (!recip) ex = f("fma") + "(" + cs + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) + ", " + sp + ")";
+            else if (!recip && !lazy_.count(X)) ex = f("fma") + "(" + cs + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) + ", " + sp + ")";
             else ex = sum(Term{sp, "", ""}, scaled(ind, X, cs, shared)).expr;
             o_ << ind << "const real " << name_k << " = " << ex << ";\n";
           }
