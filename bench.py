@@ -16,7 +16,9 @@ peak with the NT-FLOP v1 algorithmic count (nablatensor_amd/flops.py), using
 the kernel's own HIP-event duration on its stream. `cpu_baseline` times the
 CPU oracle (a C restatement of the reference's scalar `cpu` engine, OpenMP
 over contiguous path ranges) on this host on a bounded sample; the
-reference's Java engines cannot run here (no JDK).
+reference's Java engines cannot run here (no JDK). `workloads` reports the
+other benchmark configurations (European, barrier, Heston-Asian, worst-of)
+measured in the same run with fewer timed steps (--no-workloads skips them).
 """
 from __future__ import annotations
 
@@ -197,6 +199,29 @@ def other_workload(rocm, args) -> int:
     return 0
 
 
+# The other benchmark configurations, reported beside the headline in the default run: the engine's default
+# plan, each at the scenarios per dispatch its configuration names, fewer timed steps (these are
+# reports, not the headline).
+OTHER_WORKLOADS = (("C1", "fp64"), ("C3", "fp32"), ("C3", "fp64"), ("C4", "fp64"), ("C5", "fp32"), ("C5", "fp64"))
+
+
+def other_workloads(rocm, steps: int = 5, warmup: int = 1, ramp: float = 0.2) -> dict:
+    from nablatensor_amd import workloads
+
+    out = {}
+    for name, prec in OTHER_WORKLOADS:
+        desc, paths, seed, _ = workloads.DESCRIPTIONS[name]
+        m = measure(rocm, workload_tape(name), prec, paths, steps, warmup, seed, 0, 0, 0, ramp, name)
+        out[f"{name}_{prec}"] = {"workload": desc, "scenarios_per_step": paths, "seed": seed,
+                                 "value": m["value"], "unit": "scenarios/s", "ms_per_step": m["ms_per_step"],
+                                 "replay_kernel_ms": m["replay_kernel_ms"], "frac": m["roofline"]["frac"],
+                                 "peak_tflops": m["roofline"]["peak"], "mode": m["kernel"]["mode"],
+                                 "vgprs": m["kernel"]["vgprs"], "scratch_bytes": m["kernel"]["scratch_bytes"]}
+        print(f"[bench] {name} {prec} {m['value']:.3e} scen/s, {100 * m['roofline']['frac']:.1f} % of peak",
+              file=sys.stderr, flush=True)
+    return out
+
+
 def host_overheads(rocm, args) -> int:
     """Host-path costs around the replay kernel on the Asian 252 tape, fp64:
     building an executable (lowering + hipRTC compile, or a code-object cache
@@ -295,6 +320,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1_000_000)
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the other benchmark configurations reported beside the headline")
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
                     help="C2 (default) prints the headline line; the others print the same fields for that workload")
     ap.add_argument("--precision", choices=["fp64", "fp32"], default=None,
@@ -342,6 +369,7 @@ def main() -> int:
                       args.mode, args.ramp)
         print(f"[bench] fp32 {f32['kernel']['mode']} {f32['value']:.3e} scen/s", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(flat, args.cpu_sample, args.seed)
+    others = None if args.no_workloads else other_workloads(rocm)
     out = {
         "metric": "scenarios/sec for value+all Greeks (fp64), % of VALU FP64 peak",
         "value": f64["value"],
@@ -367,6 +395,7 @@ def main() -> int:
         "fp32": None if f32 is None else {k: f32[k] for k in ("value", "ms_per_step", "replay_kernel_ms",
                                                                "roofline", "kernel")},
         "cpu_baseline": cpu,
+        "workloads": others,
     }
     print(json.dumps(out), flush=True)
     return 0

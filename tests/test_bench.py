@@ -22,7 +22,7 @@ def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg,
             "roofline": {"bound": "valu", "kernel": "nt_replay", "achieved": 10.0, "peak": 78.6, "unit": "TFLOP/s",
                          "frac": 10.0 / 78.6, "traffic": None, "traffic_source": None, "algorithmic_bytes": 1,
                          "flops_per_scenario": 18723, "convention": "NT-FLOP v1"},
-            "kernel": {"vgprs": 100, "mode": resolved}}
+            "kernel": {"vgprs": 100, "scratch_bytes": 0, "mode": resolved}}
 
 
 @pytest.fixture
@@ -55,6 +55,9 @@ def test_headline_line_has_the_contract_fields(patched, monkeypatch, capsys):
     assert out["cpu_baseline"]["kind"] in ("port", "reference")
     assert out["reverse"]["kernel"]["mode"] == "reverse"
     assert out["fp32"]["value"] > 0
+    w = out["workloads"]
+    assert set(w) == {"C1_fp64", "C3_fp32", "C3_fp64", "C4_fp64", "C5_fp32", "C5_fp64"}
+    assert all(r["value"] > 0 and 0 < r["frac"] < 1 for r in w.values())
 
 
 @pytest.mark.parametrize("workload", ["C1", "C3", "C4", "C5"])
