@@ -61,11 +61,11 @@ def measured_traffic(precision: str, info: dict) -> dict | None:
 
 
 def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
-            waves=0, max_blocks=0):
+            waves=0, max_blocks=0, basis=0):
     from nablatensor_amd import flops
 
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves,
-                                                max_blocks=max_blocks)) as x:
+                                                max_blocks=max_blocks, basis=basis)) as x:
         info = x.info()
         # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
         # (untimed) before the warmup steps, so a short --warmup does not time
@@ -184,7 +184,7 @@ def other_workload(rocm, args) -> int:
         print(json.dumps(out), flush=True)
         return 0
     m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp,
-                args.workload, args.waves, args.max_blocks)
+                args.workload, args.waves, args.max_blocks, args.basis)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -312,6 +312,9 @@ def main() -> int:
     ap.add_argument("--mode", type=int, default=0, help="derivative mode (0 cost model, 1 reverse sweep, 2 tangent)")
     ap.add_argument("--max-blocks", type=int, default=0,
                     help="cap on the replay grid in blocks (0: one resident wave of blocks)")
+    ap.add_argument("--basis", type=int, default=0, choices=(0, 1, 2),
+                    help="with --workload/--precision: tangent loops over 1 the inputs, 2 the loop's parameters "
+                         "(0: the engine's choice)")
     ap.add_argument("--waves", type=int, default=0,
                     help="with --workload/--precision: minimum waves per SIMD asked of the compiler (0: the engine's choice)")
     ap.add_argument("--no-reverse", action="store_true", help="skip the reverse-sweep comparison run")

@@ -95,7 +95,11 @@ typedef struct nt_options {
                                sets from each path's draws (what nt_exec_replay_many compiles); 0 or 1 = one */
   int32_t waves;            /* replay kernel: ask the compiler for at least this many waves per SIMD (a register
                                budget; it may fail to meet it or spill); 0 = the engine's choice */
-  int32_t reserved[4];
+  int32_t basis;            /* tangent loops: the directions the step loop's tangents run over. 0 = the engine's
+                               choice, 1 = the inputs, 2 = the loop's parameters (the loop-invariant values the
+                               step reads and the carried values' start values), mapped back to the inputs
+                               once per path after the loop */
+  int32_t reserved[3];
 } nt_options;
 
 typedef struct nt_exec nt_exec;

@@ -345,6 +345,8 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   p.markets = std::max(1, o.markets);
   if (o.waves < 0 || o.waves > 8) { err = "waves must be between 0 and 8"; return NT_E_INVALID; }
   p.waves = o.waves;
+  if (o.basis < 0 || o.basis > 2) { err = "basis must be 0, 1 or 2"; return NT_E_INVALID; }
+  p.basis = o.basis;
   if (p.markets > 1 && o.mode == NT_MODE_REVERSE) {
     err = "several markets per dispatch share draws in tangent mode only";
     return NT_E_INVALID;
@@ -790,6 +792,10 @@ class Emitter {
     return (p_.deps[static_cast<size_t>(node) * p_.n_words + (j >> 6)] >> (j & 63)) & 1;
   }
   bool poshas(int pos, int j) const {
+    if (par_on_) {
+      const int d = j - t_.n_in;
+      return d >= 0 && d < static_cast<int>(par_node_.size()) && par_deps_[pos][d];
+    }
     return (p_.posdeps[static_cast<size_t>(pos) * p_.n_words + (j >> 6)] >> (j & 63)) & 1;
   }
   std::vector<int> deplist(int node) const {
@@ -799,10 +805,35 @@ class Emitter {
   }
   std::vector<int> posdeplist(int pos) const {
     std::vector<int> d;
-    for (int j = 0; j < t_.n_in; ++j) if (poshas(pos, j)) d.push_back(j);
+    const int lo = par_on_ ? t_.n_in : 0, hi = par_on_ ? t_.n_in + static_cast<int>(par_node_.size()) : t_.n_in;
+    for (int j = lo; j < hi; ++j) if (poshas(pos, j)) d.push_back(j);
     return d;
   }
   std::string tname(int node, int j) const;  // straight-line node or loop live-out
+  // Loop parameters (tangent loops). The step body reads a few loop-invariant
+  // values (a drift, a volatility per step) and the carried values' start
+  // values; each is a function of the inputs. The loop's tangents can run
+  // over those parameters instead of over the inputs (the chain rule taken
+  // at the loop's boundary): the tangent of a parameter with respect to
+  // itself is 1, so the body multiplies by no input tangent, and after the
+  // loop each carried tangent returns to the inputs as the sum over
+  // parameters of (tangent per parameter) x (the parameter's tangent per
+  // input), once per path. Worth it when the body's tangents depend on fewer
+  // parameters than inputs: the Asian step's log-return depends on 2
+  // parameters (drift, volatility) against 3 inputs (r, sigma, T). Inside
+  // the loop, direction n_in + d stands for parameter d.
+  bool par_on_ = false;                     // emitting (or planning) the loop over parameters
+  bool use_par_ = false;                    // the loop runs over parameters
+  std::vector<int> par_node_;               // parameter -> node outside the loop
+  std::map<int, int> par_of_;               // node -> parameter
+  std::vector<std::vector<char>> par_deps_; // per loop position, per parameter
+  void plan_parameters();
+  // The tangent of a value from outside the loop, for input (or parameter) j.
+  std::string inv_tname(int node, int j) const {
+    if (!par_on_) return tname(node, j);
+    auto it = par_of_.find(node);
+    return it != par_of_.end() && it->second == j - t_.n_in ? "#1" : "";
+  }
   // Scaled tangents. A node whose tangent is its operand's tangent times a
   // local factor (EXP, LOG, SQRT, ABS, NEG, a product or quotient with a value
   // that has no tangent, a max/min that follows one operand) keeps, per input,
@@ -873,7 +904,7 @@ class Emitter {
     const int ij = L_.carry_init[j], ia = L_.carry_init[a];
     const bool a_row = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
     const int e = a_row ? L_.ref_b[j] : L_.ref_a[j];  // the factor's loop position
-    return ij >= 0 && tname(ij, k) == "#1" && !poshas(e, k) && (ia < 0 || tname(ia, k).empty());
+    return ij >= 0 && inv_tname(ij, k) == "#1" && !poshas(e, k) && (ia < 0 || inv_tname(ia, k).empty());
   }
   std::vector<int> uses_;       // per node: operand references + outputs
   std::vector<int> body_uses_;  // per loop position: references within and across iterations, + live-out
@@ -1420,7 +1451,7 @@ void Emitter::body_tangent_operand(int u, int kind, int ref, std::function<std::
                    : "ts" + std::to_string(ref) + "_" + std::to_string(j) + m;
     };
   } else if (kind == ARG_INV) {
-    fn = [this, ref](int j) { return tname(ref, j); };
+    fn = [this, ref](int j) { return inv_tname(ref, j); };
   } else {
     fn = [](int) { return std::string(); };
   }
@@ -1572,7 +1603,7 @@ void Emitter::plan_geo_carries() {
     // product, quotient, max or min with an operand that has a tangent for k
     // as well pays the multiply.
     const std::vector<int> D = posdeplist(j);
-    std::vector<char> need(static_cast<size_t>(t_.n_in), 0);
+    std::vector<char> need(static_cast<size_t>(t_.n_in) + par_node_.size(), 0);  // per input or parameter
     for (int q = 0; q < L_.period; ++q) {
       const int oq = t_.op[L_.start + q];
       const int ar = arity(oq);
@@ -1584,7 +1615,7 @@ void Emitter::plan_geo_carries() {
         for (int k : D) {
           bool other = false;
           if (okind == ARG_BODY || okind == ARG_CARRY) other = poshas(oref, k);
-          else if (okind == ARG_INV) other = has(oref, k);
+          else if (okind == ARG_INV) other = !inv_tname(oref, k).empty();
           if (other) need[k] = 1;
         }
       }
@@ -1593,6 +1624,75 @@ void Emitter::plan_geo_carries() {
     for (int k : D) materialised += need[k];
     if (static_cast<int>(D.size()) - 1 - materialised > 0) geo_[j] = 1;
   }
+}
+
+// The loop's parameters: the values from outside the loop that active body
+// positions read, and the start values of active carries (a node read both
+// ways is one parameter: its tangent for each input counts once). A loop
+// position depends on a parameter it reads, directly, through an earlier
+// position or through a carry (whose state starts at its start value).
+void Emitter::plan_parameters() {
+  use_par_ = false;
+  par_on_ = false;
+  par_node_.clear();
+  par_of_.clear();
+  par_deps_.clear();
+  if (!L_.found || p_.mode != NT_MODE_TANGENT || !p_.adjoints || p_.basis == 1) return;
+  const int P = L_.period, s = L_.start;
+  auto add = [&](int node) {
+    if (node < 0 || !t_.active[node] || par_of_.count(node)) return;
+    par_of_[node] = static_cast<int>(par_node_.size());
+    par_node_.push_back(node);
+  };
+  for (int j = 0; j < P; ++j) {
+    if (!t_.active[s + j]) continue;
+    const int ar = arity(t_.op[s + j]);
+    if (ar >= 1 && L_.kind_a[j] == ARG_INV) add(L_.ref_a[j]);
+    if (ar >= 2 && L_.kind_b[j] == ARG_INV) add(L_.ref_b[j]);
+    if (L_.is_carry[j]) add(L_.carry_init[j]);
+  }
+  const int nd = static_cast<int>(par_node_.size());
+  par_deps_.assign(static_cast<size_t>(P), std::vector<char>(static_cast<size_t>(nd), 0));
+  for (bool changed = true; changed;) {
+    changed = false;
+    auto mark = [&](std::vector<char>& d, int q) {
+      if (!d[q]) d[q] = 1, changed = true;
+    };
+    for (int j = 0; j < P; ++j) {
+      if (!t_.active[s + j]) continue;
+      std::vector<char>& d = par_deps_[j];
+      if (L_.is_carry[j]) {
+        auto it = par_of_.find(L_.carry_init[j]);
+        if (it != par_of_.end()) mark(d, it->second);
+      }
+      const int ar = arity(t_.op[s + j]);
+      for (int slot = 0; slot < ar; ++slot) {
+        const int kind = slot ? L_.kind_b[j] : L_.kind_a[j], ref = slot ? L_.ref_b[j] : L_.ref_a[j];
+        if (kind == ARG_INV) {
+          auto it = par_of_.find(ref);
+          if (it != par_of_.end()) mark(d, it->second);
+        } else if (kind == ARG_BODY || kind == ARG_CARRY) {
+          for (int q = 0; q < nd; ++q) {
+            if (par_deps_[ref][q]) mark(d, q);
+          }
+        }
+      }
+    }
+  }
+  // Tangents per step: one per (active position, input or parameter) pair;
+  // the parameters win when they make fewer. On a tie, fp32 takes them too:
+  // a parameter's tangent for itself is 1, so the rules that read it multiply
+  // by nothing (the worst-of basket: 128 tangents per step either way, 3 %
+  // fewer instructions over parameters; measured 2.4 % faster in fp32 and
+  // 3 % slower in fp64, whose kernel runs one wave per SIMD and depends on
+  // the schedule's slack more than on the instruction count).
+  int by_input = 0, by_par = 0;
+  for (int j = 0; j < P; ++j) {
+    if (!t_.active[s + j]) continue;
+    by_input += popcount(&p_.posdeps[static_cast<size_t>(j) * p_.n_words], p_.n_words);
+    for (char c : par_deps_[j]) by_par += c;
+  }
+  use_par_ = p_.basis == 2 || (by_par > 0 && (by_par < by_input || (by_par == by_input && f32_)));
 }
 
 void Emitter::plan_geo_sums() {
@@ -1738,7 +1838,8 @@ void Emitter::header() {
        << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
   }
   if (tangent) {
-    o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent\n";
+    o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent basis="
+       << (use_par_ ? "params" : "inputs") << " params=" << (use_par_ ? par_node_.size() : 0) << "\n";
     // Polynomial constants held in VGPRs make v_fmac_f64 (accumulator tied to
     // the destination) cost a 64-bit copy per term; the three-source v_fma_f64
     // needs none. (The reverse sweep below asks for the same.)
@@ -1806,6 +1907,7 @@ void Emitter::body_tangent() {
         o_ << "    const real " << l2e_name(node) << " = " << vname(node) << " * 1.44269504088896341f;\n";
       }
     }
+    par_on_ = use_par_;
     for (int j = 0; j < L_.period; ++j) {
       if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
       const int init = L_.is_carry[j] ? L_.carry_init[j] : -1;
@@ -1816,7 +1918,7 @@ void Emitter::body_tangent() {
         o_ << "    real st" << j << ms(act) << " = " << (init >= 0 && !gsum ? vname(init) : zero) << ";\n";
         if (!act || !p_.adjoints) continue;
         for (int k : posdeplist(j)) {
-          const std::string tin = init >= 0 ? tname(init, k) : "";
+          const std::string tin = init >= 0 ? inv_tname(init, k) : "";
           o_ << "    real ts" << j << "_" << k << ms(true) << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin)
              << ";\n";
         }
@@ -1846,6 +1948,29 @@ void Emitter::body_tangent() {
         for (int k : posdeplist(j)) {
           o_ << "    ts" << j << "_" << k << ms(true) << " = gs" << j << ms(true) << " * ts" << j << "_" << k << ms(true)
              << ";\n";
+        }
+      }
+    }
+    if (par_on_) {
+      // back to the inputs: t_k = sum over parameters d of t_d x (d's tangent for input k)
+      par_on_ = false;
+      const int nin = t_.n_in;
+      for (int j = 0; j < L_.period; ++j) {
+        if (!(L_.is_carry[j] || L_.is_liveout[j]) || !t_.active[L_.start + j]) continue;
+        for (int m = mlo_; m < mhi_; ++m) {
+          m_ = m;
+          for (int k : posdeplist(j)) {
+            std::string e;
+            for (size_t d = 0; d < par_node_.size(); ++d) {
+              if (!par_deps_[j][d]) continue;
+              const std::string T = tname(par_node_[d], k);
+              if (T.empty()) continue;
+              const std::string td = "ts" + std::to_string(j) + "_" + std::to_string(nin + static_cast<int>(d)) + ms(true);
+              if (T == "#1") e = e.empty() ? td : "(" + e + " + " + td + ")";
+              else e = e.empty() ? "(" + td + " * " + T + ")" : f("fma") + "(" + td + ", " + T + ", " + e + ")";
+            }
+            o_ << "    const real ts" << j << "_" << k << ms(true) << " = " << (e.empty() ? zero : e) << ";\n";
+          }
         }
       }
     }
@@ -1929,8 +2054,11 @@ std::string Emitter::run() {
   count_uses();
   plan_exp2_folds();
   plan_exp_bounds();
+  plan_parameters();
+  par_on_ = use_par_;
   plan_geo_carries();
   plan_geo_sums();
+  par_on_ = false;
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;
   const bool tangent = p_.mode == NT_MODE_TANGENT;

@@ -67,6 +67,7 @@ struct Plan {
   int mode = NT_MODE_REVERSE;             // resolved NT_MODE_REVERSE or NT_MODE_TANGENT
   int markets = 1;                        // input sets per dispatch sharing each path's draws (tangent mode)
   int waves = 0;                          // launch-bound hint: minimum waves per SIMD (0: none)
+  int basis = 0;                          // tangent loops: 0 cost model, 1 inputs, 2 loop parameters
   int n_words = 0;                        // 64-bit words per dependency set
   std::vector<uint64_t> deps;             // node -> inputs it depends on (bitset), tangent mode
   std::vector<uint64_t> posdeps;          // loop position -> union over the iterations

@@ -500,6 +500,7 @@ std::unique_ptr<AadExecutable> RocmAadEngine::compile(TapePtr tape, const AadOpt
   o.libm = optionInt(options, "libm", 0);
   o.mode = optionInt(options, "mode", 0);
   o.waves = optionInt(options, "waves", 0);
+  o.basis = optionInt(options, "basis", 0);
   const auto t0 = std::chrono::steady_clock::now();
   nt_exec* exec = nullptr;
   int rc = a.create(&ct, &o, &exec);

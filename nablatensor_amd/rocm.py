@@ -37,7 +37,8 @@ class NtOptions(C.Structure):
     _fields_ = [("precision", C.c_int32), ("adjoints", C.c_int32), ("block", C.c_int32),
                 ("max_blocks", C.c_int32), ("checkpoint", C.c_int32), ("seg_len", C.c_int32),
                 ("roll", C.c_int32), ("contract", C.c_int32), ("libm", C.c_int32), ("mode", C.c_int32),
-                ("markets", C.c_int32), ("waves", C.c_int32), ("reserved", C.c_int32 * 4)]
+                ("markets", C.c_int32), ("waves", C.c_int32), ("basis", C.c_int32),
+                ("reserved", C.c_int32 * 3)]
 
 
 class NtExecInfo(C.Structure):
@@ -140,9 +141,9 @@ def wire_digest(flat: dict) -> str:
 
 def options(precision: str = "fp64", adjoints: bool = True, block: int = 0, max_blocks: int = 0,
             checkpoint: int = NT_CKPT_AUTO, seg_len: int = 0, roll: int = 1, contract: int = 0,
-            libm: int = 0, mode: int = 0, markets: int = 0, waves: int = 0) -> NtOptions:
+            libm: int = 0, mode: int = 0, markets: int = 0, waves: int = 0, basis: int = 0) -> NtOptions:
     return NtOptions(NT_FP32 if precision == "fp32" else NT_FP64, 1 if adjoints else 0, block, max_blocks,
-                     checkpoint, seg_len, roll, contract, libm, mode, markets, waves)
+                     checkpoint, seg_len, roll, contract, libm, mode, markets, waves, basis)
 
 
 def probe() -> int:

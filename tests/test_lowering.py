@@ -395,3 +395,67 @@ def test_multiplicative_carries_only_where_they_pay(nt, rocm, tapes):
         rec.output(acc)
     flat = nt.AadRecorder.record(body).flat()
     assert rocm.lower(flat, rocm.options("fp64", mode=2)).count("real gs") == 0
+
+
+@pytest.mark.parametrize("name,paths", [("C2", 300), ("C3", 200), ("C4", 100), ("C5", 30)])
+def test_loop_tangents_over_parameters_or_inputs(rocm, tapes, name, paths):
+    """The step loop's tangents run over the loop's parameters (the
+    loop-invariant values the step reads, the carries' start values) and go
+    back to the inputs once per path after the loop, or run over the inputs
+    directly: the same values bit for bit, derivatives within the per-path
+    bar of the oracle in both, and within 1e-12 of each other."""
+    flat = tapes[name]
+    ov, og = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
+    grads = {}
+    for basis in (1, 2):
+        opts = rocm.options("fp64", libm=1, mode=2, basis=basis)
+        src = rocm.lower(flat, opts)
+        assert tape_plan(src)["basis"] == ("inputs" if basis == 1 else "params")
+        _, v, g = run_emulated(flat, opts, paths, rocm=rocm)
+        assert_values_match(v, ov, src)
+        check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
+        grads[basis] = g
+    assert rel_err(grads[2], grads[1]) <= 1e-12
+
+
+def test_loop_basis_chosen_by_tangents_per_step(rocm, tapes):
+    """The engine runs the loop over parameters where that makes fewer
+    tangents per step (the Asian step: drift and volatility against r,
+    sigma and T; the barrier), in fp32 also where it makes as many (the
+    worst-of basket), and over the inputs where the parameters outnumber
+    them (Heston's step reads more invariant values than it has inputs)."""
+    plan = {k: tape_plan(rocm.lower(tapes[k], rocm.options("fp64", mode=2))) for k in ("C2", "C3", "C4", "C5")}
+    assert {k: v["basis"] for k, v in plan.items()} == {"C2": "params", "C3": "params", "C4": "inputs", "C5": "inputs"}
+    assert tape_plan(rocm.lower(tapes["C5"], rocm.options("fp32", mode=2)))["basis"] == "params"
+    assert plan["C2"]["params"] == "3"  # drift, volatility, the spot's start value
+
+
+def _shared_parameter_tape(nt):
+    """The start value of the carried spot is also read by every step (a
+    floor proportional to it): one parameter for both, whose tangent for
+    itself is 1 in both roles."""
+    def body(rec):
+        s0 = rec.input("S0", 100.0)
+        vol = rec.input("sigma", 0.25)
+        k = rec.input("K", 98.0)
+        x = s0
+        acc = s0.mul(0.0)
+        for _ in range(16):
+            x = x.mul(vol.mul(rec.randn()).exp()).max(s0.mul(0.8))
+            acc = acc.add(x.sub(k).max(0.0))
+        rec.output(acc)
+    return nt.AadRecorder.record(body).flat()
+
+
+def test_parameter_read_both_as_start_value_and_in_the_step(nt, rocm):
+    flat = _shared_parameter_tape(nt)
+    src = rocm.lower(flat, rocm.options("fp64", mode=2, basis=2))
+    # S0 (the spot's start value, and read by the floor's product), sigma, K,
+    # and the sum's start value S0 * 0 (a node of its own)
+    assert tape_plan(src)["params"] == "4"
+    ov, og = oracle.replay_paths(flat, 256, OFFSET, 5, threads=1)
+    for basis in (1, 2):
+        _, v, g = run_emulated(flat, rocm.options("fp64", mode=2, libm=1, basis=basis), 256, seed=5, rocm=rocm)
+        ev, eg = oracle.path_errors(v, g, ov, og)
+        assert ev.max() <= 1e-13 and eg.max() <= 1e-12, basis
+    assert np.any(og[:, 0] != 0.0) and np.any(og[:, 2] != 0.0)
