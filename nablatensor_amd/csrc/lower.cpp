@@ -938,10 +938,19 @@ class Emitter {
   struct ExpBound {
     bool on = false;
     int p = -1, r = -1;  // invariant nodes (p = -1: no offset)
+    int sum = -1, mul = -1, draw = -1;  // loop positions of p +- r z, r z and z
+    bool p_first = true;                // p - r z (or a sum) rather than r z - p
   };
   std::vector<ExpBound> bound_;  // per loop position
   void plan_exp_bounds();
   void exp_bound_checks();
+  // p + r z feeding only such an exponential, itself only a multiplicative
+  // carry's factor, is one fma: fused rounding moves the exponent by an ulp
+  // at most, which the carry, kept as a product of factors G (its value
+  // rebuilt as c0 G or summed as sum G after the loop, not the oracle's
+  // step-by-step product anyway), does not resolve.
+  std::vector<int> fused_exp_;  // per loop position: the exponential whose argument this sum is, or -1
+  void plan_fused_exponents();
   std::string l2e_name(int node) const { return "v" + std::to_string(node) + "_l2e" + ms(t_.active[node]); }
   void tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx, const std::vector<int>& D,
                const std::string& Vi, const std::string& Va, const std::string& Vb,
@@ -1501,6 +1510,13 @@ void Emitter::tsegment(int U, const std::string& sg) {
         recip_ = op == NT_OP_DIV && fast_sqrt() && !slow_ &&
                  ((L_.kind_a[j] == ARG_BODY && is_one(s + L_.ref_a[j])) || (L_.kind_a[j] == ARG_INV && is_one(L_.ref_a[j])));
         if (recip_) val = "nt_recip(" + y + ", nt_slow" + ms(act) + ")";
+        if (fused_exp_[j] >= 0 && p_.adjoints) {
+          const ExpBound& b = bound_[fused_exp_[j]];
+          const std::string rv = body_value(u, ARG_INV, b.r, false), pv = body_value(u, ARG_INV, b.p, false);
+          const std::string z = body_value(u, ARG_BODY, b.draw, false);
+          const bool sub = op == NT_OP_SUB;
+          val = f("fma") + "(" + (sub && b.p_first ? "-" + rv : rv) + ", " + z + ", " + (sub && !b.p_first ? "-" + pv : pv) + ")";
+        }
         if (gsum_[j] >= 0 && act && p_.adjoints) {
           // sum of G (the spots' sum is A0 + c0 sum G)
           val = body_value(u, ARG_CARRY, j, false) + " + gq" + std::to_string(u) + "_" + std::to_string(gsum_[j]) + ms(true);
@@ -1753,7 +1769,8 @@ void Emitter::plan_exp_bounds() {
   auto is_normal_draw = [&](int kind, int ref) {
     return kind == ARG_BODY && t_.op[L_.start + ref] == NT_OP_RANDN;
   };
-  // r z with r invariant: the node at loop position m; sets r
+  // r z with r invariant: the node at loop position m; sets r and the draw's position
+  int draw = -1;
   auto scaled_draw = [&](int m, int& r) {
     if (t_.op[L_.start + m] != NT_OP_MUL) return false;
     for (int side = 0; side < 2; ++side) {
@@ -1761,6 +1778,7 @@ void Emitter::plan_exp_bounds() {
       const int dk = side ? L_.kind_a[m] : L_.kind_b[m], dr = side ? L_.ref_a[m] : L_.ref_b[m];
       if (ik == ARG_INV && is_normal_draw(dk, dr)) {
         r = ir;
+        draw = dr;
         return true;
       }
     }
@@ -1779,10 +1797,30 @@ void Emitter::plan_exp_bounds() {
         if (ik == ARG_INV && mk == ARG_BODY && scaled_draw(mr, b.r)) {
           b.p = ir;
           b.on = true;
+          b.sum = a;
+          b.mul = mr;
+          b.p_first = side == 0 || t_.op[L_.start + a] == NT_OP_ADD;
         }
       }
     }
-    if (b.on) bound_[j] = b;
+    if (b.on) {
+      b.draw = draw;
+      bound_[j] = b;
+    }
+  }
+}
+
+void Emitter::plan_fused_exponents() {
+  fused_exp_.assign(L_.found ? L_.period : 0, -1);
+  if (!L_.found) return;
+  for (int c = 0; c < L_.period; ++c) {
+    if (!geo(c) || !(geo_free(c) || gsum_of_[c] >= 0)) continue;
+    const bool a_self = L_.kind_a[c] == ARG_CARRY && L_.ref_a[c] == c;
+    const int e = a_self ? L_.ref_b[c] : L_.ref_a[c];
+    if (t_.op[L_.start + e] != NT_OP_EXP || !single_body_exp(e)) continue;
+    const ExpBound& b = bound_[e];
+    if (!b.on || b.sum < 0 || body_uses_[b.sum] != 1 || body_uses_[b.mul] != 1) continue;
+    fused_exp_[b.sum] = e;
   }
 }
 
@@ -2058,6 +2096,7 @@ std::string Emitter::run() {
   par_on_ = use_par_;
   plan_geo_carries();
   plan_geo_sums();
+  plan_fused_exponents();
   par_on_ = false;
   const int nin = t_.n_in;
   const int NCH = p_.n_channels;

@@ -459,3 +459,28 @@ def test_parameter_read_both_as_start_value_and_in_the_step(nt, rocm):
         ev, eg = oracle.path_errors(v, g, ov, og)
         assert ev.max() <= 1e-13 and eg.max() <= 1e-12, basis
     assert np.any(og[:, 0] != 0.0) and np.any(og[:, 2] != 0.0)
+
+
+def test_exponent_fused_only_for_a_carry_kept_as_g(nt, rocm, tapes):
+    """drift + vol z feeding the Asian spot's factor is one fma (the spot is
+    carried as G, its sum as the sum of G); a spot read every step as a value
+    (the product of steps, as the oracle rounds it) keeps the rounded sum, and
+    so does the device-libm kernel."""
+    fused = re.compile(r"const real r\d+_\d+ = fma\(v\d+, r\d+_\d+, v\d+\);")
+    assert len(fused.findall(rocm.lower(tapes["C2"], rocm.options("fp64", mode=2)))) > 0
+    assert not fused.search(rocm.lower(tapes["C2"], rocm.options("fp64", mode=2, libm=1)))
+
+    def body(rec):
+        s = rec.input("S0", 100.0)
+        mu = rec.input("mu", 0.001)
+        vol = rec.input("sigma", 0.02)
+        hi = s.mul(0.0)
+        for _ in range(16):
+            s = s.mul(mu.add(vol.mul(rec.randn())).exp())
+            hi = hi.max(s)  # reads the spot's value every step
+        rec.output(hi)
+    flat = nt.AadRecorder.record(body).flat()
+    src = rocm.lower(flat, rocm.options("fp64", mode=2))
+    assert not fused.search(src)
+    _, v, g = run_emulated(flat, rocm.options("fp64", mode=2), 256, seed=3, rocm=rocm)
+    check_per_path(v, g, flat, 256, OFFSET, 3)
