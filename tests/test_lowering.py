@@ -484,3 +484,35 @@ def test_exponent_fused_only_for_a_carry_kept_as_g(nt, rocm, tapes):
     assert not fused.search(src)
     _, v, g = run_emulated(flat, rocm.options("fp64", mode=2), 256, seed=3, rocm=rocm)
     check_per_path(v, g, flat, 256, OFFSET, 3)
+
+
+def test_parameter_basis_on_assorted_tapes(nt, rocm):
+    """The loop's tangents forced over parameters on tapes of other shapes
+    (lookback and digital payoffs, an up-and-out barrier, a named-stream
+    uniform beside the normal, two outputs, a carry read by a sum and by the
+    payoff): values as the oracle's, derivatives to the per-path bar, every
+    output's row."""
+    from conftest import jump_clock_tape, two_output_tape
+    m = nt.EquityMarket.atmOneYear()
+    flats = [equity_tape(nt, p, m, 24).flat() for p in (
+        nt.Products.lookbackCall(), nt.ExoticProducts.digitalCash(nt.OptionTypeEnum.CALL, 1.0, 0.5),
+        nt.ExoticProducts.barrier(nt.OptionTypeEnum.PUT, nt.ExoticProducts.BarrierEnum.UP_OUT, 120.0, 2.0))]
+    flats += [jump_clock_tape(nt, 64).flat(), _growth_tape(nt)]
+    for flat in flats:
+        opts = rocm.options("fp64", libm=1, mode=2, basis=2)
+        src = rocm.lower(flat, opts)
+        assert "rolled loop" in src and "basis=params" in src
+        ov, _ = oracle.replay_paths(flat, 128, OFFSET, 42, threads=1)
+        _, v, g = run_emulated(flat, opts, 128, rocm=rocm)
+        assert_values_match(v, ov, src)
+        check_per_path(v, g, flat, 128, OFFSET, 42, min_strict=0.5)
+    flat = two_output_tape(nt).flat()
+    src = rocm.lower(flat, rocm.options("fp64", libm=1, basis=2))
+    assert "basis=params" in src
+    k = emu.EmulatedKernel(src, 3, tape_slots(src))
+    _, v, g = k.run(flat["recorded_inputs"], 200, OFFSET, 42, grid=3, block=64, outputs=2)
+    ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, threads=1, output=None)
+    assert np.array_equal(v, ov)
+    for o in range(2):
+        _, eg = oracle.path_errors(v[:, o], g[:, o, :], ov[:, o], og[:, o, :])
+        assert eg.max() <= 1e-12, o
