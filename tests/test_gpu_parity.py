@@ -258,3 +258,38 @@ def test_sqrt_routine_and_fallback_on_device(rocm, nt, s_val, floor):
     ev, eg = oracle.path_errors(v, g, ov, og)
     assert ev.max() <= 1e-12 and eg.max() <= 1e-12, (ev.max(), eg.max())
     assert np.array_equal(np.isnan(v), np.isnan(ov))
+
+
+@pytest.mark.parametrize("basis", [1, 2])
+@pytest.mark.parametrize("name,paths", [("C2", 2048), ("C3", 1024), ("C4", 512), ("C5", 256)])
+def test_loop_tangents_over_inputs_and_parameters_on_device(rocm, tapes, name, paths, basis):
+    """The step loop's tangents forced over the inputs (basis 1) and over the
+    loop's parameters (basis 2): per path within the bar of the oracle."""
+    t = tapes[name]
+    print(f"case {name} basis={basis} paths={paths}", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=2, basis=basis)) as x:
+        v, g = x.replay_paths(paths, OFFSET, 42)
+        info = x.info()
+    assert info["scratch_bytes"] == 0
+    print(check_per_path(v, g, t, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99))
+
+
+def test_worst_of_fp32_over_parameters_reconciles(rocm, tapes):
+    """The fp32 worst-of kernel (tangents over the loop's parameters) against
+    the fp64 oracle over 20,000 paths: price within 1e-5 relative, the 33
+    Greeks within 1e-5 of the largest one (normwise: a worst-of's Greeks for
+    assets that are seldom the worst are near zero, where a componentwise
+    relative bar measures fp32 rounding of nothing)."""
+    t = tapes["C5"]
+    print("case C5 fp32 paths=20000", flush=True)
+    src = rocm.lower(t, rocm.options("fp32", mode=2))
+    assert "basis=params" in src
+    with rocm.Executable(t, rocm.options("fp32", mode=2)) as x:
+        sums, _ = x.replay(20_000, 0, 42)
+    got = oracle.to_result(sums, 20_000)
+    want = oracle.to_result(oracle.replay_sums(t, 20_000, 0, 42), 20_000)
+    ep = abs(got["price"] - want["price"]) / abs(want["price"])
+    gw = np.asarray(want["gradient"])
+    eg = np.max(np.abs(np.asarray(got["gradient"]) - gw)) / np.max(np.abs(gw))
+    print(f"price rel err {ep:.2e}, Greeks normwise {eg:.2e}")
+    assert ep <= 1e-5 and eg <= 1e-5
