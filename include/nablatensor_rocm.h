@@ -183,6 +183,26 @@ int nt_exec_replay_many(nt_exec *exec, const double *input_sets, int32_t markets
 int nt_exec_replay_paths(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed,
                          double *values, double *grads);
 
+/* Bytes of the static device array behind nt_exec_replay_noalloc (one copy per device). */
+#define NT_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* nt_exec_replay without allocation, copies or waiting. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP stream capture, tight serving loops, harnesses that forbid hipMalloc).
+ * d_inputs: n_inputs doubles in device memory (may be null when the tape has
+ * no inputs); d_sums: n_sums doubles of device (or pinned host) memory that
+ * receive the sums laid out as nt_exec_replay's; stream: a hipStream_t, null
+ * for the executable's own stream. The call enqueues the replay and finishing
+ * kernels and returns; the caller synchronizes before reading d_sums. Sums are
+ * bit-identical to nt_exec_replay's for the same inputs, paths, offset and
+ * seed. The per-block partials (grid x channels doubles) and a reverse
+ * sweep's per-lane tape, if the executable keeps one in device memory, live
+ * in a static array of NT_NOALLOC_SCRATCH_BYTES per device; a dispatch that
+ * needs more is refused with NT_E_INVALID before anything is launched. Calls
+ * that overlap in time on one device share that array and race. */
+int nt_exec_replay_noalloc(nt_exec *exec, const double *d_inputs, uint64_t paths, uint64_t offset, uint64_t seed,
+                           double *d_sums, int32_t n_sums, void *stream);
+
 int nt_exec_info_get(const nt_exec *exec, nt_exec_info *info);
 
 /* Copy of the generated source (same *len protocol as nt_lower). */

@@ -52,19 +52,27 @@ def embed_skeleton() -> Path:
 
 
 def build_engine(force: bool = True) -> Path:
+    """libnt_rocm.so: the host C++ (g++) plus nt_noalloc.hip, whose static
+    device array needs a hipcc object for gfx950 linked into the library."""
     inc = embed_skeleton()
     out = PKG / "libnt_rocm.so"
     srcs = [CSRC / "nt_rocm.cpp", CSRC / "lower.cpp"]
-    deps = srcs + [CSRC / "lower.hpp", CSRC / "nt_skeleton.h", CSRC / "nt_math_tables.h", inc,
-                   ROOT / "include" / "nablatensor_rocm.h"]
+    hip_src = CSRC / "nt_noalloc.hip"
+    deps = srcs + [hip_src, CSRC / "lower.hpp", CSRC / "nt_exec.hpp", CSRC / "nt_skeleton.h",
+                   CSRC / "nt_math_tables.h", inc, ROOT / "include" / "nablatensor_rocm.h"]
     if not force and _newer(out, deps):
         return out
+    incs = [f"-I{ROOT / 'include'}", f"-I{CSRC}"]
+    hip_obj = CSRC / "nt_noalloc.o"
+    _run([str(ROCM / "bin" / "hipcc"), "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", *PACKED_FP32_OFF,
+          *incs, "-c", str(hip_src), "-o", str(hip_obj)])
     cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
-           "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", f"-I{CSRC}", f"-I{ROCM / 'include'}",
-           *map(str, srcs), "-o", str(out) + ".tmp",
+           "-D__HIP_PLATFORM_AMD__", *incs, f"-I{ROCM / 'include'}",
+           *map(str, srcs), str(hip_obj), "-o", str(out) + ".tmp",
            f"-L{ROCM / 'lib'}", "-lamdhip64", "-lhiprtc", "-lamd_comgr", f"-Wl,-rpath,{ROCM / 'lib'}", "-ldl"]
     _run(cmd)
     os.replace(str(out) + ".tmp", out)
+    hip_obj.unlink()
     return out
 
 

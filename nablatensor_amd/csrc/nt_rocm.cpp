@@ -25,11 +25,14 @@
 #include <vector>
 
 #include "lower.hpp"
+#include "nt_exec.hpp"
 #include "skeleton_src.inc"
 
-namespace {
+namespace ntr {
 
+namespace {
 thread_local std::string g_err;
+}  // namespace
 
 int fail(int code, const std::string& msg) {
   g_err = msg;
@@ -42,11 +45,16 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(static_cast<int>(e), s.str());
 }
 
-#define NT_HIP(call, what)                       \
-  do {                                           \
-    hipError_t e_ = (call);                      \
-    if (e_ != hipSuccess) return hip_fail(e_, what); \
-  } while (0)
+const char* last_error() { return g_err.c_str(); }
+
+}  // namespace ntr
+
+using ntr::fail;
+using ntr::hip_fail;
+using ntr::Lowered;
+using ntr::MarketVariant;
+
+namespace {
 
 const char* kArch = "gfx950";
 
@@ -221,12 +229,6 @@ void kernel_resources(const std::vector<char>& code, const char* kernel, nt_exec
 
 // ---- lowering shared by nt_lower / nt_compile_check / nt_exec_create ------------
 
-struct Lowered {
-  ntl::TapeIR ir;
-  ntl::Plan plan;
-  std::string source;
-};
-
 int lower(const nt_tape* tape, const nt_options* opt, Lowered& out) {
   std::string err;
   int rc = ntl::build_ir(tape, out.ir, err);
@@ -277,68 +279,67 @@ int device_index(int& dev) {
 
 }  // namespace
 
-// A kernel that prices several input sets per path (nt_exec_replay_many).
-struct MarketVariant {
-  int vgprs = 0, scratch = 0;
-  hipModule_t mod = nullptr;
-  hipFunction_t fn = nullptr, fn_finish = nullptr;
-  double* d_inputs = nullptr;
-  double* d_partials = nullptr;
-};
-
-struct nt_exec {
-  nt_options opts{};
-  Lowered low;
-  nt_exec_info info{};
-  std::vector<char> code;
-  hipModule_t mod = nullptr, mod_dump = nullptr;
-  hipFunction_t fn = nullptr, fn_finish = nullptr, fn_dump = nullptr;
-  hipStream_t stream = nullptr;
-  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
-  double* d_inputs = nullptr;
-  double* d_partials = nullptr;
-  double* h_sums = nullptr;  // pinned host rows the finishing kernels write the sums to
-  size_t h_cap = 0;          // doubles in h_sums
-  void* d_scratch = nullptr;
-  int dev = 0;
-  int grid_cap = 1;
-  std::vector<double> inputs;
-  bool dirty = true;
-  std::map<int, MarketVariant> markets;  // by set count
-  int market_chunk = 0;                  // input sets per multi-market dispatch, 0 until chosen
-  double* d_set_inputs = nullptr;        // one input set at a time (reverse-sweep executables)
-
-  nt_exec() = default;
-  nt_exec(const nt_exec&) = delete;
-  nt_exec& operator=(const nt_exec&) = delete;
-  // Releases whatever was acquired, so a create that fails part way frees it too.
-  ~nt_exec() {
-    if (stream) (void)hipStreamSynchronize(stream);
-    for (auto& e : ev) {
-      if (e) (void)hipEventDestroy(e);
-    }
-    if (stream) (void)hipStreamDestroy(stream);
-    if (d_scratch) (void)hipFree(d_scratch);
-    if (h_sums) (void)hipHostFree(h_sums);
-    if (d_partials) (void)hipFree(d_partials);
-    if (d_inputs) (void)hipFree(d_inputs);
-    for (auto& kv : markets) {
-      MarketVariant& v = kv.second;
-      if (v.d_partials) (void)hipFree(v.d_partials);
-      if (v.d_inputs) (void)hipFree(v.d_inputs);
-      if (v.mod) (void)hipModuleUnload(v.mod);
-    }
-    if (d_set_inputs) (void)hipFree(d_set_inputs);
-    if (mod_dump) (void)hipModuleUnload(mod_dump);
-    if (mod) (void)hipModuleUnload(mod);
+nt_exec::~nt_exec() {
+  if (stream) (void)hipStreamSynchronize(stream);
+  for (auto& e : ev) {
+    if (e) (void)hipEventDestroy(e);
   }
-};
+  if (stream) (void)hipStreamDestroy(stream);
+  if (d_scratch) (void)hipFree(d_scratch);
+  if (h_sums) (void)hipHostFree(h_sums);
+  if (d_partials) (void)hipFree(d_partials);
+  if (d_inputs) (void)hipFree(d_inputs);
+  for (auto& kv : markets) {
+    MarketVariant& v = kv.second;
+    if (v.d_partials) (void)hipFree(v.d_partials);
+    if (v.d_inputs) (void)hipFree(v.d_inputs);
+    if (v.mod) (void)hipModuleUnload(v.mod);
+  }
+  if (d_set_inputs) (void)hipFree(d_set_inputs);
+  if (mod_dump) (void)hipModuleUnload(mod_dump);
+  if (mod) (void)hipModuleUnload(mod);
+}
+
+namespace ntr {
+
+int grid_for(const nt_exec* x, uint64_t paths) {
+  const int block = x->low.plan.block;
+  const uint64_t need = (paths + static_cast<uint64_t>(block) - 1) / static_cast<uint64_t>(block);
+  return std::max(1, static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap))));
+}
+
+size_t tape_bytes_per_lane(const nt_exec* x) {
+  const size_t elem = x->low.plan.precision == NT_FP32 ? sizeof(float) : sizeof(double);
+  return static_cast<size_t>(x->low.plan.tape_slots) * elem;
+}
+
+int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, const double* d_inputs, double* d_partials,
+                     void* d_tape, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v, double* out_g,
+                     int grid) {
+  const int block = x->low.plan.block;
+  void* args[] = {&d_inputs, &paths, &offset, &seed, &d_partials, &d_tape, &out_v, &out_g};
+  NT_HIP(hipModuleLaunchKernel(fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0, stream,
+                               args, nullptr),
+         "hipModuleLaunchKernel(nt_replay)");
+  return NT_OK;
+}
+
+int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int nch, double* out) {
+  unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
+  const unsigned threads = 64u * static_cast<unsigned>(std::min(std::max(nch, 1), 16));
+  void* args[] = {&d_partials, &blocks, &nchu, &out};
+  NT_HIP(hipModuleLaunchKernel(fn, 1, 1, 1, threads, 1, 1, 0, stream, args, nullptr),
+         "hipModuleLaunchKernel(nt_finish)");
+  return NT_OK;
+}
+
+}  // namespace ntr
 
 extern "C" {
 
 int nt_abi_version(void) { return NT_ABI_VERSION; }
 
-const char* nt_last_error(void) { return g_err.c_str(); }
+const char* nt_last_error(void) { return ntr::last_error(); }
 
 int nt_probe(int32_t* count) {
   if (!count) return fail(NT_E_INVALID, "count is null");
@@ -428,9 +429,9 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_sums), sizeof(double) * nch, hipHostMallocDefault),
          "hipHostMalloc(sums)");
   x->h_cap = static_cast<size_t>(nch);
-  const size_t elem = x->low.plan.precision == NT_FP32 ? sizeof(float) : sizeof(double);
-  const size_t scratch = static_cast<size_t>(x->low.plan.tape_slots) * x->grid_cap * x->low.plan.block * elem;
+  const size_t scratch = ntr::tape_bytes_per_lane(x.get()) * x->grid_cap * x->low.plan.block;
   if (scratch > 0) NT_HIP(hipMalloc(&x->d_scratch, scratch), "hipMalloc(scratch)");
+  x->scratch_bytes = scratch;
   // inputs default to zero until bound; the reference starts from the recorded values (Java side)
   x->inputs.assign(static_cast<size_t>(x->low.ir.n_in), 0.0);
   for (int j = 0; j < x->low.ir.n_in; ++j) x->inputs[j] = x->low.ir.c[x->low.ir.input_node[j]];
@@ -446,30 +447,17 @@ int nt_exec_set_inputs(nt_exec* x, const double* inputs, int32_t n) {
   return NT_OK;
 }
 
-// Grid of a dispatch over `paths`: one block per 256 paths up to the resident
-// cap. Every kernel of an executable (single- or multi-market) uses it, so a
-// path always lands on the same lane and block and the sums agree bit for bit.
-static int grid_for(const nt_exec* x, uint64_t paths) {
-  const int block = x->low.plan.block;
-  const uint64_t need = (paths + static_cast<uint64_t>(block) - 1) / static_cast<uint64_t>(block);
-  return std::max(1, static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap))));
-}
+using ntr::grid_for;
 
 static int launch_kernel(nt_exec* x, hipFunction_t fn, double* d_inputs, double* d_partials, uint64_t paths,
                          uint64_t offset, uint64_t seed, double* out_v, double* out_g, int& grid) {
-  const int block = x->low.plan.block;
   grid = grid_for(x, paths);
-  void* args[] = {&d_inputs, &paths, &offset, &seed, &d_partials, &x->d_scratch, &out_v, &out_g};
-  NT_HIP(hipModuleLaunchKernel(fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0, x->stream,
-                               args, nullptr),
-         "hipModuleLaunchKernel(nt_replay)");
-  return NT_OK;
+  return ntr::launch_kernel_on(x, x->stream, fn, d_inputs, d_partials, x->d_scratch, paths, offset, seed, out_v, out_g,
+                               grid);
 }
 
 static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v,
                          double* out_g, int& grid) {
-  const int block = x->low.plan.block;
-  grid = grid_for(x, paths);
   if (x->dirty) {
     if (!x->inputs.empty()) {
       NT_HIP(hipMemcpyAsync(x->d_inputs, x->inputs.data(), sizeof(double) * x->inputs.size(), hipMemcpyHostToDevice,
@@ -478,22 +466,13 @@ static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t 
     }
     x->dirty = false;
   }
-  void* args[] = {&x->d_inputs, &paths, &offset, &seed, &x->d_partials, &x->d_scratch, &out_v, &out_g};
-  NT_HIP(hipModuleLaunchKernel(fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0, x->stream,
-                               args, nullptr),
-         "hipModuleLaunchKernel(nt_replay)");
-  return NT_OK;
+  return launch_kernel(x, fn, x->d_inputs, x->d_partials, paths, offset, seed, out_v, out_g, grid);
 }
 
 // Finishing pass over the `grid` partial rows of one replay launch: `nch` sums
 // written to host memory `out` (pinned, read after the stream drains).
 static int launch_finish(nt_exec* x, hipFunction_t fn, double* d_partials, int grid, int nch, double* out) {
-  unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
-  const unsigned threads = 64u * static_cast<unsigned>(std::min(std::max(nch, 1), 16));
-  void* args[] = {&d_partials, &blocks, &nchu, &out};
-  NT_HIP(hipModuleLaunchKernel(fn, 1, 1, 1, threads, 1, 1, 0, x->stream, args, nullptr),
-         "hipModuleLaunchKernel(nt_finish)");
-  return NT_OK;
+  return ntr::launch_finish_on(x->stream, fn, d_partials, grid, nch, out);
 }
 
 int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, double* sums, int32_t n_sums,

@@ -22,7 +22,8 @@ NT_MODE_AUTO, NT_MODE_REVERSE, NT_MODE_TANGENT = 0, 1, 2
 ABI_VERSION = 2
 
 EXPORTS = ("nt_probe", "nt_device_name", "nt_lower", "nt_compile_check", "nt_exec_create", "nt_exec_set_inputs",
-           "nt_exec_replay", "nt_exec_replay_many", "nt_exec_replay_paths", "nt_exec_info_get", "nt_exec_source",
+           "nt_exec_replay", "nt_exec_replay_many", "nt_exec_replay_paths", "nt_exec_replay_noalloc",
+           "nt_exec_info_get", "nt_exec_source",
            "nt_exec_destroy", "nt_last_error", "nt_abi_version")
 
 
@@ -81,6 +82,8 @@ def lib() -> C.CDLL:
                                           C.c_uint64, C.POINTER(C.c_double), C.c_int32, C.POINTER(C.c_double)]
         L.nt_exec_replay_paths.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64,
                                            C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.nt_exec_replay_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64,
+                                             C.c_void_p, C.c_int32, C.c_void_p]
         L.nt_exec_info_get.argtypes = [C.c_void_p, C.POINTER(NtExecInfo)]
         L.nt_exec_source.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64)]
         L.nt_exec_destroy.argtypes = [C.c_void_p]

@@ -1,0 +1,134 @@
+"""The allocation-free entry point nt_exec_replay_noalloc against nt_exec_replay.
+
+nt_exec_replay_noalloc runs the same replay and finishing kernels with the
+per-block partials (and a reverse sweep's per-lane tape) in the library's
+static device array, reading inputs from and writing sums to device memory
+the caller passes. Its sums must be bit-identical to nt_exec_replay's for the
+same inputs, paths, offset and seed, on consecutive calls (the second smaller,
+so stale partials of the first would show), and a dispatch whose scratch
+would not fit must be refused before anything runs.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+OFFSET = 0x100000003
+
+
+class Hip:
+    """The few HIP runtime calls the test needs to own device buffers, from the
+    same libamdhip64 that libnt_rocm.so links."""
+
+    def __init__(self):
+        self.L = C.CDLL("/opt/rocm/lib/libamdhip64.so.7")
+        self.L.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        self.L.hipFree.argtypes = [C.c_void_p]
+        self.L.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        self.L.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.L.hipStreamSynchronize.argtypes = [C.c_void_p]
+        self.L.hipStreamDestroy.argtypes = [C.c_void_p]
+
+    def ok(self, rc):
+        assert rc == 0, f"HIP error {rc}"
+
+    def malloc(self, nbytes):
+        p = C.c_void_p()
+        self.ok(self.L.hipMalloc(C.byref(p), nbytes))
+        return p
+
+    def to_device(self, arr):
+        a = np.ascontiguousarray(arr, dtype=np.float64)
+        p = self.malloc(max(8, a.nbytes))
+        self.ok(self.L.hipMemcpy(p, a.ctypes.data, a.nbytes, 1))  # hipMemcpyHostToDevice
+        return p
+
+    def to_host(self, p, n):
+        out = np.zeros(n, dtype=np.float64)
+        self.ok(self.L.hipMemcpy(out.ctypes.data, p, out.nbytes, 2))  # hipMemcpyDeviceToHost
+        return out
+
+
+@pytest.fixture(scope="module")
+def rocm():
+    from nablatensor_amd import rocm as r
+    assert r.probe() > 0, "no gfx950 device visible to libnt_rocm.so"
+    return r
+
+
+@pytest.fixture(scope="module")
+def hip(rocm):
+    return Hip()
+
+
+def noalloc(rocm, hip, x, inputs, paths, offset, seed, stream=None):
+    L = rocm.lib()
+    n_sums = x.n_outputs * (2 + x.n_inputs)
+    d_in = hip.to_device(inputs)
+    d_sums = hip.malloc(8 * n_sums)
+    try:
+        rc = L.nt_exec_replay_noalloc(x._h, d_in, paths, offset & 0xFFFFFFFFFFFFFFFF, seed, d_sums, n_sums, stream)
+        if rc != 0:
+            raise rocm.NtError(rc, L.nt_last_error().decode())
+        if stream is None:
+            hip.ok(hip.L.hipDeviceSynchronize())
+        else:
+            hip.ok(hip.L.hipStreamSynchronize(stream))
+        return hip.to_host(d_sums, n_sums)
+    finally:
+        hip.L.hipFree(d_in)
+        hip.L.hipFree(d_sums)
+
+
+# (workload, precision, derivative mode, path counts of three consecutive calls). The
+# reverse sweep (mode 1) keeps 288 bytes of tape per lane in device memory, so its
+# dispatches stay within the lanes whose tape fits the static array.
+CASES = [("C2", "fp64", 0, (200_001, 4_097, 65_536)), ("C3", "fp32", 0, (200_001, 4_097, 65_536)),
+         ("C2", "fp64", 1, (20_001, 4_097, 16_384))]
+
+
+@pytest.mark.parametrize("name,prec,mode,counts", CASES)
+def test_noalloc_matches_replay(rocm, hip, tapes, name, prec, mode, counts):
+    t = tapes[name]
+    recorded = np.asarray(t["recorded_inputs"], dtype=np.float64)
+    moved = recorded.copy()
+    moved[0] *= 1.05
+    print(f"case noalloc {name} {prec} mode={mode}", flush=True)
+    with rocm.Executable(t, rocm.options(prec, mode=mode)) as x:
+        # two calls in a row, the second smaller; then other inputs on a caller stream
+        for paths, inputs, own_stream in zip(counts, (recorded, recorded, moved), (False, False, True)):
+            x.set_inputs(inputs)
+            want, _ = x.replay(paths, OFFSET, 42)
+            x.set_inputs(recorded)
+            stream = None
+            if own_stream:
+                s = C.c_void_p()
+                hip.ok(hip.L.hipStreamCreate(C.byref(s)))
+                stream = s
+            try:
+                got = noalloc(rocm, hip, x, inputs, paths, OFFSET, 42, stream)
+            finally:
+                if stream is not None:
+                    hip.L.hipStreamDestroy(stream)
+            print(f"  paths={paths} sum={got[0]!r}", flush=True)
+            assert np.array_equal(got, want), (paths, got - want)
+
+
+def test_noalloc_refuses_oversized_scratch(rocm, hip, tapes):
+    """A reverse-sweep executable that keeps its tape in device memory needs
+    tape_slots x lanes of scratch; at the full grid that exceeds the static
+    array, and the call is refused before anything is launched."""
+    t = tapes["C2"]
+    with rocm.Executable(t, rocm.options("fp64", mode=1, checkpoint=2)) as x:
+        info = x.info()
+        assert info["tape_slots"] > 0
+        lanes = info["grid_cap"] * info["block"]
+        assert info["tape_slots"] * 8 * lanes > (8 << 20)
+        with pytest.raises(rocm.NtError) as e:
+            noalloc(rocm, hip, x, t["recorded_inputs"], 2_000_000, 0, 42)
+        assert e.value.status == rocm.NT_E_INVALID
+        assert "scratch" in str(e.value)
