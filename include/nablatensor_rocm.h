@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define NT_ABI_VERSION 2
+#define NT_ABI_VERSION 3
 
 enum {
   NT_OK = 0,
@@ -88,7 +88,11 @@ typedef struct nt_options {
   int32_t checkpoint;       /* NT_CKPT_* */
   int32_t seg_len;          /* loop iterations per checkpoint segment; 0 = cost model */
   int32_t roll;             /* 1 (default): roll the step loop when one is found; -1: never */
-  int32_t contract;         /* FMA contraction: 0 default (off for fp64, on for fp32), 1 on, -1 off */
+  int32_t contract;         /* FMA contraction of the tape's own products and sums: 0 default (off for fp64, on for
+                               fp32, plus the fused exponent of a step's multiplicative carry, whose value is
+                               rebuilt from a product of factors anyway), 1 on, -1 off (every product and sum of a
+                               node rounded separately). The skeleton's math routines and the tangent rules use
+                               explicit fma either way */
   int32_t libm;             /* fp64 Box-Muller: 0 the skeleton's own log/sqrt/sincos, 1 device libm, 2 own log/sqrt + libm sincos */
   int32_t mode;             /* NT_MODE_* */
   int32_t markets;          /* nt_lower / nt_compile_check only: lower the kernel that prices this many input
@@ -99,7 +103,11 @@ typedef struct nt_options {
                                choice, 1 = the inputs, 2 = the loop's parameters (the loop-invariant values the
                                step reads and the carried values' start values), mapped back to the inputs
                                once per path after the loop */
-  int32_t reserved[3];
+  int32_t allow_spill;      /* 0 (default): a tape whose replay kernel would spill registers to scratch memory
+                               is declined with NT_E_UNSUPPORTED by nt_exec_create and nt_compile_check, as the
+                               reference's engines decline a tape in compile() so that engine selection falls back
+                               (AadEngine.java:50-59); 1: compile and run it anyway */
+  int32_t reserved[2];
 } nt_options;
 
 typedef struct nt_exec nt_exec;
@@ -138,14 +146,17 @@ int nt_lower(const nt_tape *tape, const nt_options *options, char *source, int64
 
 /* Lower and compile for gfx950 with hipRTC, without a device; fills *info with
  * the loop plan and the code object's register/scratch usage. Used by build
- * checks and to prefill the code-object cache. */
+ * checks and to prefill the code-object cache. Returns NT_E_UNSUPPORTED (with
+ * *info filled) when the kernel spills and options->allow_spill is 0. */
 int nt_compile_check(const nt_tape *tape, const nt_options *options, nt_exec_info *info);
 
 /* --- executables ---------------------------------------------------------- */
 
 /* Validate, lower, compile (hipRTC, gfx950) and load a tape. Replaces
  * RocmAadEngine.compile -> DeviceAadExecutable.compile
- * (RocmAadEngine.java:76-86, DeviceAadExecutable.java:107-119). */
+ * (RocmAadEngine.java:76-86, DeviceAadExecutable.java:107-119). A tape whose
+ * kernel would spill to scratch is declined with NT_E_UNSUPPORTED unless
+ * options->allow_spill is set (AadEngine.java:50-59). */
 int nt_exec_create(const nt_tape *tape, const nt_options *options, nt_exec **out);
 
 /* Bind input values (n == tape n_inputs, input order). Replaces setInput +

@@ -334,6 +334,7 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
   // separately, and over 500-step tapes fused rounding alone moves adjoints by
   // ~5e-12 relative. fp32 is compared at aggregate level and keeps FMAs.
   p.contract = o.contract > 0 || (o.contract == 0 && p.precision == NT_FP32);
+  p.fuse = o.contract >= 0;
   p.libm = (o.libm == 1 || o.libm == 2) ? o.libm : 0;
   p.block = o.block > 0 ? o.block : 256;
   if (p.block % 64 != 0 || p.block > 1024) { err = "block must be a multiple of 64, at most 1024"; return NT_E_INVALID; }
@@ -1497,8 +1498,9 @@ void Emitter::tsegment(int U, const std::string& sg) {
         if (op == NT_OP_EXP && fold_[j].on) {
           const Exp2Fold& f = fold_[j];
           const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
-          val = "nt_hw_exp2f(" + (f.p >= 0 ? "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")"
-                                           : l2e_name(f.r) + " * " + sv) + ")";
+          const std::string arg = !p_.fuse ? l2e_name(f.r) + " * " + sv + " + " + l2e_name(f.p)
+                                           : "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")";
+          val = "nt_hw_exp2f(" + (f.p >= 0 ? arg : l2e_name(f.r) + " * " + sv) + ")";
         }
         sqrt_q_.clear();
         if (op == NT_OP_SQRT && fast_sqrt() && !slow_) {
@@ -1812,7 +1814,7 @@ void Emitter::plan_exp_bounds() {
 
 void Emitter::plan_fused_exponents() {
   fused_exp_.assign(L_.found ? L_.period : 0, -1);
-  if (!L_.found) return;
+  if (!L_.found || !p_.fuse) return;
   for (int c = 0; c < L_.period; ++c) {
     if (!geo(c) || !(geo_free(c) || gsum_of_[c] >= 0)) continue;
     const bool a_self = L_.kind_a[c] == ARG_CARRY && L_.ref_a[c] == c;

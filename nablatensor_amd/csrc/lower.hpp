@@ -75,6 +75,8 @@ struct Plan {
   int adjoints = 1;
   int block = 256;
   bool contract = false;                  // FMA contraction allowed in the generated code
+  bool fuse = true;                       // explicit fma of a tape node's own product and sum allowed where the
+                                          // lowering knows it changes nothing the oracle resolves (off: contract -1)
   int libm = 0;                           // Box-Muller: 0 own fp64 math, 1 device libm, 2 own log/sqrt + libm sincos
   LoopPlan loop;
   int seg = 0, nseg_full = 0, tail = 0;   // iterations per segment, full segments, tail iterations

@@ -268,6 +268,23 @@ int copy_out(const std::string& s, char* buf, int64_t* len) {
   return (buf && !fits) ? fail(NT_E_INVALID, "buffer too small") : NT_OK;
 }
 
+// A kernel that spills keeps part of each lane's state in scratch memory
+// (HBM behind the caches), which the engine's design excludes: the tape is
+// declined, as the reference's engines decline in compile() so that engine
+// selection falls back to another engine (AadEngine.java:50-59), unless the
+// caller opted in with allow_spill.
+int decline_spill(const nt_exec_info& info, const nt_options* opt) {
+  if (info.scratch_bytes <= 0 || (opt && opt->allow_spill)) return NT_OK;
+  char buf[320];
+  std::snprintf(buf, sizeof buf,
+                "the rocm engine declines this tape: its %s replay kernel (%d nodes, %s) would spill %d bytes per "
+                "lane to scratch memory at %d VGPRs; set nt_options.allow_spill to run it anyway",
+                info.mode == NT_MODE_TANGENT ? "tangent-mode" : "reverse-sweep", info.n_nodes,
+                info.loop_period ? "step loop rolled" : "no step loop found, straight-line", info.scratch_bytes,
+                info.vgprs);
+  return fail(NT_E_UNSUPPORTED, buf);
+}
+
 int device_index(int& dev) {
   int count = 0;
   if (nt_probe(&count) != NT_OK || count == 0) {
@@ -385,13 +402,12 @@ int nt_compile_check(const nt_tape* tape, const nt_options* options, nt_exec_inf
   double secs = 0;
   rc = compile_hiprtc(l.source, false, code, secs);
   if (rc != NT_OK) return rc;
-  if (info) {
-    *info = nt_exec_info{};
-    fill_static_info(l, *info);
-    kernel_resources(code, "nt_replay", *info);
-    info->compile_seconds = secs;
-  }
-  return NT_OK;
+  nt_exec_info res{};
+  fill_static_info(l, res);
+  kernel_resources(code, "nt_replay", res);
+  res.compile_seconds = secs;
+  if (info) *info = res;
+  return decline_spill(res, options);
 }
 
 int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out) {
@@ -410,6 +426,8 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   fill_static_info(x->low, x->info);
   kernel_resources(x->code, "nt_replay", x->info);
   x->info.compile_seconds = secs;
+  rc = decline_spill(x->info, options);
+  if (rc != NT_OK) return rc;
   NT_HIP(hipModuleLoadData(&x->mod, x->code.data()), "hipModuleLoadData");
   NT_HIP(hipModuleGetFunction(&x->fn, x->mod, "nt_replay"), "hipModuleGetFunction(nt_replay)");
   NT_HIP(hipModuleGetFunction(&x->fn_finish, x->mod, "nt_finish"), "hipModuleGetFunction(nt_finish)");
@@ -556,7 +574,12 @@ static int choose_market_chunk(nt_exec* x, int& chunk) {
   MarketVariant* v1 = nullptr;
   MarketVariant* v2 = nullptr;
   int rc = market_variant(x, 1, v1);
-  if (rc == NT_OK) rc = market_variant(x, 2, v2);
+  if (rc != NT_OK) return rc;
+  if (v1->scratch > 0 && !x->opts.allow_spill) {
+    return fail(NT_E_UNSUPPORTED, "the tangent-mode kernel that prices input sets together would spill to scratch "
+                                  "memory; set nt_options.allow_spill to run it anyway");
+  }
+  rc = market_variant(x, 2, v2);
   if (rc != NT_OK) return rc;
   const int per = std::max(1, v2->vgprs - v1->vgprs);
   int c = std::max(1, std::min(8, 1 + (256 - v1->vgprs) / per));

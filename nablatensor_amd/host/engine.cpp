@@ -342,8 +342,11 @@ const RocmAbi& abi() {
     a.source = reinterpret_cast<decltype(a.source)>(sym("nt_exec_source"));
     a.destroy = reinterpret_cast<decltype(a.destroy)>(sym("nt_exec_destroy"));
     a.last_error = reinterpret_cast<decltype(a.last_error)>(sym("nt_last_error"));
-    a.loaded = ok;
+    auto version = reinterpret_cast<decltype(&nt_abi_version)>(sym("nt_abi_version"));
+    a.loaded = ok && version() == NT_ABI_VERSION;
     if (!ok) a.error = path + " lacks an nt_* entry point";
+    else if (!a.loaded) a.error = path + " has ABI version " + std::to_string(version()) + ", this host expects " +
+                                  std::to_string(NT_ABI_VERSION);
   });
   return a;
 }
@@ -501,6 +504,7 @@ std::unique_ptr<AadExecutable> RocmAadEngine::compile(TapePtr tape, const AadOpt
   o.mode = optionInt(options, "mode", 0);
   o.waves = optionInt(options, "waves", 0);
   o.basis = optionInt(options, "basis", 0);
+  o.allow_spill = optionInt(options, "allowSpill", 0);
   const auto t0 = std::chrono::steady_clock::now();
   nt_exec* exec = nullptr;
   int rc = a.create(&ct, &o, &exec);

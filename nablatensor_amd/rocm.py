@@ -19,7 +19,7 @@ NT_E_INVALID, NT_E_UNSUPPORTED, NT_E_NO_DEVICE, NT_E_COMPILE, NT_E_CLOSED, NT_E_
 NT_FP64, NT_FP32 = 0, 1
 NT_CKPT_AUTO, NT_CKPT_RECOMPUTE, NT_CKPT_STORE_DRAWS, NT_CKPT_STORE_ALL = 0, 1, 2, 3
 NT_MODE_AUTO, NT_MODE_REVERSE, NT_MODE_TANGENT = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EXPORTS = ("nt_probe", "nt_device_name", "nt_lower", "nt_compile_check", "nt_exec_create", "nt_exec_set_inputs",
            "nt_exec_replay", "nt_exec_replay_many", "nt_exec_replay_paths", "nt_exec_replay_noalloc",
@@ -39,7 +39,7 @@ class NtOptions(C.Structure):
                 ("max_blocks", C.c_int32), ("checkpoint", C.c_int32), ("seg_len", C.c_int32),
                 ("roll", C.c_int32), ("contract", C.c_int32), ("libm", C.c_int32), ("mode", C.c_int32),
                 ("markets", C.c_int32), ("waves", C.c_int32), ("basis", C.c_int32),
-                ("reserved", C.c_int32 * 3)]
+                ("allow_spill", C.c_int32), ("reserved", C.c_int32 * 2)]
 
 
 class NtExecInfo(C.Structure):
@@ -144,9 +144,10 @@ def wire_digest(flat: dict) -> str:
 
 def options(precision: str = "fp64", adjoints: bool = True, block: int = 0, max_blocks: int = 0,
             checkpoint: int = NT_CKPT_AUTO, seg_len: int = 0, roll: int = 1, contract: int = 0,
-            libm: int = 0, mode: int = 0, markets: int = 0, waves: int = 0, basis: int = 0) -> NtOptions:
+            libm: int = 0, mode: int = 0, markets: int = 0, waves: int = 0, basis: int = 0,
+            allow_spill: bool = False) -> NtOptions:
     return NtOptions(NT_FP32 if precision == "fp32" else NT_FP64, 1 if adjoints else 0, block, max_blocks,
-                     checkpoint, seg_len, roll, contract, libm, mode, markets, waves, basis)
+                     checkpoint, seg_len, roll, contract, libm, mode, markets, waves, basis, int(allow_spill))
 
 
 def probe() -> int:

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_function(rocm):
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(rocm.EXPORTS)
-    assert lib.nt_abi_version() == 2
+    assert lib.nt_abi_version() == 3
 
 
 @pytest.mark.skipif(gpu_available(), reason="checks the no-device path")
@@ -111,3 +111,21 @@ def test_offline_gfx950_compile_has_no_scratch(rocm, tapes, name, precision):
     info = rocm.compile_check(tapes[name], rocm.options(precision))
     assert info["scratch_bytes"] == 0
     assert 0 < info["vgprs"] <= 512
+
+
+def test_spilling_kernel_is_declined(rocm, nt):
+    """A kernel that would spill to scratch is declined with NT_E_UNSUPPORTED,
+    as the reference's engines decline a tape in compile() (AadEngine.java:50-59),
+    unless the caller opts in with allow_spill. The tape: a 96-fixing Asian call
+    lowered without its step loop and swept in reverse, so every forward value
+    stays live until the sweep (600 nodes, more than 512 VGPRs hold)."""
+    flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(96)).flat()
+    opts = dict(mode=rocm.NT_MODE_REVERSE, roll=-1)
+    with pytest.raises(rocm.NtError) as e:
+        rocm.compile_check(flat, rocm.options("fp64", **opts))
+    assert e.value.status == rocm.NT_E_UNSUPPORTED
+    assert "declines" in str(e.value) and "spill" in str(e.value) and "allow_spill" in str(e.value)
+    info = rocm.compile_check(flat, rocm.options("fp64", allow_spill=True, **opts))
+    assert info["scratch_bytes"] > 0 and info["loop_period"] == 0
+    # the same tape with its step loop rolled needs no scratch
+    assert rocm.compile_check(flat, rocm.options("fp64", mode=rocm.NT_MODE_REVERSE))["scratch_bytes"] == 0

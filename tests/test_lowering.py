@@ -516,3 +516,17 @@ def test_parameter_basis_on_assorted_tapes(nt, rocm):
     for o in range(2):
         _, eg = oracle.path_errors(v[:, o], g[:, o, :], ov[:, o], og[:, o, :])
         assert eg.max() <= 1e-12, o
+
+
+@pytest.mark.parametrize("precision", ["fp64", "fp32"])
+def test_contract_off_emits_no_fused_node_value(tapes, precision):
+    """contract=-1 keeps every product and sum of a tape node separately
+    rounded: the fused exponent of a G-carried step factor (an explicit fma in
+    the default kernel) becomes a rounded product and sum again."""
+    from nablatensor_amd import rocm
+    fused = re.compile(r"const real r\d+_\d+\w* = .*fmaf?\(")
+    default = rocm.lower(tapes["C2"], rocm.options(precision))
+    off = rocm.lower(tapes["C2"], rocm.options(precision, contract=-1))
+    assert any(fused.search(line) for line in default.splitlines())
+    assert not any(fused.search(line) for line in off.splitlines())
+    assert "#pragma clang fp contract(off)" in off
