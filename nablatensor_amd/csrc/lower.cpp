@@ -691,6 +691,11 @@ class Emitter {
     return std::string("(") + buf + ")";
   }
   std::string f(const char* name) const { return f32_ ? std::string(name) + "f" : std::string(name); }
+  // Type of tangents and of their scale factors: the re-evaluation pass uses
+  // strong-zero numbers (a product with an exact zero is zero, whatever the
+  // other factor), the tangent-mode image of the oracle skipping nodes whose
+  // adjoint is zero; the fast pass plain IEEE.
+  std::string treal() const { return slow_ ? (f32_ ? "nt_szf" : "nt_sz") : "real"; }
 
   // fp64 Box-Muller and exp read LDS tables that each block loads first.
   bool needs_tables() const {
@@ -725,8 +730,22 @@ class Emitter {
 
   // Reverse rule of one active node (CudaAadCodegen.java:386-448, ScalarReplay.java:129-166);
   // Aa / Ab are empty when that operand is inactive.
+  // In the re-evaluation pass a node's rules run only when its adjoint is
+  // nonzero, as the oracle skips it (ScalarReplay.java:134-136): an infinite
+  // or NaN local derivative under a zero adjoint then contributes nothing.
   void rev(const std::string& ind, int op, const std::string& Ai, const std::string& Vi, const std::string& Va,
            const std::string& Vb, const std::string& Aa, const std::string& Ab) {
+    const std::string zero = f32_ ? "0.0f" : "0.0";
+    if (!slow_ || (Aa.empty() && Ab.empty())) {
+      rev_rules(ind, op, Ai, Vi, Va, Vb, Aa, Ab);
+      return;
+    }
+    o_ << ind << "if (" << Ai << " != " << zero << ") {\n";
+    rev_rules(ind + "  ", op, Ai, Vi, Va, Vb, Aa, Ab);
+    o_ << ind << "}\n";
+  }
+  void rev_rules(const std::string& ind, int op, const std::string& Ai, const std::string& Vi, const std::string& Va,
+                 const std::string& Vb, const std::string& Aa, const std::string& Ab) {
     const std::string half = f32_ ? "0.5f" : "0.5";
     const std::string zero = f32_ ? "0.0f" : "0.0";
     switch (op) {
@@ -958,6 +977,7 @@ class Emitter {
                const std::function<std::string(int)>& ta, const std::function<std::string(int)>& tb);
   void tline(int lo, int hi);
   void tsegment(int U, const std::string& sg);
+  int trip_ = 1;  // loop steps per trip of the pass being emitted
   void body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const;
 
   // ---- markets (tangent mode): several input sets share each path's draws ----
@@ -974,6 +994,20 @@ class Emitter {
     if (f32_ || p_.libm == 1) return false;
     for (int i = 0; i < t_.n; ++i) {
       if (t_.op[i] == NT_OP_EXP || ((t_.op[i] == NT_OP_SQRT || t_.op[i] == NT_OP_DIV) && fast_sqrt())) return true;
+    }
+    return false;
+  }
+  // An active EXP, LOG, SQRT or DIV can leave a derivative infinite or NaN
+  // where the oracle's is finite: 0 times an infinite local derivative (1 /
+  // (1 + exp(x)) once exp(x) has overflowed) is NaN in IEEE arithmetic, while
+  // the oracle never multiplies by a zero adjoint. A path whose value or
+  // derivatives come out non-finite is evaluated again in the pass that
+  // follows the oracle's zero-adjoint rule.
+  bool nonfinite_fallback() const {
+    if (!p_.adjoints) return false;
+    for (int i = 0; i < t_.n; ++i) {
+      const int op = t_.op[i];
+      if (t_.active[i] && (op == NT_OP_EXP || op == NT_OP_LOG || op == NT_OP_SQRT || op == NT_OP_DIV)) return true;
     }
     return false;
   }
@@ -994,7 +1028,12 @@ class Emitter {
   // kernels; its value is then its own tangent factor 1/b.
   bool is_one(int node) const { return t_.op[node] == NT_OP_CONST && t_.c[node] == 1.0; }
   bool recip_ = false;  // the DIV just emitted is a nt_recip
-  void header();
+  void preamble();
+  void kernel_head(bool slow);
+  void kernel(bool slow);
+  void accumulate(int m, const std::string& skip);
+  void dump_rows(int m);
+  bool fallback() const { return exp_fallback() || nonfinite_fallback(); }
   void body_tangent();
   void body_reverse();
 };
@@ -1227,7 +1266,7 @@ std::string Emitter::scalar(const std::string& ind, const std::string& e) {
   auto it = scal_.find(e);
   if (it != scal_.end()) return it->second;
   const std::string name = "ls" + std::to_string(nscal_++);
-  o_ << ind << "const real " << name << " = " << e << ";\n";
+  o_ << ind << "const " << treal() << " " << name << " = " << e << ";\n";
   scal_[e] = name;
   return name;
 }
@@ -1236,6 +1275,7 @@ std::string Emitter::scalar(const std::string& ind, const std::string& e) {
 std::string Emitter::smul(const std::string& ind, const std::string& s1, const std::string& s2) {
   if (s1.empty()) return s2;
   if (s2.empty()) return s1;
+  if (slow_) return scalar(ind, "(" + treal() + "(" + s1 + ") * " + s2 + ")");
   return scalar(ind, "(" + s1 + " * " + s2 + ")");
 }
 
@@ -1397,7 +1437,7 @@ void Emitter::tangent(const std::string& ind, int op, const std::string& tn, con
     const std::string name = tn + std::to_string(D[i]) + sfx;
     if (!t[i].base.empty()) lazy_[name] = {t[i].base, t[i].scale};
     else lazy_.erase(name);
-    o_ << ind << "const real " << name << " = " << (t[i].empty() ? zero : t[i].expr) << ";\n";
+    o_ << ind << "const " << treal() << " " << name << " = " << (t[i].empty() ? zero : t[i].expr) << ";\n";
   }
 }
 
@@ -1474,7 +1514,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
   const std::string ind = "      ";
   const auto outer_scalars = scal_;  // scalars declared in this block end with it
   o_ << "    {\n";
-  o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << p_.seg << "u;\n";
+  o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << trip_ << "u;\n";
   trip_counters(ind);
   std::map<std::pair<int, int>, std::string> pairs;
   for (int u = 0; u < U; ++u) {
@@ -1559,7 +1599,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
             if (X.empty()) ex = sp;
             else if (!recip && !lazy_.count(X)) ex = f("fma") + "(" + cs + ", " + (X == "#1" ? (f32_ ? "1.0f" : "1.0") : X) + ", " + sp + ")";
             else ex = sum(Term{sp, "", ""}, scaled(ind, X, cs, shared)).expr;
-            o_ << ind << "const real " << name_k << " = " << ex << ";\n";
+            o_ << ind << "const " << treal() << " " << name_k << " = " << ex << ";\n";
           }
           continue;
         }
@@ -1578,7 +1618,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
         for (int k : self) {
           const std::string tk = "tr" + std::to_string(u) + "_" + std::to_string(j) + "_" + std::to_string(k) + ms(true);
           lazy_.erase(tk);
-          o_ << ind << "const real " << tk << " = " << name << ms(true) << ";\n";
+          o_ << ind << "const " << treal() << " " << tk << " = " << name << ms(true) << ";\n";
         }
         sqrt_q_.clear();
       }
@@ -1862,7 +1902,7 @@ void Emitter::count_uses() {
   }
 }
 
-void Emitter::header() {
+void Emitter::preamble() {
   const int n = t_.n;
   const int nin = t_.n_in;
   const bool loop = L_.found;
@@ -1893,25 +1933,62 @@ void Emitter::header() {
   if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";
   o_ << "#include \"nt_skeleton.h\"\n";
   o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
-  o_ << "extern \"C\" __global__ __launch_bounds__(" << p_.block;
-  if (p_.waves > 0) o_ << ", " << p_.waves;
-  o_ << ") void nt_replay(\n"
+  if (fallback()) o_ << "#define NT_HAS_SLOW 1\n";
+}
+
+// Signature and prologue of the replay kernel (nt_replay) or of the exception
+// kernel (nt_replay_slow), up to the path variables of the grid-stride loop.
+// Both take `flags`: word 0 counts the lanes that left paths to the exception
+// kernel, then one bitmap per market, bit p of word p / 64 for the dispatch's
+// path p. The exception kernel returns at once when the count is zero (the
+// finishing pass then skips its rows); otherwise it visits only the paths
+// whose bit is set, and a block with none loads no tables and writes a zero
+// row of partials.
+void Emitter::kernel_head(bool slow) {
+  const int nin = t_.n_in;
+  const int M = p_.markets;
+  o_ << "\nextern \"C\" __global__ __launch_bounds__(" << p_.block;
+  if (p_.waves > 0 && !slow) o_ << ", " << p_.waves;
+  o_ << ") void " << (slow ? "nt_replay_slow" : "nt_replay") << "(\n"
      << "    const double* __restrict__ inputs, nt_u64 n_paths, nt_u64 path_offset, nt_u64 seed,\n"
      << "    double* __restrict__ partials, real* __restrict__ scratch,\n"
-     << "    double* __restrict__ out_v, double* __restrict__ out_g) {\n";
+     << "    double* __restrict__ out_v, double* __restrict__ out_g, nt_u64* __restrict__ flags) {\n";
   o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
   o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
-  o_ << "  (void)scratch; (void)out_v; (void)out_g;\n";
+  if (slow) o_ << "  if (flags[0] == 0) return;  // no lane left a path to this kernel\n";
+  o_ << "  const nt_u64 nt_words = (n_paths + 63) >> 6;  // bitmap words per market\n";
+  o_ << "  nt_u64* __restrict__ nt_bits = flags + 1;\n";
+  o_ << "  (void)scratch; (void)out_v; (void)out_g; (void)nt_bits; (void)nt_words;\n";
+  const int nacc = p_.n_channels * M;
+  o_ << "  double acc[" << nacc << "];\n";
+  o_ << "  for (int c = 0; c < " << nacc << "; ++c) acc[c] = 0.0;\n";
+  if (slow) {
+    o_ << "  int nt_any = 0;\n";
+    o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
+    o_ << "    nt_u64 w = 0;\n";
+    for (int m = 0; m < M; ++m) o_ << "    w |= nt_bits[" << m << "u * nt_words + (p >> 6)];\n";
+    o_ << "    nt_any |= (int)((w >> (p & 63)) & 1);\n";
+    o_ << "  }\n";
+    o_ << "  if (__syncthreads_or(nt_any)) {\n";
+  }
   if (needs_tables()) o_ << "  nt_tables_load();\n";
-  for (int m = 0; m < p_.markets; ++m) {
+  for (int m = 0; m < M; ++m) {
     for (int j = 0; j < nin; ++j) {
       o_ << "  const real in" << j << msuf(m) << " = (real)inputs[" << m * nin + j << "];\n";
     }
   }
-  const int nacc = p_.n_channels * p_.markets;
-  o_ << "  double acc[" << nacc << "];\n";
-  o_ << "  for (int c = 0; c < " << nacc << "; ++c) acc[c] = 0.0;\n";
+  if (!slow && fallback()) {
+    for (int m = 0; m < M; ++m) o_ << "  bool nt_lane_bad" << m << " = false;\n";
+  }
   o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
+  if (slow) {
+    for (int m = 0; m < M; ++m) {
+      o_ << "    const bool nt_f" << m << " = (nt_bits[" << m << "u * nt_words + (p >> 6)] >> (p & 63)) & 1;\n";
+    }
+    o_ << "    if (!(nt_f0";
+    for (int m = 1; m < M; ++m) o_ << " || nt_f" << m;
+    o_ << ")) continue;\n";
+  }
   o_ << "    const nt_u64 path = p + path_offset;\n";
   o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
   o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
@@ -1959,8 +2036,8 @@ void Emitter::body_tangent() {
         if (!act || !p_.adjoints) continue;
         for (int k : posdeplist(j)) {
           const std::string tin = init >= 0 ? inv_tname(init, k) : "";
-          o_ << "    real ts" << j << "_" << k << ms(true) << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin)
-             << ";\n";
+          o_ << "    " << treal() << " ts" << j << "_" << k << ms(true) << " = "
+             << (tin.empty() ? zero : tin == "#1" ? one : tin) << ";\n";
         }
         if (geo(j)) {
           o_ << "    real gs" << j << ms(true) << " = " << one << ";\n";
@@ -1969,11 +2046,17 @@ void Emitter::body_tangent() {
       }
     }
     exp_bound_checks();
-    if (p_.nseg_full > 0) {
-      o_ << "    for (nt_u32 sg = 0; sg < " << p_.nseg_full << "u; ++sg)\n";
-      tsegment(p_.seg, "sg");
+    // The re-evaluation pass, which runs for a rare path, takes the shortest
+    // trip (one step, two when a step draws an odd number of normals) so its
+    // register needs stay below the fast pass's: the kernel's register budget
+    // is the larger of the two.
+    trip_ = slow_ ? (L_.need_even ? 2 : 1) : p_.seg;
+    const int nfull = L_.iters / trip_, tail = L_.iters % trip_;
+    if (nfull > 0) {
+      o_ << "    for (nt_u32 sg = 0; sg < " << nfull << "u; ++sg)\n";
+      tsegment(trip_, "sg");
     }
-    if (p_.tail) tsegment(p_.tail, std::to_string(p_.nseg_full) + "u");
+    if (tail) tsegment(tail, std::to_string(nfull) + "u");
     for (int j = 0; j < L_.period; ++j) {
       if (!geo(j)) continue;
       for (int m = mlo_; m < mhi_; ++m) {
@@ -2009,7 +2092,7 @@ void Emitter::body_tangent() {
               if (T == "#1") e = e.empty() ? td : "(" + e + " + " + td + ")";
               else e = e.empty() ? "(" + td + " * " + T + ")" : f("fma") + "(" + td + ", " + T + ", " + e + ")";
             }
-            o_ << "    const real ts" << j << "_" << k << ms(true) << " = " << (e.empty() ? zero : e) << ";\n";
+            o_ << "    const " << treal() << " ts" << j << "_" << k << ms(true) << " = " << (e.empty() ? zero : e) << ";\n";
           }
         }
       }
@@ -2090,6 +2173,126 @@ void Emitter::body_reverse() {
   }
 }
 
+// channels: [market][output][value, value^2, derivative per input]
+// `skip` names a flag under which the path adds nothing (its value and
+// derivatives are replaced by zeros with a select, no branch).
+void Emitter::accumulate(int m, const std::string& skip) {
+  const int nin = t_.n_in;
+  const int O = static_cast<int>(t_.outputs.size());
+  auto keep = [&](const std::string& v) { return skip.empty() ? v : "(" + skip + " ? 0.0 : " + v + ")"; };
+  for (int o = 0; o < O; ++o) {
+    const int base = m * p_.n_channels + o * (2 + nin);
+    const std::string y = keep("nt_y" + msuf(m) + "[" + std::to_string(o) + "]");
+    o_ << "    {\n      const double y = " << y << ";\n";
+    o_ << "      acc[" << base << "] += y;\n      acc[" << base + 1 << "] += y * y;\n    }\n";
+    if (!p_.adjoints) continue;
+    for (int j = 0; j < nin; ++j) {
+      o_ << "    acc[" << base + 2 + j << "] += " << keep("nt_g" + msuf(m) + "[" + std::to_string(o * nin + j) + "]")
+         << ";\n";
+    }
+  }
+}
+
+// Per-path rows [market][path][output], as the oracle's per-path rows.
+void Emitter::dump_rows(int m) {
+  const int nin = t_.n_in;
+  const int M = p_.markets;
+  const int O = static_cast<int>(t_.outputs.size());
+  const std::string path_row = M > 1 ? "(" + std::to_string(m) + "u * n_paths + p)" : std::string("p");
+  for (int o = 0; o < O; ++o) {
+    const std::string row = O > 1 ? "(" + path_row + " * " + std::to_string(O) + "u + " + std::to_string(o) + "u)" : path_row;
+    o_ << "      out_v[" << row << "] = nt_y" << msuf(m) << "[" << o << "];\n";
+    for (int j = 0; j < nin; ++j) {
+      o_ << "      out_g[" << row << " * " << nin << "u + " << j << "u] = "
+         << (p_.adjoints ? "nt_g" + msuf(m) + "[" + std::to_string(o * nin + j) + "]" : std::string("0.0")) << ";\n";
+    }
+  }
+}
+
+// One kernel. The replay kernel evaluates every path on the fast pass; a path
+// whose fast pass is not valid (an own-math routine met an argument outside
+// its range, or the value or a derivative came out non-finite) is left out of
+// its sums and flagged in the bitmap. The exception kernel evaluates the
+// flagged paths again, one market at a time, with device libm and the
+// oracle's zero-adjoint rule, into a second set of partial rows. Kept apart,
+// the rare pass costs the replay kernel no registers.
+void Emitter::kernel(bool slow) {
+  const int nin = t_.n_in;
+  const int M = p_.markets;
+  const int O = static_cast<int>(t_.outputs.size());
+  const bool tangent = p_.mode == NT_MODE_TANGENT;
+  const bool fb = fallback();
+  slow_ = slow;
+  kernel_head(slow);
+  for (int m = 0; m < M; ++m) {
+    o_ << "    double nt_y" << msuf(m) << "[" << O << "];\n";
+    if (p_.adjoints && nin > 0) o_ << "    double nt_g" << msuf(m) << "[" << O * nin << "];\n";
+  }
+  if (!slow) {
+    if (fb) {
+      o_ << "    bool nt_slow = false;\n";  // a flag shared by every market (a draw-only exponent)
+      for (int m = 0; m < M && M > 1; ++m) o_ << "    bool nt_slow" << msuf(m) << " = false;\n";
+    }
+    mlo_ = 0;
+    mhi_ = M;
+    o_ << "    {\n";
+    scal_.clear();
+    if (tangent) body_tangent(); else body_reverse();
+    o_ << "    }\n";
+    for (int m = 0; m < M; ++m) {
+      if (fb) o_ << "    nt_lane_bad" << m << " |= nt_slow" << (M > 1 ? " || nt_slow" + msuf(m) : std::string()) << ";\n";
+      accumulate(m, "");
+      o_ << "#ifdef NT_DUMP_PATHS\n    {\n";
+      dump_rows(m);
+      o_ << "    }\n#endif\n";
+    }
+  } else {
+    // Each market is evaluated again alone, so its result is the one a
+    // single-market kernel gives it.
+    for (int m = 0; m < M; ++m) {
+      o_ << "    if (nt_f" << m << ") {\n";
+      mlo_ = m;
+      mhi_ = m + 1;
+      scal_.clear();
+      if (tangent) body_tangent(); else body_reverse();
+      accumulate(m, "");
+      o_ << "#ifdef NT_DUMP_PATHS\n";
+      dump_rows(m);
+      o_ << "#endif\n";
+      o_ << "    }\n";
+    }
+  }
+  o_ << "  }\n";
+  if (slow) o_ << "  }\n";  // the block had a flagged path
+  if (!slow && fb) {
+    // A lane that flagged a path, or whose sums are not finite (a value or a
+    // derivative of one of its paths was not: the oracle's may still be, where
+    // it skips a zero adjoint), adds nothing and leaves every one of its paths
+    // to the exception kernel: a rare event, and its paths' contributions need
+    // not stay live to the end of each path.
+    for (int m = 0; m < M; ++m) {
+      const std::string bad = "nt_lane_bad" + std::to_string(m);
+      const int c0 = m * p_.n_channels, c1 = c0 + p_.n_channels;
+      if (nonfinite_fallback()) {
+        o_ << "  for (int c = " << c0 << "; c < " << c1 << "; ++c) " << bad << " |= !__builtin_isfinite(acc[c]);\n";
+      }
+      o_ << "  if (" << bad << ") {\n    for (int c = " << c0 << "; c < " << c1 << "; ++c) acc[c] = 0.0;\n  }\n";
+      o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) nt_flag_paths(nt_bits + " << m << "u * nt_words, p, " << bad
+         << ");\n";
+    }
+    o_ << "  if (nt_lane_bad0";
+    for (int m = 1; m < M; ++m) o_ << " || nt_lane_bad" << m;
+    o_ << ") atomicAdd(flags, 1ull);\n";
+  }
+  const int nacc = p_.n_channels * M;
+  o_ << "  __shared__ double nt_lds[" << nacc << " * (" << p_.block << " / 64)];\n";
+  o_ << "  nt_block_store<" << nacc << ">(acc, partials, nt_lds);\n";
+  o_ << "}\n";
+  slow_ = false;
+  mlo_ = 0;
+  mhi_ = M;
+}
+
 std::string Emitter::run() {
   count_uses();
   plan_exp2_folds();
@@ -2100,77 +2303,9 @@ std::string Emitter::run() {
   plan_geo_sums();
   plan_fused_exponents();
   par_on_ = false;
-  const int nin = t_.n_in;
-  const int NCH = p_.n_channels;
-  const bool tangent = p_.mode == NT_MODE_TANGENT;
-  header();
-  // fp64 exp's fast path covers |x| <= 708; a path with an exponent outside
-  // flags itself and is evaluated again with device libm exp. The fast pass
-  // is the only one a Monte-Carlo path normally takes, and it stays one
-  // basic block per loop trip.
-  const bool fallback = exp_fallback();
-  const int M = p_.markets;
-  const int O = static_cast<int>(t_.outputs.size());
-  for (int m = 0; m < M; ++m) {
-    o_ << "    double nt_y" << msuf(m) << "[" << O << "];\n";
-    if (p_.adjoints && nin > 0) o_ << "    double nt_g" << msuf(m) << "[" << O * nin << "];\n";
-  }
-  if (fallback) {
-    o_ << "    bool nt_slow = false;\n";  // an exponent shared by every market
-    for (int m = 0; m < M && M > 1; ++m) o_ << "    bool nt_slow" << msuf(m) << " = false;\n";
-  }
-  slow_ = false;
-  mlo_ = 0;
-  mhi_ = M;
-  o_ << "    {\n";
-  scal_.clear();
-  if (tangent) body_tangent(); else body_reverse();
-  o_ << "    }\n";
-  if (fallback) {
-    // Each market is evaluated again alone, so its result is the one a
-    // single-market kernel gives it.
-    slow_ = true;
-    for (int m = 0; m < M; ++m) {
-      o_ << "    if (nt_slow" << (M > 1 ? " || nt_slow" + msuf(m) : std::string()) << ") {\n";
-      mlo_ = m;
-      mhi_ = m + 1;
-      scal_.clear();
-      if (tangent) body_tangent(); else body_reverse();
-      o_ << "    }\n";
-    }
-    slow_ = false;
-    mlo_ = 0;
-    mhi_ = M;
-  }
-  // channels: [market][output][value, value^2, derivative per input]
-  for (int m = 0; m < M; ++m) {
-    for (int o = 0; o < O; ++o) {
-      const int base = m * NCH + o * (2 + nin);
-      const std::string y = "nt_y" + msuf(m) + "[" + std::to_string(o) + "]";
-      o_ << "    acc[" << base << "] += " << y << ";\n    acc[" << base + 1 << "] += " << y << " * " << y << ";\n";
-      if (!p_.adjoints) continue;
-      for (int j = 0; j < nin; ++j) {
-        o_ << "    acc[" << base + 2 + j << "] += nt_g" << msuf(m) << "[" << o * nin + j << "];\n";
-      }
-    }
-  }
-  o_ << "#ifdef NT_DUMP_PATHS\n";  // rows [market][path][output], as the oracle's per-path rows
-  for (int m = 0; m < M; ++m) {
-    const std::string path_row = M > 1 ? "(" + std::to_string(m) + "u * n_paths + p)" : std::string("p");
-    for (int o = 0; o < O; ++o) {
-      const std::string row = O > 1 ? "(" + path_row + " * " + std::to_string(O) + "u + " + std::to_string(o) + "u)" : path_row;
-      o_ << "    out_v[" << row << "] = nt_y" << msuf(m) << "[" << o << "];\n";
-      for (int j = 0; j < nin; ++j) {
-        o_ << "    out_g[" << row << " * " << nin << "u + " << j << "u] = "
-           << (p_.adjoints ? "nt_g" + msuf(m) + "[" + std::to_string(o * nin + j) + "]" : std::string("0.0")) << ";\n";
-      }
-    }
-  }
-  o_ << "#endif\n";
-  o_ << "  }\n";
-  o_ << "  __shared__ double nt_lds[" << NCH * M << " * (" << p_.block << " / 64)];\n";
-  o_ << "  nt_block_store<" << NCH * M << ">(acc, partials, nt_lds);\n";
-  o_ << "}\n";
+  preamble();
+  kernel(false);
+  if (fallback()) kernel(true);
   return o_.str();
 }
 

@@ -40,7 +40,7 @@ struct Lowered {
 struct MarketVariant {
   int vgprs = 0, scratch = 0;
   hipModule_t mod = nullptr;
-  hipFunction_t fn = nullptr, fn_finish = nullptr;
+  hipFunction_t fn = nullptr, fn_slow = nullptr, fn_finish = nullptr;  // fn_slow: null when the kernel has none
   double* d_inputs = nullptr;
   double* d_partials = nullptr;
 };
@@ -54,6 +54,7 @@ struct nt_exec {
   std::vector<char> code;
   hipModule_t mod = nullptr, mod_dump = nullptr;
   hipFunction_t fn = nullptr, fn_finish = nullptr, fn_dump = nullptr;
+  hipFunction_t fn_slow = nullptr, fn_dump_slow = nullptr;  // exception kernels, null when the tape needs none
   hipStream_t stream = nullptr;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   double* d_inputs = nullptr;
@@ -62,6 +63,9 @@ struct nt_exec {
   size_t h_cap = 0;          // doubles in h_sums
   void* d_scratch = nullptr;
   size_t scratch_bytes = 0;  // bytes of d_scratch: the reverse sweep's per-lane tape at the resident grid
+  uint64_t* d_flags = nullptr;  // count of lanes that left paths to the exception kernel, then their bitmap
+                                //   (grown with the dispatch; the count is zero between dispatches)
+  size_t flags_bytes = 0;
   int dev = 0;
   int grid_cap = 1;
   std::vector<double> inputs;
@@ -87,13 +91,27 @@ int grid_for(const nt_exec* x, uint64_t paths);
 // Bytes per lane of the reverse sweep's tape (checkpoints and stored values).
 size_t tape_bytes_per_lane(const nt_exec* x);
 
-// Launches the replay kernel `fn` over `grid` blocks on `stream`.
-int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, const double* d_inputs, double* d_partials,
-                     void* d_tape, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v, double* out_g,
-                     int grid);
+// Bytes of the flags of a dispatch over `paths` pricing `markets` input sets:
+// a 64-bit count, then one bit per path and set in 64-bit words.
+size_t flags_bytes_for(uint64_t paths, int markets);
 
-// Finishing pass over the `grid` partial rows of one replay launch on
-// `stream`: `nch` sums written to `out` (device or pinned host memory).
-int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int nch, double* out);
+// Partial rows a dispatch over `grid` blocks may write: the replay kernel's
+// and, when there is an exception kernel, as many again.
+int partial_rows(int grid, bool has_slow);
+
+// Launches the replay kernel `fn` over `grid` blocks on `stream` and, when
+// `fn_slow` is set, the exception kernel after it, whose partial rows follow
+// the replay kernel's (rows grid .. 2 grid - 1 of `nch` doubles each).
+// `between`, when set, is recorded after the replay kernel (it times that kernel alone).
+int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFunction_t fn_slow, const double* d_inputs,
+                     double* d_partials, int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset,
+                     uint64_t seed, double* out_v, double* out_g, int grid, hipEvent_t between = nullptr);
+
+// Finishing pass on `stream` over the `grid` rows of the replay kernel and,
+// when the count at `d_flags` (null: none) is nonzero, the `slow_grid` rows of
+// the exception kernel after them: `nch` sums written to `out` (device or
+// pinned host memory); the count is reset to zero.
+int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int slow_grid, int nch,
+                     double* out, uint64_t* d_flags);
 
 }  // namespace ntr

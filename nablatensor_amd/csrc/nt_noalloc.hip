@@ -1,12 +1,13 @@
 // Allocation-free replay: nt_exec_replay_noalloc (include/nablatensor_rocm.h).
 //
-// nt_exec_replay keeps the replay kernel's per-block partial sums (and, for a
-// reverse-sweep executable that stores its tape in device memory, that
-// per-lane tape) in buffers the executable allocated with hipMalloc, and
-// copies inputs from, and sums to, host memory. This entry point runs the
-// same two kernels (replay, then the finishing pass) with those buffers carved
-// out of `scratch`, a static device array of NT_NOALLOC_SCRATCH_BYTES that
-// each device holds from the first call until the process ends. The caller
+// nt_exec_replay keeps the replay kernels' per-block partial sums, the bitmap
+// of paths left to the exception kernel and, for a reverse-sweep executable
+// that stores its tape in device memory, that per-lane tape in buffers the
+// executable allocated with hipMalloc, and copies inputs from, and sums to,
+// host memory. This entry point runs the same kernels (replay, exception,
+// finishing pass) with those buffers carved out of `scratch`, a static device
+// array of NT_NOALLOC_SCRATCH_BYTES that each device holds from the first
+// call until the process ends. The caller
 // passes device pointers for the inputs and the sums and a stream; nothing is
 // allocated, copied or waited for, so the call can sit in a tight loop or
 // under stream capture.
@@ -15,8 +16,14 @@
 // to that entry point's for the same paths, offset, seed and inputs. Every
 // call on a device shares that device's array: calls that overlap in time on
 // one device (on different streams, or from different threads) race on it.
-// Nothing in the array has to start at zero: every block writes its own row
-// of partials and the finishing pass reads only those rows.
+// The array is laid out as the flags (a count of the lanes that left paths to
+// the exception kernel, then its bitmap), the partial rows, and a reverse
+// sweep's tape. Only the count has to start at zero: the array is zero when
+// the device loads it and every finishing pass sets the count back to zero;
+// it sits at the start of the array whatever the dispatch's sizes, so a
+// dispatch never reads another's rows as its count. Every block writes its
+// own rows of partials, the replay kernel writes every word of the bitmap the
+// exception kernel reads, and the finishing pass reads only the rows written.
 //
 // Compiled by hipcc (the array is device code); the rest of libnt_rocm.so is
 // host C++ built with g++.
@@ -64,15 +71,17 @@ extern "C" int nt_exec_replay_noalloc(nt_exec* x, const double* d_inputs, uint64
   if (!d_sums || n_sums != nch) return ntr::fail(NT_E_INVALID, "d_sums must hold n_outputs * (2 + n_inputs) doubles");
   if (x->low.ir.n_in > 0 && !d_inputs) return ntr::fail(NT_E_INVALID, "d_inputs is null");
   const int grid = ntr::grid_for(x, paths);
-  const size_t partial_bytes = round_up_256(sizeof(double) * static_cast<size_t>(grid) * static_cast<size_t>(nch));
+  const int rows = ntr::partial_rows(grid, x->fn_slow != nullptr);
+  const size_t partial_bytes = round_up_256(sizeof(double) * static_cast<size_t>(rows) * static_cast<size_t>(nch));
+  const size_t flag_bytes = round_up_256(ntr::flags_bytes_for(paths, 1));
   const size_t tape_bytes =
       ntr::tape_bytes_per_lane(x) * static_cast<size_t>(grid) * static_cast<size_t>(x->low.plan.block);
-  if (partial_bytes + tape_bytes > static_cast<size_t>(NT_NOALLOC_SCRATCH_BYTES)) {
-    char buf[256];
+  if (partial_bytes + flag_bytes + tape_bytes > static_cast<size_t>(NT_NOALLOC_SCRATCH_BYTES)) {
+    char buf[320];
     std::snprintf(buf, sizeof buf,
-                  "this dispatch needs %zu bytes of scratch (%zu of partials, %zu of per-lane tape at %d blocks); "
-                  "the allocation-free entry point has %zu",
-                  partial_bytes + tape_bytes, partial_bytes, tape_bytes, grid,
+                  "this dispatch needs %zu bytes of scratch (%zu of partials, %zu of path flags, %zu of per-lane "
+                  "tape at %d blocks); the allocation-free entry point has %zu",
+                  partial_bytes + flag_bytes + tape_bytes, partial_bytes, flag_bytes, tape_bytes, grid,
                   static_cast<size_t>(NT_NOALLOC_SCRATCH_BYTES));
     return ntr::fail(NT_E_INVALID, buf);
   }
@@ -81,9 +90,13 @@ extern "C" int nt_exec_replay_noalloc(nt_exec* x, const double* d_inputs, uint64
   if (rc != NT_OK) return rc;
   NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : x->stream;
-  double* partials = static_cast<double*>(base);
-  void* tape = tape_bytes ? static_cast<void*>(static_cast<char*>(base) + partial_bytes) : nullptr;
-  rc = ntr::launch_kernel_on(x, s, x->fn, d_inputs, partials, tape, paths, offset, seed, nullptr, nullptr, grid);
+  char* at = static_cast<char*>(base);
+  uint64_t* flags = reinterpret_cast<uint64_t*>(at);
+  double* partials = reinterpret_cast<double*>(at + flag_bytes);
+  void* tape = tape_bytes ? static_cast<void*>(at + flag_bytes + partial_bytes) : nullptr;
+  rc = ntr::launch_kernel_on(x, s, x->fn, x->fn_slow, d_inputs, partials, nch, tape, flags, paths, offset, seed, nullptr,
+                             nullptr, grid);
   if (rc != NT_OK) return rc;
-  return ntr::launch_finish_on(s, x->fn_finish, partials, grid, nch, d_sums);
+  return ntr::launch_finish_on(s, x->fn_finish, partials, grid, x->fn_slow ? grid : 0, nch, d_sums,
+                               x->fn_slow ? flags : nullptr);
 }

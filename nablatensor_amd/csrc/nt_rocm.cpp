@@ -285,6 +285,16 @@ int decline_spill(const nt_exec_info& info, const nt_options* opt) {
   return fail(NT_E_UNSUPPORTED, buf);
 }
 
+// A kernel the module may or may not hold (the exception kernel): null when absent.
+hipFunction_t optional_function(hipModule_t mod, const char* name) {
+  hipFunction_t fn = nullptr;
+  if (hipModuleGetFunction(&fn, mod, name) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return fn;
+}
+
 int device_index(int& dev) {
   int count = 0;
   if (nt_probe(&count) != NT_OK || count == 0) {
@@ -303,6 +313,7 @@ nt_exec::~nt_exec() {
   }
   if (stream) (void)hipStreamDestroy(stream);
   if (d_scratch) (void)hipFree(d_scratch);
+  if (d_flags) (void)hipFree(d_flags);
   if (h_sums) (void)hipHostFree(h_sums);
   if (d_partials) (void)hipFree(d_partials);
   if (d_inputs) (void)hipFree(d_inputs);
@@ -330,21 +341,36 @@ size_t tape_bytes_per_lane(const nt_exec* x) {
   return static_cast<size_t>(x->low.plan.tape_slots) * elem;
 }
 
-int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, const double* d_inputs, double* d_partials,
-                     void* d_tape, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v, double* out_g,
-                     int grid) {
+size_t flags_bytes_for(uint64_t paths, int markets) {
+  return (1 + static_cast<size_t>((paths + 63) / 64) * static_cast<size_t>(std::max(1, markets))) * sizeof(uint64_t);
+}
+
+int partial_rows(int grid, bool has_slow) { return has_slow ? 2 * grid : grid; }
+
+int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFunction_t fn_slow, const double* d_inputs,
+                     double* d_partials, int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset,
+                     uint64_t seed, double* out_v, double* out_g, int grid, hipEvent_t between) {
   const int block = x->low.plan.block;
-  void* args[] = {&d_inputs, &paths, &offset, &seed, &d_partials, &d_tape, &out_v, &out_g};
+  void* args[] = {&d_inputs, &paths, &offset, &seed, &d_partials, &d_tape, &out_v, &out_g, &d_flags};
   NT_HIP(hipModuleLaunchKernel(fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0, stream,
                                args, nullptr),
          "hipModuleLaunchKernel(nt_replay)");
+  if (between) NT_HIP(hipEventRecord(between, stream), "hipEventRecord");
+  if (!fn_slow) return NT_OK;
+  double* slow_rows = d_partials + static_cast<size_t>(grid) * static_cast<size_t>(nch);
+  void* sargs[] = {&d_inputs, &paths, &offset, &seed, &slow_rows, &d_tape, &out_v, &out_g, &d_flags};
+  NT_HIP(hipModuleLaunchKernel(fn_slow, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0,
+                               stream, sargs, nullptr),
+         "hipModuleLaunchKernel(nt_replay_slow)");
   return NT_OK;
 }
 
-int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int nch, double* out) {
-  unsigned blocks = static_cast<unsigned>(grid), nchu = static_cast<unsigned>(nch);
+int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int slow_grid, int nch,
+                     double* out, uint64_t* d_flags) {
+  unsigned blocks = static_cast<unsigned>(grid), slow_blocks = static_cast<unsigned>(slow_grid);
+  unsigned nchu = static_cast<unsigned>(nch);
   const unsigned threads = 64u * static_cast<unsigned>(std::min(std::max(nch, 1), 16));
-  void* args[] = {&d_partials, &blocks, &nchu, &out};
+  void* args[] = {&d_partials, &blocks, &slow_blocks, &nchu, &out, &d_flags};
   NT_HIP(hipModuleLaunchKernel(fn, 1, 1, 1, threads, 1, 1, 0, stream, args, nullptr),
          "hipModuleLaunchKernel(nt_finish)");
   return NT_OK;
@@ -431,6 +457,7 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   NT_HIP(hipModuleLoadData(&x->mod, x->code.data()), "hipModuleLoadData");
   NT_HIP(hipModuleGetFunction(&x->fn, x->mod, "nt_replay"), "hipModuleGetFunction(nt_replay)");
   NT_HIP(hipModuleGetFunction(&x->fn_finish, x->mod, "nt_finish"), "hipModuleGetFunction(nt_finish)");
+  x->fn_slow = optional_function(x->mod, "nt_replay_slow");
   int per_cu = 0, cus = 0;
   NT_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, x->fn, x->low.plan.block, 0),
          "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
@@ -443,7 +470,9 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   for (auto& e : x->ev) NT_HIP(hipEventCreate(&e), "hipEventCreate");
   const int nch = x->low.plan.n_channels;
   NT_HIP(hipMalloc(&x->d_inputs, sizeof(double) * std::max(1, x->low.ir.n_in)), "hipMalloc(inputs)");
-  NT_HIP(hipMalloc(&x->d_partials, sizeof(double) * static_cast<size_t>(x->grid_cap) * nch), "hipMalloc(partials)");
+  NT_HIP(hipMalloc(&x->d_partials,
+                   sizeof(double) * static_cast<size_t>(ntr::partial_rows(x->grid_cap, x->fn_slow != nullptr)) * nch),
+         "hipMalloc(partials)");
   NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_sums), sizeof(double) * nch, hipHostMallocDefault),
          "hipHostMalloc(sums)");
   x->h_cap = static_cast<size_t>(nch);
@@ -467,15 +496,37 @@ int nt_exec_set_inputs(nt_exec* x, const double* inputs, int32_t n) {
 
 using ntr::grid_for;
 
-static int launch_kernel(nt_exec* x, hipFunction_t fn, double* d_inputs, double* d_partials, uint64_t paths,
-                         uint64_t offset, uint64_t seed, double* out_v, double* out_g, int& grid) {
-  grid = grid_for(x, paths);
-  return ntr::launch_kernel_on(x, x->stream, fn, d_inputs, d_partials, x->d_scratch, paths, offset, seed, out_v, out_g,
-                               grid);
+// Grows the flag bitmap to a dispatch over `paths` pricing `markets` sets.
+// The stream is drained first: the old bitmap may still be in use.
+static int ensure_flags(nt_exec* x, uint64_t paths, int markets) {
+  const size_t need = ntr::flags_bytes_for(paths, markets);
+  if (need <= x->flags_bytes) return NT_OK;
+  NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  if (x->d_flags) (void)hipFree(x->d_flags);
+  x->d_flags = nullptr;
+  x->flags_bytes = 0;
+  const size_t bytes = std::max(need, x->flags_bytes + x->flags_bytes / 2);
+  NT_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_flags), bytes), "hipMalloc(flags)");
+  x->flags_bytes = bytes;
+  // the count starts at zero; every finishing pass leaves it there
+  NT_HIP(hipMemsetAsync(x->d_flags, 0, sizeof(uint64_t), x->stream), "hipMemsetAsync(flags)");
+  return NT_OK;
 }
 
-static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v,
-                         double* out_g, int& grid) {
+// Replay kernel and, when it has one, exception kernel over `paths` on
+// `grid` blocks each.
+static int launch_kernel(nt_exec* x, hipFunction_t fn, hipFunction_t fn_slow, double* d_inputs, double* d_partials,
+                         int nch, int markets, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v,
+                         double* out_g, int& grid, hipEvent_t between = nullptr) {
+  grid = grid_for(x, paths);
+  int rc = ensure_flags(x, paths, markets);
+  if (rc != NT_OK) return rc;
+  return ntr::launch_kernel_on(x, x->stream, fn, fn_slow, d_inputs, d_partials, nch, x->d_scratch, x->d_flags, paths,
+                               offset, seed, out_v, out_g, grid, between);
+}
+
+static int launch_replay(nt_exec* x, hipFunction_t fn, hipFunction_t fn_slow, uint64_t paths, uint64_t offset,
+                         uint64_t seed, double* out_v, double* out_g, int& grid, hipEvent_t between = nullptr) {
   if (x->dirty) {
     if (!x->inputs.empty()) {
       NT_HIP(hipMemcpyAsync(x->d_inputs, x->inputs.data(), sizeof(double) * x->inputs.size(), hipMemcpyHostToDevice,
@@ -484,13 +535,16 @@ static int launch_replay(nt_exec* x, hipFunction_t fn, uint64_t paths, uint64_t 
     }
     x->dirty = false;
   }
-  return launch_kernel(x, fn, x->d_inputs, x->d_partials, paths, offset, seed, out_v, out_g, grid);
+  return launch_kernel(x, fn, fn_slow, x->d_inputs, x->d_partials, x->low.plan.n_channels, 1, paths, offset, seed,
+                       out_v, out_g, grid, between);
 }
 
-// Finishing pass over the `grid` partial rows of one replay launch: `nch` sums
-// written to host memory `out` (pinned, read after the stream drains).
-static int launch_finish(nt_exec* x, hipFunction_t fn, double* d_partials, int grid, int nch, double* out) {
-  return ntr::launch_finish_on(x->stream, fn, d_partials, grid, nch, out);
+// Finishing pass over the partial rows of one dispatch on `grid` blocks: `nch`
+// sums written to host memory `out` (pinned, read after the stream drains).
+static int launch_finish(nt_exec* x, hipFunction_t fn, hipFunction_t fn_slow, double* d_partials, int grid, int nch,
+                         double* out) {
+  return ntr::launch_finish_on(x->stream, fn, d_partials, grid, fn_slow ? grid : 0, nch, out,
+                               fn_slow ? x->d_flags : nullptr);
 }
 
 int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, double* sums, int32_t n_sums,
@@ -503,10 +557,9 @@ int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, d
   NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
   NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");
   int grid = 0;
-  int rc = launch_replay(x, x->fn, paths, offset, seed, nullptr, nullptr, grid);
+  int rc = launch_replay(x, x->fn, x->fn_slow, paths, offset, seed, nullptr, nullptr, grid, x->ev[1]);
   if (rc != NT_OK) return rc;
-  NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
-  rc = launch_finish(x, x->fn_finish, x->d_partials, grid, nch, x->h_sums);
+  rc = launch_finish(x, x->fn_finish, x->fn_slow, x->d_partials, grid, nch, x->h_sums);
   if (rc != NT_OK) return rc;
   NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
   NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
@@ -550,8 +603,12 @@ static int market_variant(nt_exec* x, int markets, MarketVariant*& out) {
   const size_t nch = static_cast<size_t>(x->low.plan.n_channels) * markets;
   hipError_t e = hipModuleGetFunction(&v.fn, v.mod, "nt_replay");
   if (e == hipSuccess) e = hipModuleGetFunction(&v.fn_finish, v.mod, "nt_finish");
+  if (e == hipSuccess) v.fn_slow = optional_function(v.mod, "nt_replay_slow");
   if (e == hipSuccess) e = hipMalloc(&v.d_inputs, sizeof(double) * std::max<size_t>(1, static_cast<size_t>(nin) * markets));
-  if (e == hipSuccess) e = hipMalloc(&v.d_partials, sizeof(double) * static_cast<size_t>(x->grid_cap) * nch);
+  if (e == hipSuccess) {
+    const size_t rows = static_cast<size_t>(ntr::partial_rows(x->grid_cap, v.fn_slow != nullptr));
+    e = hipMalloc(&v.d_partials, sizeof(double) * rows * nch);
+  }
   if (e != hipSuccess) {
     if (v.d_partials) (void)hipFree(v.d_partials);
     if (v.d_inputs) (void)hipFree(v.d_inputs);
@@ -638,9 +695,11 @@ int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, u
                               hipMemcpyHostToDevice, x->stream),
                "hipMemcpyAsync(input sets)");
       }
-      rc = launch_kernel(x, v->fn, v->d_inputs, v->d_partials, paths, offset, seed, nullptr, nullptr, grid);
+      rc = launch_kernel(x, v->fn, v->fn_slow, v->d_inputs, v->d_partials, nch * k, k, paths, offset, seed, nullptr,
+                         nullptr, grid);
       if (rc != NT_OK) return rc;
-      rc = launch_finish(x, v->fn_finish, v->d_partials, grid, nch * k, x->h_sums + static_cast<size_t>(m0) * nch);
+      rc = launch_finish(x, v->fn_finish, v->fn_slow, v->d_partials, grid, nch * k,
+                         x->h_sums + static_cast<size_t>(m0) * nch);
       if (rc != NT_OK) return rc;
     }
     NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
@@ -653,9 +712,11 @@ int nt_exec_replay_many(nt_exec* x, const double* input_sets, int32_t markets, u
                               hipMemcpyHostToDevice, x->stream),
                "hipMemcpyAsync(input set)");
       }
-      int rc = launch_kernel(x, x->fn, x->d_set_inputs, x->d_partials, paths, offset, seed, nullptr, nullptr, grid);
+      int rc = launch_kernel(x, x->fn, x->fn_slow, x->d_set_inputs, x->d_partials, nch, 1, paths, offset, seed, nullptr,
+                             nullptr, grid);
       if (rc != NT_OK) return rc;
-      rc = launch_finish(x, x->fn_finish, x->d_partials, grid, nch, x->h_sums + static_cast<size_t>(m) * nch);
+      rc = launch_finish(x, x->fn_finish, x->fn_slow, x->d_partials, grid, nch,
+                         x->h_sums + static_cast<size_t>(m) * nch);
       if (rc != NT_OK) return rc;
     }
     NT_HIP(hipEventRecord(x->ev[1], x->stream), "hipEventRecord");
@@ -686,6 +747,7 @@ int nt_exec_replay_paths(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t s
     if (rc != NT_OK) return rc;
     NT_HIP(hipModuleLoadData(&x->mod_dump, code.data()), "hipModuleLoadData(dump)");
     NT_HIP(hipModuleGetFunction(&x->fn_dump, x->mod_dump, "nt_replay"), "hipModuleGetFunction(dump)");
+    x->fn_dump_slow = optional_function(x->mod_dump, "nt_replay_slow");
   }
   const uint64_t rows = paths * static_cast<uint64_t>(x->low.ir.outputs.size());
   double* d_v = nullptr;
@@ -697,7 +759,12 @@ int nt_exec_replay_paths(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t s
     return hip_fail(e, "hipMalloc(grads)");
   }
   int grid = 0;
-  int rc = launch_replay(x, x->fn_dump, paths, offset, seed, d_v, d_g, grid);
+  int rc = launch_replay(x, x->fn_dump, x->fn_dump_slow, paths, offset, seed, d_v, d_g, grid);
+  if (rc == NT_OK && x->fn_dump_slow) {
+    // no finishing pass follows: the count of lanes with exception paths goes back to zero here
+    e = hipMemsetAsync(x->d_flags, 0, sizeof(uint64_t), x->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync(flags)");
+  }
   if (rc == NT_OK) {
     e = hipMemcpyAsync(values, d_v, sizeof(double) * rows, hipMemcpyDeviceToHost, x->stream);
     if (e == hipSuccess && nin > 0) {

@@ -67,6 +67,34 @@ __device__ __forceinline__ float nt_hw_cos2pif(float x) { return __builtin_amdgc
 __device__ __forceinline__ float nt_rcpf(float x) { return __builtin_amdgcn_rcpf(x); }
 #endif
 
+// Strong-zero numbers for the tangents of the re-evaluation pass: a product
+// with an exact zero is zero whatever the other factor is, infinite or NaN
+// included. The reverse sweep of the reference skips a node whose adjoint is
+// zero (ScalarReplay.java:134-136), so nothing flows back through it however
+// large its local derivative; in tangent mode the same happens when a zero
+// factor meets an infinite tangent, as in 1 / (1 + e) once e = exp(x) has
+// overflowed: the quotient's factor for e is 0 / inf = 0 and e's tangent is
+// infinite. Sums and differences stay IEEE. Only the re-evaluation pass of a
+// path uses them; the fast pass sends any path whose result is not finite
+// there.
+#define NT_STRONG_ZERO(T, S, FMA)                                                                              \
+  struct S {                                                                                                   \
+    T v;                                                                                                       \
+    __device__ __forceinline__ constexpr S(T x) : v(x) {}                                                      \
+    template <class U>                                                                                         \
+    __device__ __forceinline__ explicit operator U() const { return static_cast<U>(v); }                       \
+  };                                                                                                           \
+  __device__ __forceinline__ S operator*(S a, S b) { return (a.v == T(0) || b.v == T(0)) ? S(T(0)) : S(a.v * b.v); } \
+  __device__ __forceinline__ S operator+(S a, S b) { return S(a.v + b.v); }                                    \
+  __device__ __forceinline__ S operator-(S a, S b) { return S(a.v - b.v); }                                    \
+  __device__ __forceinline__ S operator-(S a) { return S(-a.v); }                                              \
+  __device__ __forceinline__ S FMA(S a, S b, S c) {                                                            \
+    return (a.v == T(0) || b.v == T(0)) ? c : S(FMA(a.v, b.v, c.v));                                          \
+  }
+NT_STRONG_ZERO(double, nt_sz, fma)
+NT_STRONG_ZERO(float, nt_szf, fmaf)
+#undef NT_STRONG_ZERO
+
 // fp32 exp as 2^(x log2 e) on the hardware exp2: the rounding of the product
 // adds |x| * 2^-24 relative error, well inside fp32 replay's 1e-5 reconcile
 // bar for Monte-Carlo exponents (|x| of order 1).
@@ -316,6 +344,18 @@ __device__ __forceinline__ double nt_wave_sum(double x) {
   return x;
 }
 
+// Bitmap of the paths a replay kernel leaves to the exception kernel: bit
+// p % 64 of word p / 64 for the dispatch's path p. A wave's 64 lanes hold 64
+// consecutive paths starting at a multiple of 64 (blocks are whole waves and
+// the grid stride is a multiple of 64), so lane l is bit l of the wave's
+// ballot and the lowest active lane stores the whole word: no atomics, and
+// every word of the dispatch is written (zero where no path was flagged).
+__device__ __forceinline__ void nt_flag_paths(nt_u64* __restrict__ flags, nt_u64 p, bool flagged) {
+  const nt_u64 mask = __ballot(flagged);
+  const nt_u64 active = __ballot(1);
+  if (__lane_id() == static_cast<unsigned>(__ffsll(static_cast<long long>(active)) - 1)) flags[p >> 6] = mask;
+}
+
 // Reduce NCH per-lane accumulators over the block and write one row of
 // partials[blockIdx.x * NCH + c]. `lds` holds NCH * (blockDim.x / 64) doubles.
 template <int NCH>
@@ -344,10 +384,16 @@ __device__ __forceinline__ void nt_block_store(const double (&acc)[NCH], double*
 // the block count, so a channel's result is bitwise the same whatever nch is (a
 // market's sums do not change with the markets priced beside it) and run to
 // run. `out` is host memory the caller reads after the stream has drained.
+// The rows of an exception kernel (slow_blocks of them, after the replay
+// kernel's) are added only when `count`, the number of lanes that left paths
+// to it, is nonzero (an exception kernel that found it zero wrote no rows);
+// the pass then sets `count` back to zero for the next dispatch.
 extern "C" __global__ __launch_bounds__(1024) void nt_finish(const double* __restrict__ partials, nt_u32 blocks,
-                                                           nt_u32 nch, double* __restrict__ out) {
+                                                           nt_u32 slow_blocks, nt_u32 nch, double* __restrict__ out,
+                                                           nt_u64* __restrict__ count) {
   const nt_u32 lane = threadIdx.x & 63;
   const nt_u32 waves = blockDim.x >> 6;
+  if (count && count[0] != 0) blocks += slow_blocks;
   for (nt_u32 c = threadIdx.x >> 6; c < nch; c += waves) {
     double s = 0.0;
     // unrolled so the loads of several rows are in flight at once; the adds
@@ -356,6 +402,10 @@ extern "C" __global__ __launch_bounds__(1024) void nt_finish(const double* __res
     for (nt_u32 b = lane; b < blocks; b += 64) s += partials[static_cast<nt_u64>(b) * nch + c];
     s = nt_wave_sum(s);
     if (lane == 0) out[c] = s;
+  }
+  if (count) {
+    __syncthreads();  // every thread has read count
+    if (threadIdx.x == 0) count[threadIdx.x] = 0;
   }
 }
 

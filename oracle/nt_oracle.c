@@ -36,6 +36,36 @@ void nto_philox2x32_10(uint32_t ctr0, uint32_t ctr1, uint32_t key, uint32_t out[
   out[1] = c1;
 }
 
+/* ---- sensitivity patterns (no reference counterpart) ------------------------
+ * A perturbed replay moves every transcendental result by one unit, up or
+ * down by a fixed pseudo-random pattern: log, sqrt, exp by one ulp (nextafter),
+ * sin and cos by 2^-53 absolute (their errors are absolute near zero). The
+ * difference from the unperturbed replay measures how much a path amplifies
+ * last-bit differences of libm, which is what separates two correct engines
+ * whose transcendentals differ in the last place. pattern 0 is the oracle. */
+static uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+static int nudge_up(uint64_t key, uint64_t pattern) {
+  return (int)(splitmix64(key ^ splitmix64(pattern)) >> 63);
+}
+
+static double nudge_rel(double x, uint64_t key, uint64_t pattern) {
+  if (!pattern || !isfinite(x) || x == 0.0) return x;
+  return nextafter(x, nudge_up(key, pattern) ? INFINITY : -INFINITY);
+}
+
+static double nudge_abs(double x, uint64_t key, uint64_t pattern) {
+  if (!pattern || !isfinite(x)) return x;
+  return nudge_up(key, pattern) ? x + 0x1p-53 : x - 0x1p-53;
+}
+
+static uint64_t path_key(uint64_t path) { return splitmix64(path * 0x9E3779B97F4A7C15ull + 0x632BE59BD9B4E019ull); }
+
 /* One random stream, the state of a reference Philox instance (Philox.java:34-53). */
 typedef struct stream_state {
   uint32_t lo, hi;
@@ -43,6 +73,7 @@ typedef struct stream_state {
   uint32_t uniform_counter;
   double spare;
   int has;
+  uint64_t key, pattern;  /* sensitivity pattern (0: none) and this stream's key for it */
 } stream_state;
 
 static void stream_init(stream_state *s, uint64_t path, uint64_t seed, int32_t stream) {
@@ -57,6 +88,8 @@ static void stream_init(stream_state *s, uint64_t path, uint64_t seed, int32_t s
   s->uniform_counter = 0;
   s->spare = 0.0;
   s->has = 0;
+  s->key = path_key(path) ^ ((uint64_t)(uint32_t)stream << 40);
+  s->pattern = 0;
 }
 
 /* Philox.normal(), Philox.java:55-78. */
@@ -66,14 +99,15 @@ static double stream_normal(stream_state *s) {
     return s->spare;
   }
   uint32_t o[2];
+  const uint64_t k = s->key ^ ((uint64_t)s->counter << 3);
   nto_philox2x32_10(s->lo, s->hi ^ s->counter++, NTO_KEY0, o);
   double u1 = ((double)o[0] + 0.5) * NTO_UINT_SCALE;
   double u2 = ((double)o[1] + 0.5) * NTO_UINT_SCALE;
-  double radius = sqrt(-2.0 * log(u1));
+  double radius = nudge_rel(sqrt(-2.0 * nudge_rel(log(u1), k ^ 1, s->pattern)), k ^ 2, s->pattern);
   double angle = 6.283185307179586 * u2;
-  s->spare = radius * sin(angle);
+  s->spare = radius * nudge_abs(sin(angle), k ^ 3, s->pattern);
   s->has = 1;
-  return radius * cos(angle);
+  return radius * nudge_abs(cos(angle), k ^ 4, s->pattern);
 }
 
 /* Philox.uniform(), Philox.java:81-94. */
@@ -156,7 +190,7 @@ static inline void adj_add(double *d, int32_t node, double contribution, int f32
 static void run_range(const nto_tape *t, const uint8_t *active, const double *in,
                       uint64_t from, uint64_t count, uint64_t seed, int f32, int adjoints,
                       double *value, double *sumsq, double *gradient,
-                      double *row_values, double *row_grads, uint64_t row_base) {
+                      double *row_values, double *row_grads, uint64_t row_base, uint64_t pattern) {
   const int32_t n = t->n;
   double *v = (double *)malloc(sizeof(double) * (size_t)n);
   double *d = (double *)malloc(sizeof(double) * (size_t)n);
@@ -167,7 +201,9 @@ static void run_range(const nto_tape *t, const uint8_t *active, const double *in
     const uint64_t path = from + i;
     for (int32_t s = 0; s < t->n_streams; s++) {
       stream_init(&rng[s], path, seed, s);
+      rng[s].pattern = pattern;
     }
+    const uint64_t nkey = path_key(path) ^ 0x5A5A000000000000ull;
     for (int32_t i = 0; i < n; i++) {
       int32_t a = t->arg_a[i], b = t->arg_b[i];
       double x;
@@ -181,9 +217,9 @@ static void run_range(const nto_tape *t, const uint8_t *active, const double *in
         case NTO_MUL: x = v[a] * v[b]; break;
         case NTO_DIV: x = v[a] / v[b]; break;
         case NTO_NEG: x = -v[a]; break;
-        case NTO_EXP: x = exp(v[a]); break;
-        case NTO_LOG: x = log(v[a]); break;
-        case NTO_SQRT: x = sqrt(v[a]); break;
+        case NTO_EXP: x = nudge_rel(exp(v[a]), nkey ^ ((uint64_t)i << 3), pattern); break;
+        case NTO_LOG: x = nudge_rel(log(v[a]), nkey ^ ((uint64_t)i << 3), pattern); break;
+        case NTO_SQRT: x = nudge_rel(sqrt(v[a]), nkey ^ ((uint64_t)i << 3), pattern); break;
         case NTO_ABS: x = fabs(v[a]); break;
         /* java.lang.Math.max/min: NaN if either is NaN, and -0.0 < +0.0 */
         case NTO_MAX:
@@ -267,7 +303,7 @@ static int resolve_threads(int threads) {
  * units/T (+1 for the first units%T workers); totals are added in worker order. */
 static int replay_impl(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                        uint64_t seed, int f32, int adjoints, int threads, nto_totals *out,
-                       double *row_values, double *row_grads) {
+                       double *row_values, double *row_grads, uint64_t pattern) {
   int rc = validate(t);
   if (rc != 0) return rc;
   uint8_t *active = (uint8_t *)malloc((size_t)t->n);
@@ -287,7 +323,7 @@ static int replay_impl(const nto_tape *t, const double *inputs, uint64_t paths, 
     if (count > 0) {
       run_range(t, active, inputs, from, count, seed, f32, adjoints,
                 val + (size_t)w * no, sq + (size_t)w * no, gr + (size_t)w * no * ni,
-                row_values, row_grads, offset);
+                row_values, row_grads, offset, pattern);
     }
   }
   if (out) {
@@ -313,12 +349,17 @@ static int replay_impl(const nto_tape *t, const double *inputs, uint64_t paths, 
 
 int nto_replay(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                uint64_t seed, int f32, int adjoints, int threads, nto_totals *out) {
-  return replay_impl(t, inputs, paths, offset, seed, f32, adjoints, threads, out, NULL, NULL);
+  return replay_impl(t, inputs, paths, offset, seed, f32, adjoints, threads, out, NULL, NULL, 0);
 }
 
 int nto_replay_paths(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                      uint64_t seed, int f32, int threads, double *values, double *grads) {
-  return replay_impl(t, inputs, paths, offset, seed, f32, 1, threads, NULL, values, grads);
+  return replay_impl(t, inputs, paths, offset, seed, f32, 1, threads, NULL, values, grads, 0);
+}
+
+int nto_replay_paths_perturbed(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
+                               uint64_t seed, int threads, uint64_t pattern, double *values, double *grads) {
+  return replay_impl(t, inputs, paths, offset, seed, 0, 1, threads, NULL, values, grads, pattern);
 }
 
 /* AadTotals.toResult, AadTotals.java:68-89. */
@@ -336,65 +377,4 @@ void nto_to_result(const nto_totals *sums, int32_t n_outputs, int32_t n_inputs, 
       mean_gradient[o * n_inputs + j] = sums->gradient[o * n_inputs + j] / (double)paths;
     }
   }
-}
-
-/* Forward sweep only, tracking the distance of each path to the singular
- * points of its active nodes (see nt_oracle.h). */
-int nto_replay_conditioning(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
-                            uint64_t seed, int f32, int threads, double *sing, double *tie) {
-  int rc = validate(t);
-  if (rc != 0) return rc;
-  uint8_t *active = (uint8_t *)malloc((size_t)t->n);
-  nto_mark_active(t, active);
-  const int T = resolve_threads(threads);
-#ifdef _OPENMP
-#pragma omp parallel num_threads(T)
-#endif
-  {
-    double *v = (double *)malloc(sizeof(double) * (size_t)t->n);
-    stream_state *rng = (stream_state *)malloc(sizeof(stream_state) * (size_t)t->n_streams);
-#ifdef _OPENMP
-#pragma omp for schedule(static)
-#endif
-    for (long long pi = 0; pi < (long long)paths; pi++) {
-      const uint64_t path = offset + (uint64_t)pi;
-      for (int32_t s = 0; s < t->n_streams; s++) stream_init(&rng[s], path, seed, s);
-      double ms = INFINITY, mt = INFINITY;
-      for (int32_t i = 0; i < t->n; i++) {
-        int32_t a = t->arg_a[i], b = t->arg_b[i];
-        double x;
-        switch (t->op[i]) {
-          case NTO_CONST: x = t->constant[i]; break;
-          case NTO_INPUT: x = inputs[a]; break;
-          case NTO_RANDN: x = stream_normal(&rng[b]); break;
-          case NTO_RANDU: x = stream_uniform(&rng[b]); break;
-          case NTO_ADD: x = v[a] + v[b]; break;
-          case NTO_SUB: x = v[a] - v[b]; break;
-          case NTO_MUL: x = v[a] * v[b]; break;
-          case NTO_DIV: x = v[a] / v[b]; if (active[i]) ms = fmin(ms, fabs(v[b])); break;
-          case NTO_NEG: x = -v[a]; break;
-          case NTO_EXP: x = exp(v[a]); break;
-          case NTO_LOG: x = log(v[a]); if (active[i]) ms = fmin(ms, fabs(v[a])); break;
-          /* sqrt(0) is a kink that a MAX/MIN in front of it decides (counted in tie) */
-          case NTO_SQRT: x = sqrt(v[a]); if (active[i] && v[a] != 0.0) ms = fmin(ms, fabs(v[a])); break;
-          case NTO_ABS: x = fabs(v[a]); break;
-          case NTO_MAX:
-          case NTO_MIN: {
-            const double p = v[a], q = v[b];
-            if (active[i]) mt = fmin(mt, fabs(p - q) / fmax(1.0, fmax(fabs(p), fabs(q))));
-            x = t->op[i] == NTO_MAX ? (p >= q ? p : q) : (p <= q ? p : q);
-            break;
-          }
-          default: x = NAN; break;
-        }
-        v[i] = f32 ? (double)(float)x : x;
-      }
-      sing[pi] = ms;
-      tie[pi] = mt;
-    }
-    free(rng);
-    free(v);
-  }
-  free(active);
-  return 0;
 }

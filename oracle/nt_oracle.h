@@ -18,12 +18,23 @@
  *                       split over threads as HostAadExecutable.runRanges
  *                       (nablatensor-core/.../HostAadExecutable.java:85-117)
  *   nto_replay_paths    the same per-path values and adjoints, one row per path
+ *   nto_replay_paths_perturbed
+ *                       the same with every transcendental result moved by one
+ *                       unit (no reference counterpart: the tests' yardstick
+ *                       of each path's sensitivity to libm's last place)
  *   nto_to_result       AadTotals.toResult, nablatensor-core/.../AadTotals.java:68-89
  *
  * Parity pins (tests/test_oracle.py): Random123 KATs for the round function;
  * the reference-held Asian-call aggregates (docs/validation.md:56-63);
  * Black-Scholes closed form; knock-out + knock-in = vanilla; central
- * differences on small tapes; per-path hand evaluation of the 1-step European.
+ * differences on small tapes; per-path hand evaluation of the 1-step European;
+ * sums and standard error against the per-path rows (sample standard
+ * deviation); the Merton jump tape (uniform draws) against the exact Poisson
+ * series within 1.5% (JumpModelsTest.java:46-53), its no-jump limit against
+ * Black-Scholes, its adjoint delta against a bump; uniform and named-stream
+ * moments as RandomStreamsTest.java:51-103. The named-stream multiplier
+ * 0x9E3779B1 (Philox.java:48-50) is restated from the source text: only the
+ * streams' independence is pinned, not the literal.
  */
 #ifndef NT_ORACLE_H
 #define NT_ORACLE_H
@@ -77,14 +88,15 @@ int nto_replay(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t
 int nto_replay_paths(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
                      uint64_t seed, int f32, int threads, double *values, double *grads);
 
-/* Conditioning of each path of output 0 (no reference counterpart; used by the
- * tests to tell ill-conditioned paths from engine error). sing[p] = smallest
- * |argument| of an active SQRT (nonzero arguments), LOG or DIV-denominator
- * node (their local derivatives grow without bound as it goes to 0); tie[p] = smallest
- * |a - b| / max(1, |a|, |b|) over active MAX/MIN nodes (a branch within
- * rounding of flipping). Either is +inf when the tape has no such node. */
-int nto_replay_conditioning(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
-                            uint64_t seed, int f32, int threads, double *sing, double *tie);
+/* nto_replay_paths in fp64 with every transcendental result moved by one
+ * unit, up or down by the fixed pseudo-random pattern `pattern` (nonzero):
+ * the log, sqrt and exp results of Box-Muller and of EXP/LOG/SQRT nodes by
+ * one ulp, Box-Muller's sin and cos by 2^-53 absolute. No reference
+ * counterpart: the difference from nto_replay_paths is each path's
+ * sensitivity to last-place differences of libm, the yardstick the tests
+ * scale their per-path bound by. */
+int nto_replay_paths_perturbed(const nto_tape *t, const double *inputs, uint64_t paths, uint64_t offset,
+                               uint64_t seed, int threads, uint64_t pattern, double *values, double *grads);
 
 /* mean, standard error and mean gradient from raw sums (AadTotals.toResult). */
 void nto_to_result(const nto_totals *sums, int32_t n_outputs, int32_t n_inputs, uint64_t paths,

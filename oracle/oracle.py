@@ -49,9 +49,9 @@ def lib() -> C.CDLL:
         L.nto_replay_paths.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
                                        C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
                                        C.POINTER(C.c_double)]
-        L.nto_replay_conditioning.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
-                                              C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
-                                              C.POINTER(C.c_double)]
+        L.nto_replay_paths_perturbed.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
+                                                 C.c_uint64, C.c_int, C.c_uint64, C.POINTER(C.c_double),
+                                                 C.POINTER(C.c_double)]
         _lib = L
     return _lib
 
@@ -122,24 +122,50 @@ def replay_sums(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=
 
 
 def replay_paths(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, f32: bool = False,
-                 threads: int = 0, output=0) -> tuple[np.ndarray, np.ndarray]:
+                 threads: int = 0, output=0, perturb: int = 0) -> tuple[np.ndarray, np.ndarray]:
     """Per-path value and adjoints of output `output` (None: every output,
-    shapes (paths, outputs) and (paths, outputs, inputs))."""
+    shapes (paths, outputs) and (paths, outputs, inputs)). perturb != 0 (fp64
+    only) moves every transcendental result by one unit in the fixed
+    pseudo-random pattern `perturb` (nto_replay_paths_perturbed)."""
     t = Tape(flat)
     x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
     no = len(t.output_node)
     values = np.zeros((paths, no))
     grads = np.zeros((paths, no, max(1, t.n_inputs)))
-    rc = lib().nto_replay_paths(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
-                                offset & (2**64 - 1), seed & (2**64 - 1), int(f32), threads,
-                                values.ctypes.data_as(C.POINTER(C.c_double)),
-                                grads.ctypes.data_as(C.POINTER(C.c_double)))
+    if perturb:
+        if f32:
+            raise ValueError("perturbed replays are fp64")
+        rc = lib().nto_replay_paths_perturbed(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
+                                              offset & (2**64 - 1), seed & (2**64 - 1), threads, perturb,
+                                              values.ctypes.data_as(C.POINTER(C.c_double)),
+                                              grads.ctypes.data_as(C.POINTER(C.c_double)))
+    else:
+        rc = lib().nto_replay_paths(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
+                                    offset & (2**64 - 1), seed & (2**64 - 1), int(f32), threads,
+                                    values.ctypes.data_as(C.POINTER(C.c_double)),
+                                    grads.ctypes.data_as(C.POINTER(C.c_double)))
     if rc != 0:
         raise ValueError(f"oracle rejected the tape ({rc})")
     grads = grads[:, :, :t.n_inputs]
     if output is None:
         return values, grads
     return values[:, output].copy(), grads[:, output, :].copy()
+
+
+def to_result_c(sums: np.ndarray, paths: int, n_inputs: int) -> dict:
+    """nto_to_result (the C restatement of AadTotals.toResult) for one output."""
+    L = lib()
+    L.nto_to_result.argtypes = [C.POINTER(_Totals), C.c_int32, C.c_int32, C.c_uint64, C.POINTER(C.c_double),
+                                C.POINTER(C.c_double), C.POINTER(C.c_double)]
+    val = np.array([sums[0]], dtype=np.float64)
+    sq = np.array([sums[1]], dtype=np.float64)
+    gr = np.ascontiguousarray(sums[2:2 + n_inputs], dtype=np.float64)
+    tot = _Totals(val.ctypes.data_as(C.POINTER(C.c_double)), sq.ctypes.data_as(C.POINTER(C.c_double)),
+                  gr.ctypes.data_as(C.POINTER(C.c_double)))
+    mean, se, mg = np.zeros(1), np.zeros(1), np.zeros(max(1, n_inputs))
+    L.nto_to_result(C.byref(tot), 1, n_inputs, paths, mean.ctypes.data_as(C.POINTER(C.c_double)),
+                    se.ctypes.data_as(C.POINTER(C.c_double)), mg.ctypes.data_as(C.POINTER(C.c_double)))
+    return {"price": float(mean[0]), "stderr": float(se[0]), "gradient": mg[:n_inputs]}
 
 
 def to_result(sums: np.ndarray, paths: int) -> dict:
@@ -152,22 +178,6 @@ def to_result(sums: np.ndarray, paths: int) -> dict:
     else:
         se = float("nan")
     return {"price": mean, "stderr": se, "gradient": np.asarray(sums[2:]) / n}
-
-
-def conditioning(flat: dict, paths: int, offset: int = 0, seed: int = 42, inputs=None, threads: int = 0):
-    """Per path: (smallest |arg| of an active SQRT/LOG/DIV denominator, smallest
-    relative MAX/MIN gap) -- how close the path runs to a singular point."""
-    t = Tape(flat)
-    x = np.ascontiguousarray(t.recorded if inputs is None else inputs, dtype=np.float64)
-    sing = np.zeros(paths)
-    tie = np.zeros(paths)
-    rc = lib().nto_replay_conditioning(C.byref(t.s), x.ctypes.data_as(C.POINTER(C.c_double)), paths,
-                                       offset & (2**64 - 1), seed & (2**64 - 1), 0, threads,
-                                       sing.ctypes.data_as(C.POINTER(C.c_double)),
-                                       tie.ctypes.data_as(C.POINTER(C.c_double)))
-    if rc != 0:
-        raise ValueError(f"oracle rejected the tape ({rc})")
-    return sing, tie
 
 
 def path_errors(values, grads, ref_values, ref_grads):

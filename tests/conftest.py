@@ -75,37 +75,110 @@ def gpu_available() -> bool:
         return False
 
 
-COND_STRICT = 1e-5  # distance to a singular point at or above which a path must meet 1e-12
+# Per-path bar. Each path is held, per component (its value and each
+# derivative, relative with floor 1), to max(TOL, SENS_K x s), where s is the
+# oracle's own sensitivity: the largest change of that component when the
+# oracle replays the path with every transcendental result moved by one unit
+# (log, sqrt, exp by one ulp; Box-Muller's sin and cos by 2^-53), up or down in
+# each of the fixed pseudo-random patterns SENS_PATTERNS. A correct engine
+# differs from the oracle by last-place differences of its libm (the
+# skeleton's own log within 2 ulp, sin/cos within 2 * 2^-53) and of its
+# arithmetic order; a well-conditioned path has s below TOL / SENS_K and is held
+# to TOL. Measured on the CPU emulation of the kernels (4,096 Heston paths,
+# both derivative modes): actual error / s has median 0.4, and no component
+# above 1e-12 exceeds 4 s; SENS_K = 8 keeps a factor 2 beyond that.
+TOL = 1e-12
+SENS_K = 8.0
+SENS_PATTERNS = (1, 2, 3)
+# Fraction of paths held to TOL on every component, per workload: the lowest
+# measured over the path samples the tests use (30 to 4,096 paths at offset
+# 0x100000003, seeds 42 and 7). The rest are paths whose value is a small
+# difference of large quantities (an Asian or barrier payoff just in the
+# money: A - K with A near 100 loses two digits against the floor of 1) or,
+# in the Heston tape, whose variance grazes the full-truncation floor.
+STRICT = {"C1": 1.0, "C2": 0.94, "C3": 0.84, "C4": 0.80, "C5": 0.95}
 
 
-ILL_CONDITIONED_TOL = 1e-8
+def componentwise_errors(values, grads, ref_values, ref_grads):
+    """Per path: |dv| / max(1, |v|), and per derivative |dg_j| / max(1, |g_j|).
+    Equal values (also equal infinities) and NaN against NaN agree; any other
+    non-finite difference is an infinite error."""
+    def rel(a, b):
+        a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+        with np.errstate(invalid="ignore"):
+            d = np.abs(a - b)
+            d = np.where((a == b) | (np.isnan(a) & np.isnan(b)), 0.0, d)
+            d = np.where(np.isnan(d), np.inf, d)
+            return d / np.maximum(1.0, np.nan_to_num(np.abs(b), nan=1.0))
+    return rel(values, ref_values), rel(grads, ref_grads)
 
 
-def per_path_bounds(cond: np.ndarray, tol: float = 1e-12) -> np.ndarray:
-    """Per-path tolerance: `tol` on well-conditioned paths. A path that comes
-    within 1e-5 of a singular point of an active node (SQRT/LOG argument, DIV
-    denominator, MAX/MIN tie) amplifies a last-bit difference in its draws
-    roughly as 1e-17 / distance (measured on the Heston tape, where the
-    variance grazes the full-truncation floor); such paths are held to 1e-8."""
-    return np.where(cond >= COND_STRICT, tol, ILL_CONDITIONED_TOL)
-
-
-def check_per_path(values, grads, flat, paths, offset, seed, tol=1e-12, min_strict=0.5):
-    """Compares per-path values/adjoints with the oracle (value componentwise,
-    gradient normwise) under per_path_bounds; returns a summary dict."""
+def path_sensitivity(flat, paths, offset, seed, inputs=None):
+    """The oracle's per-path rows (values, gradients) and their sensitivity to
+    one-unit moves of every transcendental result (same shapes), the largest
+    over SENS_PATTERNS."""
     import oracle
-    ov, og = oracle.replay_paths(flat, paths, offset, seed)
-    ev, eg = oracle.path_errors(values, grads, ov, og)
-    sing, tie = oracle.conditioning(flat, paths, offset, seed)
-    cond = np.minimum(sing, tie)
-    bound = per_path_bounds(cond, tol)
-    err = np.maximum(ev, eg)
-    strict = cond >= COND_STRICT
-    out = {"max_err_strict": float(err[strict].max()) if strict.any() else 0.0,
-           "max_err_all": float(err.max()), "strict_paths": int(strict.sum()), "paths": paths,
-           "violations": int(np.sum(err > bound))}
+    ov, og = oracle.replay_paths(flat, paths, offset, seed, inputs=inputs)
+    sv, sg = np.zeros_like(ov), np.zeros_like(og)
+    for pattern in SENS_PATTERNS:
+        pv, pg = oracle.replay_paths(flat, paths, offset, seed, inputs=inputs, perturb=pattern)
+        dv, dg = componentwise_errors(pv, pg, ov, og)
+        sv, sg = np.maximum(sv, dv), np.maximum(sg, dg)
+    return ov, og, sv, sg
+
+
+def check_per_path(values, grads, flat, paths, offset, seed, tol=TOL, min_strict=1.0, inputs=None):
+    """Compares per-path values and derivatives with the oracle, component by
+    component, under the sensitivity-scaled bound above. `min_strict` is the
+    fraction of paths that must be held to `tol` on every component (their
+    sensitivity is below tol / SENS_K), set at the measured fraction of the
+    call's path sample: the fraction is a property of the oracle alone, and
+    pinning it keeps the sensitivity measurement from excusing paths it did
+    not excuse when the bar was set. Returns a summary, with the normwise
+    gradient error (max_j |dg_j| / max(1, max_j |g_j|)) beside."""
+    import oracle
+    ov, og, sv, sg = path_sensitivity(flat, paths, offset, seed, inputs)
+    ev, eg = componentwise_errors(values, grads, ov, og)
+    bv, bg = np.maximum(tol, SENS_K * sv), np.maximum(tol, SENS_K * sg)
+    bad = (ev > bv) | (np.any(eg > bg, axis=1) if eg.size else False)
+    strict = (bv == tol) & (np.all(bg == tol, axis=1) if bg.size else True)
+    err = np.maximum(ev, eg.max(axis=1)) if eg.size else ev
+    _, normwise = oracle.path_errors(values, grads, ov, og)
+    out = {"paths": paths, "violations": int(np.sum(bad)), "strict_fraction": float(np.mean(strict)),
+           "paths_above_tol": int(np.sum(err > tol)), "max_err": float(err.max()),
+           "max_err_strict": float(err[strict].max()) if strict.any() else 0.0,
+           "max_normwise": float(normwise.max()) if normwise.size else 0.0}
     assert out["violations"] == 0, out
-    assert strict.mean() >= min_strict, out
+    assert out["strict_fraction"] >= min_strict, out
+    return out
+
+
+def reconcile(got_sums, want_sums, paths, flat, seed, offset=0, sample=20_000, rel=1e-5, in_se=0.05):
+    """fp32 against fp64 aggregates. The price within `rel` relative; each
+    Greek within max(rel |g_j|, in_se se_j), se_j the Greek's own Monte-Carlo
+    standard error at `paths` scenarios (from the oracle's per-path rows of the
+    first `sample` paths): an fp32 engine may differ by a negligible fraction
+    of the Monte-Carlo error the result carries anyway. That floor matters
+    where a path's derivative jumps between Greeks on a rounding-level change:
+    a worst-of path on which two assets end within fp32 rounding of each other
+    credits its delta and vega to the other one, about 1 / n of a per-path
+    Greek in absolute terms, far above 1e-5 of a small mean. Returns the
+    per-Greek relative errors, the errors in standard errors, the Greeks held
+    by the floor, the normwise error max_j |dg_j| / max_j |g_j|, and `ok`."""
+    import oracle
+    got, want = oracle.to_result(got_sums, paths), oracle.to_result(want_sums, paths)
+    _, rows = oracle.replay_paths(flat, min(paths, sample), offset, seed)
+    se = rows.std(axis=0, ddof=1) / np.sqrt(paths)
+    g, w = np.asarray(got["gradient"]), np.asarray(want["gradient"])
+    d = np.abs(g - w)
+    rel_err = d / np.abs(w)
+    in_se_err = d / se
+    by_floor = [int(j) for j in np.nonzero((rel_err > rel) & (in_se_err <= in_se))[0]]
+    out = {"price": abs(got["price"] - want["price"]) / abs(want["price"]),
+           "greek_rel_max": float(rel_err.max()), "greek_se_max": float(in_se_err.max()),
+           "held_by_se_floor": by_floor, "normwise": float(d.max() / np.abs(w).max())}
+    out["ok"] = bool(out["price"] <= rel and np.all(d <= np.maximum(rel * np.abs(w), in_se * se))
+                     and out["normwise"] <= rel)
     return out
 
 
@@ -178,3 +251,74 @@ def sqrt_classes_tape(nt, s_val, floor=True, steps=16):
             acc = acc.add(x.sqrt().mul(w))
         rec.output(acc)
     return nt.AadRecorder.record(body)
+
+
+MERTON_FIELDS = ("spot", "strike", "vol", "rate", "maturity", "jumpIntensity", "jumpMean", "jumpVol")
+
+
+def merton_call_tape(nt, market: dict, maturity=1.0, steps=128, width=2.0e-4):
+    """MertonJumpModel.european(CALL, maturity, steps, width) as the reference
+    records it (MertonJumpModel.java:59-121): the MertonJumpMarket inputs in
+    field order (MertonJumpMarket.java, recorded up front by Nabla.Inputs,
+    Nabla.java:201-207), kappa = exp(muJ + deltaJ^2/2) - 1 once, then per step
+    a diffusion normal, a uniform and a jump normal (in that order), the
+    compensator -ln(1 + lambda kappa dt), the log-Euler diffusion, the smoothed
+    indicator Smooth.lt(u, lambda dt) = 1 / (1 + exp(-(lambda dt - u) / width))
+    (Smooth.java:44-68) and the jump factor exp(muJ + deltaJ zJ) - 1; payoff
+    max(S - K, 0) exp(-r T)."""
+    dt = maturity / steps
+    sqrt_dt = dt ** 0.5
+
+    def body(rec):
+        x = {f: rec.input(f, float(market[f])) for f in MERTON_FIELDS}
+        rate, vol, lam, mu_j, dl_j = x["rate"], x["vol"], x["jumpIntensity"], x["jumpMean"], x["jumpVol"]
+        kappa = mu_j.add(dl_j.mul(dl_j).mul(0.5)).exp().sub(1.0)
+        s = x["spot"]
+        for _ in range(steps):
+            z = rec.randn()
+            u = rec.randu()
+            zj = rec.randn()
+            compensator = lam.mul(kappa).mul(dt).add(1.0).log()
+            drift = rate.sub(vol.mul(vol).mul(0.5)).mul(dt).sub(compensator)
+            diffused = s.mul(drift.add(vol.mul(sqrt_dt).mul(z)).exp())
+            p = lam.mul(dt)
+            e = p.sub(u).div(width).neg().exp()
+            occurs = rec.constant(1.0).div(e.add(1.0))
+            factor = mu_j.add(dl_j.mul(zj)).exp().sub(1.0)
+            s = diffused.mul(rec.constant(1.0).add(occurs.mul(factor)))
+        intrinsic = s.sub(x["strike"]).max(0.0)
+        discount = rate.neg().mul(maturity).exp()
+        rec.output(intrinsic.mul(discount))
+    return nt.AadRecorder.record(body)
+
+
+def merton_series_call(spot, strike, maturity, rate, vol, lam, mu_j, dl_j):
+    """The Merton jump-diffusion call as its truncated Poisson series of
+    Black-Scholes prices (MertonJumpDiffusion.price, MertonJumpDiffusion.java:
+    price(); Merton 1976): with kappa = exp(muJ + deltaJ^2/2) - 1 and
+    lambda' = lambda (1 + kappa), the sum over n of Poisson(lambda' T) weights
+    times Black-Scholes with sigma_n^2 = sigma^2 + n deltaJ^2 / T and
+    r_n = r - lambda kappa + n ln(1 + kappa) / T (carry b = r_n), stopped once
+    the weights cover 1 - 1e-14."""
+    from math import erfc, exp, log, log1p, sqrt
+
+    def ncdf(x):
+        return 0.5 * erfc(-x / sqrt(2.0))
+
+    def bs_call(r, b, sigma):
+        d1 = (log(spot / strike) + (b + 0.5 * sigma * sigma) * maturity) / (sigma * sqrt(maturity))
+        d2 = d1 - sigma * sqrt(maturity)
+        return spot * exp((b - r) * maturity) * ncdf(d1) - strike * exp(-r * maturity) * ncdf(d2)
+
+    kappa = exp(mu_j + 0.5 * dl_j * dl_j) - 1.0
+    lam_t = lam * (1.0 + kappa) * maturity
+    total, weight, covered = 0.0, exp(-lam_t), 0.0
+    for n in range(256):
+        sigma_n = sqrt(vol * vol + n * dl_j * dl_j / maturity)
+        r_n = rate - lam * kappa + n * log1p(kappa) / maturity
+        total += weight * bs_call(r_n, r_n, sigma_n)
+        covered += weight
+        if covered > 1.0 - 1e-14 and n > 0:
+            break
+        weight *= lam_t / (n + 1)
+    return total

@@ -15,12 +15,23 @@ extern "C" int emu_run(nt_u64 n_paths, nt_u64 offset, nt_u64 seed, const double*
   nt_tables_load();
   blockDim.x = block;
   std::vector<real> scratch(static_cast<size_t>(grid) * block * (slots ? slots : 1));
+  // one bitmap per market (at most 64 markets)
+  std::vector<nt_u64> flags(1 + static_cast<size_t>((n_paths + 63) / 64) * 64, 0);  // count, then the bitmaps
   for (unsigned b = 0; b < grid; ++b) {
     for (unsigned t = 0; t < block; ++t) {
       blockIdx.x = b;
       threadIdx.x = t;
-      nt_replay(inputs, n_paths, offset, seed, sums, scratch.data(), out_v, out_g);
+      nt_replay(inputs, n_paths, offset, seed, sums, scratch.data(), out_v, out_g, flags.data());
     }
   }
+#ifdef NT_HAS_SLOW
+  for (unsigned b = 0; b < grid; ++b) {
+    for (unsigned t = 0; t < block; ++t) {
+      blockIdx.x = b;
+      threadIdx.x = t;
+      nt_replay_slow(inputs, n_paths, offset, seed, sums, scratch.data(), out_v, out_g, flags.data());
+    }
+  }
+#endif
   return 0;
 }

@@ -54,6 +54,19 @@ inline void sincospif(float x, float* s, float* c) {
   *c = static_cast<float>(::cos(a));
 }
 
+// The emulated threads of a block run one after another: every block is taken
+// to hold a flagged path, and each thread sets its own bits in a bitmap the
+// driver zeroed.
+inline int __syncthreads_or(int) { return 1; }
+inline unsigned long long atomicAdd(unsigned long long* a, unsigned long long v) {
+  const unsigned long long old = *a;
+  *a += v;
+  return old;
+}
+inline void nt_flag_paths(unsigned long long* flags, unsigned long long p, bool flagged) {
+  if (flagged) flags[p >> 6] |= 1ull << (p & 63);
+}
+
 // Sequential stand-in for the block reduction: every emulated thread adds its
 // accumulators into partials[0 .. NCH).
 template <int NCH>

@@ -1,11 +1,13 @@
 """GPU parity of the HIP replay engine against the CPU oracle, through the C ABI.
 
 Both derivative modes (the reverse sweep under each checkpoint policy, and
-tangent mode) are held to the same bars. Bars (fp64): per path within 1e-12 of the oracle (value relative with floor 1,
-gradient normwise) on every path that stays at least 1e-5 from a singular point
-of an active node, with the bound scaled by the conditioning below that
-(conftest.per_path_bounds); sums over paths within 1e-10. fp32 reconciles with the fp64 oracle within 1e-5 on price
-and first-order Greeks. The reference-held aggregates of the Asian call
+tangent mode) are held to the same bars. Bars (fp64): per path and per
+component (the value and each Greek, relative with floor 1) within
+max(1e-12, 8 x the oracle's own sensitivity to one-unit moves of its
+transcendental results) (conftest.check_per_path), with the fraction of paths
+held to 1e-12 itself pinned; sums over paths within 1e-10. fp32 reconciles with
+the fp64 oracle within 1e-5 on price and on each first-order Greek (floored at
+that Greek's standard error, conftest.reconcile). The reference-held aggregates of the Asian call
 (docs/validation.md:56-63) are reproduced at their printed precision.
 """
 from __future__ import annotations
@@ -14,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import check_per_path, rel_err
+from conftest import STRICT, check_per_path, reconcile, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -48,18 +50,18 @@ def test_per_path_fp64_matches_oracle(rocm, tapes, name, paths, mode, ckpt, libm
         info = x.info()
     assert info["scratch_bytes"] == 0
     assert info["mode"] == mode
-    summary = check_per_path(v, g, t, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
+    summary = check_per_path(v, g, t, paths, OFFSET, 42, min_strict=STRICT[name])
     print(summary)
 
 
 @pytest.mark.parametrize("mode", [1, 2])
 def test_per_path_fp64_heston_many_paths(rocm, tapes, mode):
-    """4096 Heston paths: the conditioning-scaled bound holds on all of them."""
+    """4096 Heston paths: the sensitivity-scaled bound holds on every path and component."""
     t = tapes["C4"]
     print(f"case C4 mode={mode} paths=4096 seed=7", flush=True)
     with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         v, g = x.replay_paths(4096, OFFSET, 7)
-    print(check_per_path(v, g, t, 4096, OFFSET, 7, min_strict=0.5))
+    print(check_per_path(v, g, t, 4096, OFFSET, 7, min_strict=STRICT["C4"]))
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -68,7 +70,7 @@ def test_per_path_fp64_worst_of_matches_oracle(rocm, tapes, mode):
     print(f"case C5 mode={mode} paths=256", flush=True)
     with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         v, g = x.replay_paths(256, 7, 42)
-    print(check_per_path(v, g, t, 256, 7, 42, min_strict=0.99))
+    print(check_per_path(v, g, t, 256, 7, 42, min_strict=STRICT["C5"]))
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -105,13 +107,9 @@ def test_fp32_reconciles_with_fp64_oracle(rocm, tapes, name, paths, mode):
     with rocm.Executable(t, rocm.options("fp32", mode=mode)) as x:
         sums, _ = x.replay(paths, 0, 42)
     ref = oracle.replay_sums(t, paths, 0, 42)
-    got = oracle.to_result(sums, paths)
-    want = oracle.to_result(ref, paths)
-    errs = {"price": abs(got["price"] - want["price"]) / abs(want["price"])}
-    for j, gj in enumerate(want["gradient"]):
-        errs[f"grad{j}"] = abs(got["gradient"][j] - gj) / max(abs(gj), 1e-12)
-    print(name, "mode", mode, {k: f"{v:.2e}" for k, v in errs.items()})
-    assert max(errs.values()) <= 1e-5, errs
+    errs = reconcile(sums, ref, paths, t, 42)
+    print(name, "mode", mode, errs)
+    assert errs["ok"] and errs["greek_rel_max"] <= 1e-5, errs  # every Greek within 1e-5 relative
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -271,25 +269,56 @@ def test_loop_tangents_over_inputs_and_parameters_on_device(rocm, tapes, name, p
         v, g = x.replay_paths(paths, OFFSET, 42)
         info = x.info()
     assert info["scratch_bytes"] == 0
-    print(check_per_path(v, g, t, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99))
+    print(check_per_path(v, g, t, paths, OFFSET, 42, min_strict=STRICT[name]))
 
 
 def test_worst_of_fp32_over_parameters_reconciles(rocm, tapes):
     """The fp32 worst-of kernel (tangents over the loop's parameters) against
-    the fp64 oracle over 20,000 paths: price within 1e-5 relative, the 33
-    Greeks within 1e-5 of the largest one (normwise: a worst-of's Greeks for
-    assets that are seldom the worst are near zero, where a componentwise
-    relative bar measures fp32 rounding of nothing)."""
+    the fp64 oracle over 20,000 paths: price within 1e-5 relative, each of the
+    33 Greeks within 1e-5 relative or 0.05 of its standard error, and 1e-5
+    normwise (conftest.reconcile)."""
     t = tapes["C5"]
     print("case C5 fp32 paths=20000", flush=True)
     src = rocm.lower(t, rocm.options("fp32", mode=2))
     assert "basis=params" in src
     with rocm.Executable(t, rocm.options("fp32", mode=2)) as x:
         sums, _ = x.replay(20_000, 0, 42)
-    got = oracle.to_result(sums, 20_000)
-    want = oracle.to_result(oracle.replay_sums(t, 20_000, 0, 42), 20_000)
-    ep = abs(got["price"] - want["price"]) / abs(want["price"])
-    gw = np.asarray(want["gradient"])
-    eg = np.max(np.abs(np.asarray(got["gradient"]) - gw)) / np.max(np.abs(gw))
-    print(f"price rel err {ep:.2e}, Greeks normwise {eg:.2e}")
-    assert ep <= 1e-5 and eg <= 1e-5
+    errs = reconcile(sums, oracle.replay_sums(t, 20_000, 0, 42), 20_000, t, 42)
+    print(errs)
+    assert errs["ok"], errs
+
+
+MERTON = dict(spot=100.0, strike=100.0, vol=0.18, rate=0.03, maturity=1.0, jumpIntensity=0.75, jumpMean=-0.05,
+              jumpVol=0.15)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_merton_jump_tape_per_path(rocm, nt, mode):
+    """The Merton jump-diffusion call (MertonJumpModel.european, 128 steps: a
+    normal, a uniform and a normal per step) per path against the oracle."""
+    from conftest import merton_call_tape
+    flat = merton_call_tape(nt, MERTON).flat()
+    print(f"case merton mode={mode} paths=2048", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+        v, g = x.replay_paths(2048, OFFSET, 42)
+        assert x.info()["loop_period"] > 0
+    print(check_per_path(v, g, flat, 2048, OFFSET, 42, min_strict=0.94))  # measured 0.947
+
+
+def test_merton_jump_tape_converges_to_the_poisson_series(rocm, nt):
+    """JumpModelsTest.mertonMonteCarloConvergesToThePoissonSeries at its own
+    size (1,500,000 scenarios, seed 42, 128 steps): the device sums agree with
+    the oracle's within 1e-10 and the price is within 1.5% of the exact
+    Poisson-series price (docs/examples/jump-models.md:48-50)."""
+    from conftest import merton_call_tape, merton_series_call
+    flat = merton_call_tape(nt, MERTON).flat()
+    paths = 1_500_000
+    print(f"case merton series paths={paths}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64")) as x:
+        sums, _ = x.replay(paths, 0, 42)
+    ref = oracle.replay_sums(flat, paths, 0, 42)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-10
+    price = oracle.to_result(sums, paths)["price"]
+    exact = merton_series_call(100, 100, 1.0, 0.03, 0.18, 0.75, -0.05, 0.15)
+    print(f"price {price:.6f} series {exact:.6f} rel {(price - exact) / exact:.2e}")
+    assert abs(price - exact) <= 0.015 * exact

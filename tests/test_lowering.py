@@ -20,7 +20,7 @@ import pytest
 
 import emu
 import oracle
-from conftest import check_per_path, equity_tape, rel_err, scaled_exp_tape, sqrt_classes_tape, tape_slots
+from conftest import STRICT, check_per_path, equity_tape, rel_err, scaled_exp_tape, sqrt_classes_tape, tape_slots
 
 OFFSET = 0x100000003
 
@@ -77,7 +77,7 @@ def test_emulated_tangent_values_bit_exact_gradients_within_bar(rocm, tapes, nam
     sums, v, g = run_emulated(flat, opts, paths, rocm=rocm)
     ov, _ = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
     assert_values_match(v, ov, rocm.lower(flat, opts))
-    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
+    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=STRICT[name])
     ref = oracle.replay_sums(flat, paths, OFFSET, 42, threads=1)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-12
 
@@ -100,7 +100,7 @@ def test_tangent_trip_lengths_with_tail(rocm, tapes, seg):
     _, v, g = run_emulated(flat, opts, 64, rocm=rocm)
     ov, _ = oracle.replay_paths(flat, 64, OFFSET, 42, threads=1)
     assert_values_match(v, ov, rocm.lower(flat, opts))
-    check_per_path(v, g, flat, 64, OFFSET, 42, min_strict=0.5)
+    check_per_path(v, g, flat, 64, OFFSET, 42, min_strict=STRICT["C4"])
 
 
 def test_unrolled_straight_line_matches(rocm, tapes):
@@ -110,7 +110,7 @@ def test_unrolled_straight_line_matches(rocm, tapes):
     assert np.array_equal(v, ov) and np.array_equal(g, og)
     _, v, g = run_emulated(equity_tape_flat, rocm.options("fp64", roll=-1, libm=1, mode=2), 64, rocm=rocm)
     assert np.array_equal(v, ov)
-    check_per_path(v, g, flat, 64, OFFSET, 42)
+    check_per_path(v, g, flat, 64, OFFSET, 42, min_strict=STRICT["C2"])
 
 
 def test_price_only_and_moved_inputs(rocm, tapes):
@@ -128,7 +128,7 @@ def test_emulated_own_math_within_1e12(rocm, tapes, name, paths, mode):
     """The skeleton's own log/sqrt/sincos keep paths within the per-path bar."""
     flat = tapes[name]
     _, v, g = run_emulated(flat, rocm.options("fp64", mode=mode), paths, rocm=rocm)
-    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
+    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=STRICT[name])
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -154,7 +154,7 @@ def test_lookback_and_digital_tapes(nt, rocm):
         opts = rocm.options("fp64", libm=1, mode=2)
         _, v, g = run_emulated(flat, opts, 96, rocm=rocm)
         assert_values_match(v, ov, rocm.lower(flat, opts))
-        check_per_path(v, g, flat, 96, OFFSET, 42, min_strict=0.5)
+        check_per_path(v, g, flat, 96, OFFSET, 42, min_strict=0.95)  # measured 0.958 on these tapes
 
 
 def test_loop_plan_of_the_workloads(rocm, tapes):
@@ -292,7 +292,7 @@ def test_markets_share_draws_and_match_single_market_bit_for_bit(rocm, tapes, na
     src = rocm.lower(flat, rocm.options("fp64", markets=3))
     # the fast pass draws once per path, as a single-market kernel with the same trip length does
     one = rocm.lower(flat, rocm.options("fp64", mode=2, seg_len=int(tape_plan(src)["seg"])))
-    fast = lambda text: text.split("if (nt_slow")[0].count("nt_normal_pair(")
+    fast = lambda text: text.split("void nt_replay_slow(")[0].count("nt_normal_pair(")  # the replay kernel alone
     assert fast(src) == fast(one) > 0
     k = emu.EmulatedKernel(src, len(x0), 0)
     sums, v, g = k.run(sets, paths, OFFSET, 42, grid=3, block=64, markets=3)
@@ -382,7 +382,9 @@ def test_multiplicative_carries_only_where_they_pay(nt, rocm, tapes):
     the smoothed barrier test through scalings, and the survival product, a
     carry times 1 / (1 + e)) take G sigma. A carry multiplied by another
     value with a tangent keeps the product rule (below)."""
-    gs = {k: rocm.lower(tapes[k], rocm.options("fp32", mode=2)).count("real gs") for k in ("C2", "C3", "C4", "C5")}
+    def carries(src):  # distinct G-form carries (the re-evaluation pass declares its own copies)
+        return len(set(re.findall(r"real (gs\d+) ", src)))
+    gs = {k: carries(rocm.lower(tapes[k], rocm.options("fp32", mode=2))) for k in ("C2", "C3", "C4", "C5")}
     assert gs == {"C2": 1, "C3": 2, "C4": 1, "C5": 16}
 
     def body(rec):
@@ -394,7 +396,7 @@ def test_multiplicative_carries_only_where_they_pay(nt, rocm, tapes):
             acc = acc.add(s.mul(vol))  # a product with a value that has a tangent for sigma
         rec.output(acc)
     flat = nt.AadRecorder.record(body).flat()
-    assert rocm.lower(flat, rocm.options("fp64", mode=2)).count("real gs") == 0
+    assert carries(rocm.lower(flat, rocm.options("fp64", mode=2))) == 0
 
 
 @pytest.mark.parametrize("name,paths", [("C2", 300), ("C3", 200), ("C4", 100), ("C5", 30)])
@@ -413,7 +415,7 @@ def test_loop_tangents_over_parameters_or_inputs(rocm, tapes, name, paths):
         assert tape_plan(src)["basis"] == ("inputs" if basis == 1 else "params")
         _, v, g = run_emulated(flat, opts, paths, rocm=rocm)
         assert_values_match(v, ov, src)
-        check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.5 if name == "C4" else 0.99)
+        check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=STRICT[name])
         grads[basis] = g
     assert rel_err(grads[2], grads[1]) <= 1e-12
 
@@ -483,7 +485,7 @@ def test_exponent_fused_only_for_a_carry_kept_as_g(nt, rocm, tapes):
     src = rocm.lower(flat, rocm.options("fp64", mode=2))
     assert not fused.search(src)
     _, v, g = run_emulated(flat, rocm.options("fp64", mode=2), 256, seed=3, rocm=rocm)
-    check_per_path(v, g, flat, 256, OFFSET, 3)
+    check_per_path(v, g, flat, 256, OFFSET, 3, min_strict=0.99)  # measured 0.996
 
 
 def test_parameter_basis_on_assorted_tapes(nt, rocm):
@@ -505,7 +507,7 @@ def test_parameter_basis_on_assorted_tapes(nt, rocm):
         ov, _ = oracle.replay_paths(flat, 128, OFFSET, 42, threads=1)
         _, v, g = run_emulated(flat, opts, 128, rocm=rocm)
         assert_values_match(v, ov, src)
-        check_per_path(v, g, flat, 128, OFFSET, 42, min_strict=0.5)
+        check_per_path(v, g, flat, 128, OFFSET, 42, min_strict=0.93)  # measured 0.9375 on these tapes
     flat = two_output_tape(nt).flat()
     src = rocm.lower(flat, rocm.options("fp64", libm=1, basis=2))
     assert "basis=params" in src
@@ -530,3 +532,29 @@ def test_contract_off_emits_no_fused_node_value(tapes, precision):
     assert any(fused.search(line) for line in default.splitlines())
     assert not any(fused.search(line) for line in off.splitlines())
     assert "#pragma clang fp contract(off)" in off
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("precision,libm", [("fp64", 0), ("fp64", 1), ("fp32", 0)])
+def test_saturating_indicator_follows_the_zero_adjoint_rule(nt, rocm, precision, libm, mode):
+    """The Merton jump tape's smoothed indicator 1 / (1 + exp(-(lambda dt - u) /
+    2e-4)) saturates on most steps: exp overflows to infinity and the
+    indicator is exactly 0. The oracle never multiplies by a zero adjoint
+    (ScalarReplay.java:134-136), so no derivative flows back through the
+    overflowed exponential; IEEE arithmetic gives 0 x inf = NaN there in both
+    derivative modes. Such paths go to the exception kernel, which keeps the
+    oracle's rule: per path within the bar (fp64), the sums within 1e-5 of the
+    fp32 oracle's (fp32), no NaN anywhere."""
+    from conftest import merton_call_tape
+    m = dict(spot=100.0, strike=100.0, vol=0.18, rate=0.03, maturity=1.0, jumpIntensity=0.75, jumpMean=-0.05,
+             jumpVol=0.15)
+    flat = merton_call_tape(nt, m, steps=32).flat()
+    src = rocm.lower(flat, rocm.options(precision, mode=mode, libm=libm))
+    assert "void nt_replay_slow(" in src
+    sums, v, g = run_emulated(flat, rocm.options(precision, mode=mode, libm=libm), 256, rocm=rocm)
+    assert np.all(np.isfinite(sums)) and np.all(np.isfinite(g))
+    if precision == "fp64":
+        check_per_path(v, g, flat, 256, OFFSET, 42, min_strict=0.98)  # measured 0.988
+    else:
+        ref = oracle.replay_sums(flat, 256, OFFSET, 42, f32=True)
+        assert rel_err(sums, ref, floor=1.0) <= 1e-5

@@ -283,3 +283,96 @@ def test_path_ranges_wrap_modulo_two_to_the_64(tapes):
         head = oracle.replay_sums(t, 1500, 2**64 - 1500, 11, threads=threads)
         tail = oracle.replay_sums(t, 2500, 0, 11, threads=threads)
         assert np.allclose(whole, head + tail, rtol=1e-12, atol=0.0)
+
+
+# ---- standard error: AadTotals.toResult against the per-path rows -----------------------
+
+@pytest.mark.parametrize("name,paths", [("C1", 4000), ("C2", 3000), ("C3", 2000), ("C4", 800)])
+def test_sums_and_stderr_match_the_per_path_rows(tapes, name, paths):
+    """The raw sums are the sums of the per-path rows (sum y, sum y^2, sum of
+    each adjoint) and the standard error of AadTotals.toResult
+    (AadTotals.java:68-89), sqrt(max(0, (sum y^2 - n ybar^2) / (n - 1)) / n), is
+    the sample standard deviation of the rows over sqrt(n): a wrong square, a
+    missing root or n in place of n - 1 fails. Both the Python and the C
+    restatement are checked."""
+    t = tapes[name]
+    seed = 7 if name == "C4" else 42
+    sums = oracle.replay_sums(t, paths, 0, seed)
+    v, g = oracle.replay_paths(t, paths, 0, seed)
+    assert sums[0] == pytest.approx(v.sum(), rel=1e-12)
+    assert sums[1] == pytest.approx(np.sum(v * v), rel=1e-12)
+    assert np.allclose(sums[2:], g.sum(axis=0), rtol=1e-12, atol=1e-12 * np.abs(g).sum())
+    want = np.std(v, ddof=1) / np.sqrt(paths)
+    assert want > 0
+    for res in (oracle.to_result(sums, paths), oracle.to_result_c(sums, paths, g.shape[1])):
+        assert res["stderr"] == pytest.approx(want, rel=1e-10)
+        assert res["price"] == pytest.approx(v.mean(), rel=1e-12)
+        assert np.allclose(res["gradient"], g.mean(axis=0), rtol=1e-12, atol=1e-14)
+    # one scenario has no standard error
+    assert np.isnan(oracle.to_result(sums, 1)["stderr"]) and np.isnan(oracle.to_result_c(sums, 1, 0)["stderr"])
+
+
+# ---- Merton jump-diffusion: uniforms against a closed form ------------------------------
+
+MERTON = dict(spot=100.0, strike=100.0, vol=0.18, rate=0.03, maturity=1.0, jumpIntensity=0.75, jumpMean=-0.05,
+              jumpVol=0.15)
+
+
+def test_merton_series_reduces_to_black_scholes():
+    """The Poisson series with no jumps is the Black-Scholes call: 9.4134 for
+    S = K = 100, sigma 0.2, r 0.03, T 1 (d1 = 0.25, d2 = 0.05)."""
+    from conftest import merton_series_call
+    from math import erf, exp, log, sqrt
+    ncdf = lambda x: 0.5 * (1.0 + erf(x / sqrt(2.0)))
+    d1 = (log(1.0) + (0.03 + 0.02) * 1.0) / 0.2
+    bs = 100.0 * ncdf(d1) - 100.0 * exp(-0.03) * ncdf(d1 - 0.2)
+    assert merton_series_call(100, 100, 1.0, 0.03, 0.2, 0.0, -0.1, 0.2) == pytest.approx(bs, rel=1e-14)
+    assert bs == pytest.approx(9.4134, abs=1e-4)
+
+
+def test_merton_monte_carlo_converges_to_the_poisson_series(nt):
+    """JumpModelsTest.mertonMonteCarloConvergesToThePoissonSeries
+    (JumpModelsTest.java:46-53; docs/examples/jump-models.md:48-50): the Merton
+    tape (a uniform per step decides the jump) within 1.5% of the exact
+    Poisson-series price. A uniform that reused a normal's Philox block (a
+    missing 2^30 tag) would tie the jump to the largest diffusion moves and
+    fail it."""
+    from conftest import merton_call_tape, merton_series_call
+    flat = merton_call_tape(nt, MERTON).flat()
+    paths = 400_000
+    res = oracle.to_result(oracle.replay_sums(flat, paths, 0, 42), paths)
+    exact = merton_series_call(100, 100, 1.0, 0.03, 0.18, 0.75, -0.05, 0.15)
+    assert abs(res["price"] - exact) <= 0.015 * exact, (res["price"], exact)
+
+
+def test_merton_without_jumps_is_black_scholes(nt):
+    """JumpModelsTest.mertonCollapsesToBlackScholesWhenIntensityIsZero
+    (JumpModelsTest.java:56-62): intensity 0 gives the Black-Scholes call
+    within 2%."""
+    from conftest import merton_call_tape, merton_series_call
+    m = dict(MERTON, vol=0.2, jumpIntensity=0.0, jumpMean=-0.1, jumpVol=0.2)
+    flat = merton_call_tape(nt, m, steps=64).flat()
+    res = oracle.to_result(oracle.replay_sums(flat, 200_000, 0, 7), 200_000)
+    bs = merton_series_call(100, 100, 1.0, 0.03, 0.2, 0.0, -0.1, 0.2)
+    assert abs(res["price"] - bs) <= 0.02 * bs, (res["price"], bs)
+
+
+def test_merton_adjoint_spot_delta_matches_bump(nt):
+    """JumpModelsTest.mertonAdjointSpotDeltaMatchesBump (JumpModelsTest.java:
+    75-87): the adjoint spot delta against a central bump of 1.0 with common
+    random numbers, within 5e-3 (1 + |bump|); the jumpMean adjoint within 8%."""
+    from conftest import merton_call_tape
+    m = dict(MERTON, jumpIntensity=0.8)
+    flat = merton_call_tape(nt, m, steps=64).flat()
+    paths, seed = 100_000, 42
+    base = np.array([m[f] for f in ("spot", "strike", "vol", "rate", "maturity", "jumpIntensity", "jumpMean",
+                                    "jumpVol")])
+    adj = oracle.to_result(oracle.replay_sums(flat, paths, 0, seed, inputs=base), paths)["gradient"]
+    for j, h, tol in ((0, 1.0, 5e-3), (6, 5e-3, 0.08)):
+        up, dn = base.copy(), base.copy()
+        up[j] += h
+        dn[j] -= h
+        pu = oracle.replay_sums(flat, paths, 0, seed, inputs=up, adjoints=False)[0] / paths
+        pd = oracle.replay_sums(flat, paths, 0, seed, inputs=dn, adjoints=False)[0] / paths
+        bump = (pu - pd) / (2 * h)
+        assert abs(adj[j] - bump) <= tol * (1 + abs(bump)), (j, adj[j], bump)
