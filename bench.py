@@ -42,6 +42,8 @@ REFERENCE_ROCM_FP64 = 2.16e6
 def workload_tape(name: str):
     from nablatensor_amd import workloads
 
+    if name == "asian_weekdays":
+        return workloads.schedule_tapes()[name].flat()
     return workloads.workload_tapes()[name].flat()
 
 
@@ -202,7 +204,8 @@ def other_workload(rocm, args) -> int:
 # The other benchmark configurations, reported beside the headline in the default run: the engine's default
 # plan, each at the scenarios per dispatch its configuration names, fewer timed steps (these are
 # reports, not the headline).
-OTHER_WORKLOADS = (("C1", "fp64"), ("C3", "fp32"), ("C3", "fp64"), ("C4", "fp64"), ("C5", "fp32"), ("C5", "fp64"))
+OTHER_WORKLOADS = (("C1", "fp64"), ("C3", "fp32"), ("C3", "fp64"), ("C4", "fp64"), ("C5", "fp32"), ("C5", "fp64"),
+                   ("asian_weekdays", "fp64"))
 
 
 def other_workloads(rocm, steps: int = 5, warmup: int = 1, ramp: float = 0.2) -> dict:
@@ -325,7 +328,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",
                     help="skip the other benchmark configurations reported beside the headline")
-    ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5"],
+    ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "asian_weekdays"],
                     help="C2 (default) prints the headline line; the others print the same fields for that workload")
     ap.add_argument("--precision", choices=["fp64", "fp32"], default=None,
                     help="run one workload at one precision and print its line (default: the workload's own; "

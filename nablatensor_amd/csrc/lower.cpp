@@ -122,12 +122,13 @@ bool draw_repeats(const TapeIR& t, int i, int k, int D) {
   return t.simple_draws ? t.a[k] - t.a[i] == D : t.a[k] > t.a[i];
 }
 
-// Node k = i + P repeats node i: same op and literal, draw ordinal advanced,
-// each operand either shifted by P (same iteration / carried) or unchanged (invariant).
-bool repeats(const TapeIR& t, int i, int k, int P, int D) {
+// Node k = i + P repeats node i: same op and literal (any literal when `lit`),
+// draw ordinal advanced, each operand either shifted by P (same iteration /
+// carried) or unchanged (invariant).
+bool repeats(const TapeIR& t, int i, int k, int P, int D, bool lit) {
   const int op = t.op[i];
   if (op != t.op[k] || op == NT_OP_INPUT) return false;
-  if (op == NT_OP_CONST) return bits(t.c[i]) == bits(t.c[k]);
+  if (op == NT_OP_CONST) return lit || bits(t.c[i]) == bits(t.c[k]);
   if (is_draw(op)) return draw_repeats(t, i, k, D);
   const int ar = arity(op);
   if (ar >= 1 && !(t.a[k] == t.a[i] + P || t.a[k] == t.a[i])) return false;
@@ -138,13 +139,13 @@ bool repeats(const TapeIR& t, int i, int k, int P, int D) {
 // Iteration [s0, s0+P) followed by [s1 = s0+P, ...): like repeats(), except a
 // carried operand of the later iteration may come from any node before s0 (the
 // carry's initial value).
-bool extends(const TapeIR& t, int s0, int P, int D) {
+bool extends(const TapeIR& t, int s0, int P, int D, bool lit) {
   const int s1 = s0 + P;
   for (int j = 0; j < P; ++j) {
     const int i = s0 + j, k = s1 + j;
     const int op = t.op[i];
     if (op != t.op[k] || op == NT_OP_INPUT) return false;
-    if (op == NT_OP_CONST) { if (bits(t.c[i]) != bits(t.c[k])) return false; continue; }
+    if (op == NT_OP_CONST) { if (!lit && bits(t.c[i]) != bits(t.c[k])) return false; continue; }
     if (is_draw(op)) { if (!draw_repeats(t, i, k, D)) return false; continue; }
     const int ar = arity(op);
     for (int slot = 0; slot < ar; ++slot) {
@@ -160,7 +161,7 @@ bool extends(const TapeIR& t, int s0, int P, int D) {
 
 enum { V_OK = 0, V_ITER0 = 1, V_EPI = 2, V_FAIL = 3 };
 
-int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
+int verify(const TapeIR& t, int s, int P, int iters, int D, bool lit, LoopPlan& L) {
   const int e = s + P * iters;
   L = LoopPlan();
   L.start = s; L.period = P; L.iters = iters; L.draws = D;
@@ -213,7 +214,7 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
       const int i = s + it * P + j;
       const int op = t.op[i];
       if (op != t.op[s1 + j]) return fail;
-      if (op == NT_OP_CONST && bits(t.c[i]) != bits(t.c[s + j])) return fail;
+      if (op == NT_OP_CONST && !lit && bits(t.c[i]) != bits(t.c[s + j])) return fail;
       if (op == NT_OP_INPUT) return fail;
       if (is_draw(op) && (t.b[i] != t.b[s + j] || t.a[i] != L.rand_base[j] + it * L.rand_step[j])) return fail;
       // one body serves every iteration, so activity must not change along the loop
@@ -256,13 +257,25 @@ int verify(const TapeIR& t, int s, int P, int iters, int D, LoopPlan& L) {
       L.is_liveout[out - last] = 1;
     }
   }
+  if (lit) {
+    L.lit_table.assign(P, 0);
+    L.lit_values.assign(P, {});
+    for (int j = 0; j < P; ++j) {
+      if (t.op[s + j] != NT_OP_CONST) continue;
+      bool same = true;
+      for (int it = 1; it < iters && same; ++it) same = bits(t.c[s + it * P + j]) == bits(t.c[s + j]);
+      if (same) continue;
+      L.lit_table[j] = 1;
+      for (int it = 0; it < iters; ++it) L.lit_values[j].push_back(t.c[s + it * P + j]);
+    }
+  }
   L.found = true;
   return V_OK;
 }
 
 }  // namespace
 
-LoopPlan detect_loop(const TapeIR& t) {
+LoopPlan detect_loop(const TapeIR& t, bool lit) {
   std::vector<int> rp;
   for (int i = 0; i < t.n; ++i) {
     if (is_draw(t.op[i])) rp.push_back(i);
@@ -284,7 +297,7 @@ LoopPlan detect_loop(const TapeIR& t) {
     const int P = cd.first, D = cd.second;
     int runStart = -1;
     for (int i = 0; i + P <= t.n; ++i) {
-      const bool ok = i + P < t.n && repeats(t, i, i + P, P, D);
+      const bool ok = i + P < t.n && repeats(t, i, i + P, P, D, lit);
       if (ok && runStart < 0) runStart = i;
       if (!ok && runStart >= 0) {
         const int x = runStart, y = i;
@@ -301,10 +314,10 @@ LoopPlan detect_loop(const TapeIR& t) {
     if (is_draw(t.op[bestX + j])) { s = bestX + j; break; }
   }
   int iters = (bestY + P - s) / P;
-  while (s - P >= 0 && extends(t, s - P, P, D)) { s -= P; ++iters; }
+  while (s - P >= 0 && extends(t, s - P, P, D, lit)) { s -= P; ++iters; }
   LoopPlan L;
   for (int attempt = 0; attempt < 8 && iters >= 4; ++attempt) {
-    const int r = verify(t, s, P, iters, D, L);
+    const int r = verify(t, s, P, iters, D, lit, L);
     if (r == V_OK) break;
     if (r == V_EPI) { --iters; continue; }
     if (r == V_ITER0) { s += P; --iters; continue; }
@@ -312,6 +325,63 @@ LoopPlan detect_loop(const TapeIR& t) {
   }
   if (!L.found || iters < 4 || static_cast<long>(iters) * P < 32) return none;
   return L;
+}
+
+TapeIR sink_invariants(const TapeIR& t) {
+  const int n = t.n;
+  std::vector<uint8_t> drawn(n, 0), output(n, 0);
+  for (int out : t.outputs) output[out] = 1;
+  for (int i = 0; i < n; ++i) {
+    const int op = t.op[i];
+    const int ar = arity(op);
+    drawn[i] = is_draw(op) || (ar >= 1 && drawn[t.a[i]]) || (ar >= 2 && drawn[t.b[i]]);
+  }
+  auto deferred = [&](int i) { return !drawn[i] && t.op[i] != NT_OP_INPUT && !output[i]; };
+  std::vector<int> order;
+  order.reserve(n);
+  std::vector<uint8_t> placed(n, 0);
+  std::vector<std::pair<int, int>> stack;  // (node, operands visited)
+  auto place = [&](int root) {
+    if (placed[root]) return;
+    stack.push_back({root, 0});
+    while (!stack.empty()) {
+      auto& top = stack.back();
+      const int i = top.first;
+      const int ar = arity(t.op[i]);
+      if (top.second < ar) {
+        const int x = top.second == 0 ? t.a[i] : t.b[i];
+        ++top.second;
+        if (!placed[x]) stack.push_back({x, 0});
+        continue;
+      }
+      stack.pop_back();
+      if (!placed[i]) {
+        placed[i] = 1;
+        order.push_back(i);
+      }
+    }
+  };
+  for (int i = 0; i < n; ++i) {
+    if (!deferred(i)) place(i);
+  }
+  for (int i = 0; i < n; ++i) place(i);  // what nothing else reads
+  std::vector<int> at(n);
+  for (int k = 0; k < n; ++k) at[order[k]] = k;
+  TapeIR r = t;
+  for (int k = 0; k < n; ++k) {
+    const int i = order[k];
+    const int op = t.op[i];
+    const int ar = arity(op);
+    r.op[k] = op;
+    r.c[k] = t.c[i];
+    r.a[k] = ar >= 1 ? at[t.a[i]] : t.a[i];
+    r.b[k] = ar >= 2 ? at[t.b[i]] : t.b[i];
+    r.active[k] = t.active[i];
+  }
+  for (int j = 0; j < t.n_in; ++j) r.input_node[j] = at[t.input_node[j]];
+  for (size_t o = 0; o < t.outputs.size(); ++o) r.outputs[o] = at[t.outputs[o]];
+  r.output = r.outputs[0];
+  return r;
 }
 
 // ---- plan ----------------------------------------------------------------------
@@ -323,7 +393,7 @@ double fwd_cost(int op, bool f32);
 double store_cost(bool f32);
 }  // namespace
 
-int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err) {
+int make_plan(TapeIR& t, const nt_options* opt, Plan& p, std::string& err) {
   nt_options o{};
   if (opt) o = *opt;
   p = Plan();
@@ -356,7 +426,22 @@ int make_plan(const TapeIR& t, const nt_options* opt, Plan& p, std::string& err)
     err = "the reverse sweep follows one output; a multi-output tape takes tangent mode";
     return NT_E_UNSUPPORTED;
   }
-  if (o.roll >= 0) p.loop = detect_loop(t);
+  if (o.roll >= 0) {
+    p.loop = detect_loop(t);
+    const long cover = p.loop.found ? static_cast<long>(p.loop.period) * p.loop.iters : 0;
+    if (2 * cover < t.n) {
+      // No exactly repeating step covers most of the tape: the step's schedule
+      // (per-step fractions, drifts, volatilities) may have been recorded up
+      // front. Moved next to the steps that read it, with per-step literals
+      // read from a table, it can make the step repeat.
+      TapeIR sunk = sink_invariants(t);
+      LoopPlan L = detect_loop(sunk, true);
+      if (L.found && static_cast<long>(L.period) * L.iters > cover) {
+        t = std::move(sunk);
+        p.loop = std::move(L);
+      }
+    }
+  }
   if (p.loop.found) {
     const int rc = plan_reverse_loop(t, o, p, err);
     if (rc != NT_OK) return rc;
@@ -1026,7 +1111,17 @@ class Emitter {
   std::string sqrt_q_;  // tangent factor of the SQRT just emitted, if nt_sqrt_q made it
   // A DIV whose numerator is the constant 1 takes nt_recip in the same
   // kernels; its value is then its own tangent factor 1/b.
-  bool is_one(int node) const { return t_.op[node] == NT_OP_CONST && t_.c[node] == 1.0; }
+  bool is_one(int node) const {
+    if (L_.found && node >= L_.start && node < L_.end() && L_.table_lit((node - L_.start) % L_.period)) return false;
+    return t_.op[node] == NT_OP_CONST && t_.c[node] == 1.0;
+  }
+  // Literal of loop position j in iteration u of the trip: from the position's
+  // table when it changes along the loop (a wave-uniform index: one scalar load).
+  std::string body_expr(int j, int u, int op, const std::string& x, const std::string& y) const {
+    const int i = L_.start + j;
+    if (op == NT_OP_CONST && L_.table_lit(j)) return "nt_lit" + std::to_string(j) + "[it0 + " + std::to_string(u) + "u]";
+    return expr(op, x, y, t_.c[i], t_.a[i]);
+  }
   bool recip_ = false;  // the DIV just emitted is a nt_recip
   void preamble();
   void kernel_head(bool slow);
@@ -1197,7 +1292,7 @@ void Emitter::segment(int U, const std::string& sg, bool forward) {
         const int ar = arity(op);
         const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], !forward) : "";
         const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], !forward) : "";
-        o_ << ind << "const real " << name << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+        o_ << ind << "const real " << name << " = " << body_expr(j, u, op, x, y) << ";\n";
       }
       if (forward && p_.adjoints && p_.stored[j]) {
         o_ << ind << "scratch[" << slot << "] = " << name << ";\n";
@@ -1534,7 +1629,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
         exp_active_ = act;
         const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], false) : "";
         const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], false) : "";
-        std::string val = expr(op, x, y, t_.c[i], t_.a[i]);
+        std::string val = body_expr(j, u, op, x, y);
         if (op == NT_OP_EXP && fold_[j].on) {
           const Exp2Fold& f = fold_[j];
           const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
@@ -1934,6 +2029,12 @@ void Emitter::preamble() {
   o_ << "#include \"nt_skeleton.h\"\n";
   o_ << "typedef " << (f32_ ? "float" : "double") << " real;\n";
   if (fallback()) o_ << "#define NT_HAS_SLOW 1\n";
+  for (int j = 0; loop && j < L_.period; ++j) {
+    if (!L_.table_lit(j)) continue;
+    o_ << "__constant__ real nt_lit" << j << "[" << L_.iters << "] = {";
+    for (int it = 0; it < L_.iters; ++it) o_ << (it ? ", " : "") << lit(L_.lit_values[j][it]);
+    o_ << "};\n";
+  }
 }
 
 // Signature and prologue of the replay kernel (nt_replay) or of the exception

@@ -59,7 +59,13 @@ struct LoopPlan {
   std::vector<int> carry_init;        // init node of a carried position, -1 otherwise
   std::vector<uint8_t> is_carry;      // read as carry-in by the next iteration
   std::vector<uint8_t> is_liveout;    // read by the epilogue from the last iteration
+  // CONST positions whose literal changes from one iteration to the next (a
+  // per-step year fraction): lit_table[j] set, lit_values[j][it] the literal
+  // of iteration it. Only a loop detected with literal tables has them.
+  std::vector<uint8_t> lit_table;
+  std::vector<std::vector<double>> lit_values;
   int end() const { return start + period * iters; }
+  bool table_lit(int pos) const { return pos >= 0 && pos < static_cast<int>(lit_table.size()) && lit_table[pos]; }
 };
 
 struct Plan {
@@ -92,8 +98,18 @@ struct Plan {
 
 // Returns NT_OK or an NT_E_* code with a message in err.
 int build_ir(const nt_tape* tape, TapeIR& ir, std::string& err);
-LoopPlan detect_loop(const TapeIR& ir);
-int make_plan(const TapeIR& ir, const nt_options* opt, Plan& plan, std::string& err);
+// `lit_tables`: a CONST of the step body may take another literal in each
+// iteration (kept as a per-iteration table).
+LoopPlan detect_loop(const TapeIR& ir, bool lit_tables = false);
+// The same tape with every node that depends on no draw (and is neither an
+// INPUT nor an output) moved to just before its first use, operands first;
+// draws and the nodes that depend on them keep their order. A step schedule
+// recorded up front (the per-step drift and volatility of a non-uniform time
+// grid, GbmPath.java:49-66) then sits inside the step it feeds.
+TapeIR sink_invariants(const TapeIR& ir);
+// May replace `ir` by its sink_invariants form when only that form has a step
+// loop covering most of the tape.
+int make_plan(TapeIR& ir, const nt_options* opt, Plan& plan, std::string& err);
 std::string emit_source(const TapeIR& ir, const Plan& plan);
 
 }  // namespace ntl

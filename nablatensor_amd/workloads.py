@@ -25,6 +25,8 @@ DESCRIPTIONS = {
     "C4": ("Heston-Asian call, 504 full-truncation Euler steps, value + 8 adjoints", 10_000_000, 7, "fp64"),
     "C5": ("Worst-of call on 16 correlated GBM assets, 252 steps, value + 33 adjoints, 1e6 scenarios per launch",
            1_000_000, 42, "fp32"),
+    "asian_weekdays": ("Asian call, GBM, 252 weekday fixings (TimeGrid.of, non-uniform), ATM 1y, value + 5 Greeks",
+                       2_000_000, 42, "fp64"),
 }
 
 
@@ -48,3 +50,26 @@ def workload_tapes(steps_c4: int = 504, steps_c5: int = 252) -> dict:
     basket = nt.WorstOfBasket.market([100.0] * 16, fx["sigma"], 0.03)
     out["C5"] = nt.record(nt.WorstOfBasket.call(fx["corr"], 100.0, 1.0, steps_c5), basket)
     return out
+
+
+def weekday_fixings(n: int = 252) -> list[float]:
+    """n fixing times in years on weekdays of the calendar: one day apart, three
+    days after every fifth fixing (a weekend), day 1 first."""
+    days, d = [], 0
+    for i in range(n):
+        d += 3 if (i % 5 == 0 and i > 0) else 1
+        days.append(d / 365.0)
+    return days
+
+
+def schedule_tapes() -> dict:
+    """Tapes whose step schedule is recorded up front rather than repeated
+    exactly: the Asian call on TimeGrid.of 252 weekday fixings (GbmPath
+    records a drift and a diffusion node per step for a non-uniform grid,
+    GbmPath.java:49-66, and TimeGrid.of's fractions differ in their last bits
+    even where the gaps are equal)."""
+    from . import _host as nt
+
+    grid = nt.TimeGrid.of(weekday_fixings())
+    return {"asian_weekdays": nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), grid)}
+

@@ -56,7 +56,7 @@ def test_headline_line_has_the_contract_fields(patched, monkeypatch, capsys):
     assert out["reverse"]["kernel"]["mode"] == "reverse"
     assert out["fp32"]["value"] > 0
     w = out["workloads"]
-    assert set(w) == {"C1_fp64", "C3_fp32", "C3_fp64", "C4_fp64", "C5_fp32", "C5_fp64"}
+    assert set(w) == {"C1_fp64", "C3_fp32", "C3_fp64", "C4_fp64", "C5_fp32", "C5_fp64", "asian_weekdays_fp64"}
     assert all(r["value"] > 0 and 0 < r["frac"] < 1 for r in w.values())
 
 

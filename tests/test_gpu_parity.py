@@ -322,3 +322,22 @@ def test_merton_jump_tape_converges_to_the_poisson_series(rocm, nt):
     exact = merton_series_call(100, 100, 1.0, 0.03, 0.18, 0.75, -0.05, 0.15)
     print(f"price {price:.6f} series {exact:.6f} rel {(price - exact) / exact:.2e}")
     assert abs(price - exact) <= 0.015 * exact
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_step_schedule_recorded_up_front_on_device(rocm, mode):
+    """The Asian call on TimeGrid.of 252 weekday fixings (its per-step drift
+    and diffusion recorded before the first step, GbmPath.java:61-66) runs as
+    a rolled loop with a per-step fraction table: no scratch, per path within
+    the bar, sums within 1e-10 of the oracle's."""
+    from nablatensor_amd import workloads
+    flat = workloads.schedule_tapes()["asian_weekdays"].flat()
+    print(f"case asian_weekdays mode={mode}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+        info = x.info()
+        assert info["scratch_bytes"] == 0 and info["loop_period"] == 11
+        v, g = x.replay_paths(2048, OFFSET, 42)
+        sums, _ = x.replay(200_000, 0, 42)
+    print(check_per_path(v, g, flat, 2048, OFFSET, 42, min_strict=0.94))  # measured 0.943
+    ref = oracle.replay_sums(flat, 200_000, 0, 42)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-10

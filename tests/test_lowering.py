@@ -558,3 +558,51 @@ def test_saturating_indicator_follows_the_zero_adjoint_rule(nt, rocm, precision,
     else:
         ref = oracle.replay_sums(flat, 256, OFFSET, 42, f32=True)
         assert rel_err(sums, ref, floor=1.0) <= 1e-5
+
+
+def test_step_schedule_recorded_up_front_rolls(rocm):
+    """An Asian call on TimeGrid.of 252 weekday fixings records every step's
+    drift and diffusion before the first step (GbmPath.java:61-66), with
+    year fractions that differ in their last bits: moved next to the steps
+    that read them, with the fractions read from a per-step table, the step
+    repeats (11 nodes x 251 steps; the first step carries the shared
+    half-variance and stays straight-line). Both modes compile in seconds
+    with no scratch, where the straight-line kernel took two minutes of hipRTC
+    and spilled 11-20 KB per lane."""
+    from nablatensor_amd import workloads
+    import time
+    flat = workloads.schedule_tapes()["asian_weekdays"].flat()
+    assert len(flat["op"]) == 2791
+    for precision in ("fp64", "fp32"):
+        for mode in (rocm.NT_MODE_REVERSE, rocm.NT_MODE_TANGENT):
+            t0 = time.time()
+            info = rocm.compile_check(flat, rocm.options(precision, mode=mode))
+            assert (info["loop_period"], info["loop_iters"]) == (11, 251)
+            assert info["scratch_bytes"] == 0
+            assert time.time() - t0 < 60
+    src = rocm.lower(flat, rocm.options("fp64"))
+    assert src.count("__constant__ real nt_lit") == 1  # the step's year fraction
+
+
+@pytest.mark.parametrize("mode,libm", [(1, 0), (1, 1), (2, 0), (2, 1)])
+def test_step_schedule_per_path_matches_oracle(rocm, mode, libm):
+    """The rolled weekday-fixing Asian against the oracle, per path (the
+    reordered tape accumulates the adjoints of the schedule's shared inputs in
+    another order, so the reverse sweep with libm is within the bar rather
+    than bit-exact)."""
+    from nablatensor_amd import workloads
+    flat = workloads.schedule_tapes()["asian_weekdays"].flat()
+    sums, v, g = run_emulated(flat, rocm.options("fp64", mode=mode, libm=libm), 300, rocm=rocm)
+    ov, _ = oracle.replay_paths(flat, 300, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov) or rel_err(v, ov) <= 1e-12
+    check_per_path(v, g, flat, 300, OFFSET, 42, min_strict=0.95)  # measured 0.953
+    ref = oracle.replay_sums(flat, 300, OFFSET, 42, threads=1)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-12
+
+
+def test_uniform_workloads_keep_their_exact_loops(rocm, tapes):
+    """Only a tape whose exactly repeating step covers less than half of it is
+    reordered: the five workloads keep their plans (their sources are pinned
+    by tests/golden/tape_digests.json), with no literal tables."""
+    for name in ("C2", "C3", "C4", "C5"):
+        assert "nt_lit" not in rocm.lower(tapes[name], rocm.options("fp64"))
