@@ -121,11 +121,18 @@ def check_offline_hipcc(source: str, name: str = "check") -> Path:
     return out
 
 
-def build_mathbench() -> Path:
-    """hipcc build of the building-block microbenchmark (csrc/mathbench.hip)."""
-    out = PKG / "mathbench"
-    _run([str(ROCM / "bin" / "hipcc"), "--offload-arch=gfx950", "-O3", *PACKED_FP32_OFF, "-w",
-          str(CSRC / "mathbench.hip"), "-o", str(out)])
+def build_math_device(force: bool = True) -> Path:
+    """Test driver of the skeleton's own fp64 math on the device
+    (tests/device_math/nt_math_device.hip -> libnt_math_device.so, loaded by
+    tests/test_gpu_math.py)."""
+    src = ROOT / "tests" / "device_math" / "nt_math_device.hip"
+    out = src.parent / "libnt_math_device.so"
+    deps = [src, CSRC / "nt_skeleton.h", CSRC / "nt_math_tables.h"]
+    if not force and _newer(out, deps):
+        return out
+    _run([str(ROCM / "bin" / "hipcc"), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+          *PACKED_FP32_OFF, f"-I{CSRC}", str(src), "-o", str(out) + ".tmp"])
+    os.replace(str(out) + ".tmp", out)
     return out
 
 
@@ -133,7 +140,7 @@ def build_all(force: bool = True) -> None:
     build_engine(force)
     build_host(force)
     build_oracle()
-    build_mathbench()
+    build_math_device(force)
 
 
 if __name__ == "__main__":

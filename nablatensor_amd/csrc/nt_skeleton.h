@@ -250,11 +250,11 @@ __device__ __forceinline__ void nt_sincos_2pi_u32(nt_u32 c, double& s, double& c
 // sqrt(a) and the tangent factor 1/(2 sqrt(a)) of a SQRT node, for a = +-0 or
 // a positive normal, where a correctly rounded sqrt and a division take two
 // dozen instructions. nt_sqrt_pos's coupled Newton step and residual
-// correction give the root; the factor after that step is low by 1.5 e^2 (e
-// the seed's relative error), the same sign every time, so a second step on
-// it (against the corrected root) brings it to full precision: in a carried
-// tangent (a variance process) a one-sided error would compound over the
-// steps. The seed is taken at max(a, 2^-1022), so a = +-0 gives sqrt = a and
+// correction give the root s; the factor after that step is low by 1.5 e^2
+// (e the seed's relative error, about 2^-24 for v_rsq_f64), the same sign
+// every time, so a Newton step for h = 1/(2 s), h + 2 h (1/2 - s h), brings it
+// to full precision (its error squares): in a carried tangent (a variance
+// process) a one-sided error would compound over the steps. The seed is taken at max(a, 2^-1022), so a = +-0 gives sqrt = a and
 // a large finite factor (the derivative is infinite there; a zero tangent
 // stays zero, as with the capped factor of the libm path). Any other
 // argument (negative, subnormal, infinite, NaN) sets `bad`, and the caller
@@ -268,7 +268,7 @@ __device__ __forceinline__ double nt_sqrt_q(double a, double& q, bool& bad) {
   g = fma(g, r, g);
   h = fma(h, r, h);
   const double s = fma(fma(-g, g, a), h, g);
-  q = fma(h, fma(-s, h, 0.5), h);
+  q = fma(h + h, fma(-s, h, 0.5), h);
   return s;
 }
 #else

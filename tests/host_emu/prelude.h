@@ -30,10 +30,21 @@ inline bool nt_zero_or_pos_normal(double x) {
   const int c = std::fpclassify(x);
   return c == FP_ZERO || (c == FP_NORMAL && !std::signbit(x));
 }
-// correctly rounded stand-in for the device's reciprocal-square-root seed
-inline double nt_rsq(double x) { return 1.0 / std::sqrt(x); }
-// correctly rounded stand-in for the device's reciprocal seed
-inline double nt_rcp(double x) { return 1.0 / x; }
+// Stand-ins for the device's seed instructions v_rsq_f64 and v_rcp_f64: the
+// correctly rounded value with a relative error of up to 2^-22 (the hardware
+// seeds' are near 2^-24), one deterministic pseudo-random error per argument,
+// so the host tests see routines that start from an inexact seed as the
+// device ones do.
+inline double nt_seed_error(double x) {
+  unsigned long long u;
+  std::memcpy(&u, &x, 8);
+  u ^= u >> 33;
+  u *= 0xff51afd7ed558ccdull;
+  u ^= u >> 33;
+  return std::ldexp(static_cast<double>(static_cast<long long>(u >> 11) - (1ll << 52)) / (1ll << 52), -22);
+}
+inline double nt_rsq(double x) { return (1.0 / std::sqrt(x)) * (1.0 + nt_seed_error(x)); }
+inline double nt_rcp(double x) { return (1.0 / x) * (1.0 + nt_seed_error(x)); }
 
 struct nt_emu_dim3 {
   unsigned x = 0, y = 1, z = 1;

@@ -180,3 +180,40 @@ def test_exp_within_one_ulp_and_special_values(lib):
     with np.errstate(over="ignore"):
         want = np.exp(sp[:-1])
     assert np.array_equal(out[:-1], want) and np.isnan(out[-1])
+
+
+# ---- the long double reference of the device accuracy test ------------------------------
+
+def long_double_refs(fx):
+    """numpy long double (64-bit mantissa) values of each routine's exact result
+    on the fixture's arguments, as tests/test_gpu_math.py computes them for 10^6."""
+    ld = np.longdouble
+    c = np.array(fx["neg2log"]["c"], dtype=np.uint64)
+    u = (c.astype(np.float64) + 0.5) * 2.0**-32
+    theta = np.array([float.fromhex(t) for t in fx["sincos"]["theta"]])
+    x = np.array([float.fromhex(v) for v in fx["exp"]["x"]])
+    a = np.array([float.fromhex(v) for v in fx["sqrt"]["a"]])
+    b = np.array([float.fromhex(v) for v in fx["recip"]["b"]])
+    return {"neg2log": -2 * np.log(u.astype(ld)), "sin": np.sin(theta.astype(ld)), "cos": np.cos(theta.astype(ld)),
+            "exp": np.exp(x.astype(ld)), "sqrt": np.sqrt(a.astype(ld)), "half_rsqrt": ld(0.5) / np.sqrt(a.astype(ld)),
+            "recip": ld(1) / b.astype(ld)}
+
+
+def test_long_double_reference_is_within_a_thousandth_of_a_double_ulp():
+    """The device accuracy test measures ulp errors of double results against
+    numpy long double; on the fixture's arguments (tests/golden/math_mpmath.json,
+    mpmath at 40 digits, edge cases included) that reference is within 1e-3 of
+    a double ulp of the exact result, so it resolves errors of 1 ulp to 0.1 %."""
+    import json
+    fx = json.loads((ROOT / "tests" / "golden" / "math_mpmath.json").read_text())
+    refs = long_double_refs(fx)
+    exact = {"neg2log": fx["neg2log"]["value"], "sin": fx["sincos"]["sin"], "cos": fx["sincos"]["cos"],
+             "exp": fx["exp"]["value"], "sqrt": fx["sqrt"]["value"], "half_rsqrt": fx["sqrt"]["half_rsqrt"],
+             "recip": fx["recip"]["value"]}
+    for name, values in exact.items():
+        worst = 0.0
+        for r, v in zip(refs[name], values):
+            e = mp.mpf(v)
+            unit = mp.mpf(2.0**-53) if name in ("sin", "cos") else mp.mpf(float(np.spacing(abs(float(e))) or 5e-324))
+            worst = max(worst, float(abs(mp.mpf(str(r)) - e) / unit))
+        assert worst <= 1e-3, (name, worst)
