@@ -67,7 +67,8 @@ enum {
   NT_CKPT_AUTO = 0,       /* cost model picks one of the below */
   NT_CKPT_RECOMPUTE = 1,  /* carries checkpointed per segment; the reverse recomputes each segment */
   NT_CKPT_STORE_DRAWS = 2,/* draw-derived (inactive) values stored; active values recomputed */
-  NT_CKPT_STORE_ALL = 3   /* every value the reverse reads is stored; nothing recomputed */
+  NT_CKPT_STORE_ALL = 3   /* every value the reverse reads is stored; nothing recomputed (a tape with no rolled
+                             loop: not cut into segments, every forward value kept live) */
 };
 
 /* How the first-order Greeks are propagated. Both give the same derivatives
@@ -86,7 +87,9 @@ typedef struct nt_options {
   int32_t block;            /* threads per block; 0 = 256 */
   int32_t max_blocks;       /* grid cap; 0 = sized from occupancy */
   int32_t checkpoint;       /* NT_CKPT_* */
-  int32_t seg_len;          /* loop iterations per checkpoint segment; 0 = cost model */
+  int32_t seg_len;          /* loop iterations per checkpoint segment; 0 = cost model. For a tape with no rolled
+                               loop swept in reverse: nodes per checkpointed segment (0: about sqrt(nodes), at
+                               least 48, on tapes over 512 nodes, as AadCheckpointPlan.java:95-110) */
   int32_t roll;             /* 1 (default): roll the step loop when one is found; -1: never */
   int32_t contract;         /* FMA contraction of the tape's own products and sums: 0 default (off for fp64, on for
                                fp32, plus the fused exponent of a step's multiplicative carry, whose value is

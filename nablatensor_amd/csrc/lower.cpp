@@ -388,6 +388,8 @@ TapeIR sink_invariants(const TapeIR& t) {
 
 namespace {
 int plan_reverse_loop(const TapeIR& t, const nt_options& o, Plan& p, std::string& err);
+bool wants_line_segments(const TapeIR& t, const nt_options& o, const Plan& p);
+void plan_line_segments(const TapeIR& t, const nt_options& o, Plan& p);
 void choose_mode(const TapeIR& t, const nt_options& o, Plan& p);
 double fwd_cost(int op, bool f32);
 double store_cost(bool f32);
@@ -445,6 +447,20 @@ int make_plan(TapeIR& t, const nt_options* opt, Plan& p, std::string& err) {
   if (p.loop.found) {
     const int rc = plan_reverse_loop(t, o, p, err);
     if (rc != NT_OK) return rc;
+  } else if (wants_line_segments(t, o, p)) {
+    plan_line_segments(t, o, p);
+    if (p.kf + p.ka > 16) {
+      // Values that depend on no draw (a step schedule recorded up front)
+      // are carried from where they are computed to where they are read;
+      // moved next to their readers, they may not cross a boundary at all.
+      TapeIR sunk = sink_invariants(t);
+      Plan q = p;
+      plan_line_segments(sunk, o, q);
+      if (q.kf + q.ka < p.kf + p.ka) {
+        t = std::move(sunk);
+        p = std::move(q);
+      }
+    }
   }
   choose_mode(t, o, p);
   return NT_OK;
@@ -624,6 +640,181 @@ double fwd_cost(int op, bool f32) {
 // reverse sweep, in VALU instructions' worth (the HBM round trip dominates).
 double store_cost(bool f32) { return f32 ? 48 : 96; }
 
+// ---- checkpointed straight line ----
+//
+// A tape with no rolled loop is one basic block: its reverse sweep reads
+// forward values from the whole tape, so the kernel keeps O(n) of them live
+// and spills once they exceed the register file. Cut into segments (the
+// reference's segment-checkpoint plan, AadCheckpointPlan.java:95-172: about
+// sqrt(n) nodes each, at least 48, for tapes over 512 nodes,
+// DeviceAadExecutable.java:92), the forward pass keeps only what the next
+// segments read, and the reverse recomputes one segment at a time before its
+// rules, so the live set is one segment's plus the values crossing its start.
+// Unlike the reference, which saves every value crossing each boundary once
+// per boundary, a value is stored once, in its own slot, and read back only
+// by the segments whose reverse needs it; constants and inputs are never
+// stored (they are re-emitted), and each boundary moves by up to a quarter
+// segment to where the fewest values cross it.
+
+constexpr int kLineMinNodes = 512;
+
+int line_seg_len(const TapeIR& t, const nt_options& o) {
+  if (o.seg_len > 0) return std::max(4, o.seg_len);
+  return std::max(48, static_cast<int>(std::lround(std::sqrt(static_cast<double>(t.n)))));
+}
+
+bool rematerialized(const TapeIR& t, int i) { return t.op[i] == NT_OP_CONST || t.op[i] == NT_OP_INPUT; }
+
+// seg_len > 0 asks for segments of that many nodes on any tape of two or more.
+bool wants_line_segments(const TapeIR& t, const nt_options& o, const Plan& p) {
+  if (p.loop.found || !p.adjoints || p.markets > 1 || t.outputs.size() > 1) return false;
+  if (o.checkpoint == NT_CKPT_STORE_ALL || o.mode == NT_MODE_TANGENT || !t.active[t.output]) return false;
+  if (o.seg_len <= 0 && t.n <= kLineMinNodes) return false;
+  return t.n >= 2 * line_seg_len(t, o);
+}
+
+// Operand values the reverse rule of active node i reads (the rules of
+// rev_rules): bit 0 operand a, bit 1 operand b, bit 2 the node's own value.
+int rule_reads(const TapeIR& t, int i) {
+  const int op = t.op[i];
+  const int ar = arity(op);
+  const bool aa = ar >= 1 && t.active[t.a[i]];
+  const bool ba = ar >= 2 && t.active[t.b[i]];
+  switch (op) {
+    case NT_OP_MUL: return (aa ? 2 : 0) | (ba ? 1 : 0);
+    case NT_OP_DIV: return (aa ? 2 : 0) | (ba ? 6 : 0);
+    case NT_OP_EXP: case NT_OP_SQRT: return aa ? 4 : 0;
+    case NT_OP_LOG: case NT_OP_ABS: return aa ? 1 : 0;
+    case NT_OP_MAX: case NT_OP_MIN: return (aa || ba) ? 3 : 0;
+    default: return 0;
+  }
+}
+
+// Slots for values carried across segment boundaries: node x occupies one
+// over boundaries lo[x] .. hi[x] (boundary k sits before segment k); nodes
+// come in order of lo, so taking the lowest free slot colours the intervals
+// with as many slots as the most that overlap. Returns the slot count.
+int colour_intervals(const std::vector<int>& lo, const std::vector<int>& hi, std::vector<int>& slot) {
+  const int n = static_cast<int>(lo.size());
+  slot.assign(n, -1);
+  std::vector<int> busy_until;  // per slot: the last boundary its node occupies
+  for (int x = 0; x < n; ++x) {
+    if (lo[x] > hi[x]) continue;
+    int k = 0;
+    while (k < static_cast<int>(busy_until.size()) && busy_until[k] >= lo[x]) ++k;
+    if (k == static_cast<int>(busy_until.size())) busy_until.push_back(0);
+    busy_until[k] = hi[x];
+    slot[x] = k;
+  }
+  return static_cast<int>(busy_until.size());
+}
+
+void plan_line_segments(const TapeIR& t, const nt_options& o, Plan& p) {
+  const int n = t.n, len = line_seg_len(t, o);
+  // cross[b]: values other than constants and inputs defined before b and
+  // read at or after b
+  std::vector<int> last(n, -1);
+  for (int j = 0; j < n; ++j) {
+    const int ar = arity(t.op[j]);
+    if (ar >= 1) last[t.a[j]] = std::max(last[t.a[j]], j);
+    if (ar >= 2) last[t.b[j]] = std::max(last[t.b[j]], j);
+  }
+  std::vector<int> cross(n + 1, 0);
+  for (int i = 0; i < n; ++i) {
+    if (rematerialized(t, i) || last[i] <= i) continue;
+    cross[i + 1] += 1;
+    if (last[i] + 1 <= n) cross[last[i] + 1] -= 1;
+  }
+  for (int b = 1; b <= n; ++b) cross[b] += cross[b - 1];
+  const int S = (n + len - 1) / len;
+  std::vector<int> bound{0};
+  for (int s = 1; s < S; ++s) {
+    const int nominal = s * len;
+    const int lo = std::max(bound.back() + 1, nominal - len / 4), hi = std::min(n - 1, nominal + len / 4);
+    int best = std::max(lo, std::min(nominal, hi));
+    for (int b = lo; b <= hi; ++b) {
+      if (cross[b] < cross[best] || (cross[b] == cross[best] && std::abs(b - nominal) < std::abs(best - nominal))) best = b;
+    }
+    bound.push_back(best);
+  }
+  bound.push_back(n);
+  std::vector<int>& seg_of = p.lseg;
+  seg_of.assign(n, 0);
+  for (int s = 0; s < S; ++s) {
+    for (int i = bound[s]; i < bound[s + 1]; ++i) seg_of[i] = s;
+  }
+  // forward: a value read by a later segment is carried from its own
+  // segment's end to its last reader's start
+  std::vector<int> flo(n, 1), fhi(n, 0), alo(n, 1), ahi(n, -1);
+  for (int x = 0; x < n; ++x) {
+    if (rematerialized(t, x) || last[x] < 0 || seg_of[last[x]] == seg_of[x]) continue;
+    flo[x] = seg_of[x] + 1;
+    fhi[x] = seg_of[last[x]];
+  }
+  // reverse: the adjoint of x is carried from its last active reader in a
+  // later segment down to its own segment
+  for (int i = 0; i < n; ++i) {
+    if (!t.active[i]) continue;
+    const int ar = arity(t.op[i]);
+    for (int k = 0; k < ar; ++k) {
+      const int x = k == 0 ? t.a[i] : t.b[i];
+      if (t.active[x] && t.op[x] != NT_OP_INPUT && seg_of[i] > seg_of[x]) ahi[x] = std::max(ahi[x], seg_of[i]);
+    }
+  }
+  std::vector<int> ahi_c(n, 0);  // alo > ahi_c: not carried
+  for (int x = 0; x < n; ++x) {
+    if (ahi[x] >= 0) {
+      alo[x] = seg_of[x] + 1;
+      ahi_c[x] = ahi[x];
+    } else {
+      ahi[x] = seg_of[x];
+    }
+  }
+  p.kf = colour_intervals(flo, fhi, p.fslot);
+  p.ka = colour_intervals(alo, ahi_c, p.aslot);
+  p.ahi = ahi;
+  // reverse recompute: what each segment's rules read, and what computing
+  // those reads
+  p.lneed.assign(n, 0);
+  p.lslot.assign(n, -1);
+  p.lin.assign(S, {});
+  std::vector<uint8_t> stored(n, 0);
+  for (int s = 0; s < S; ++s) {
+    const int lo = bound[s], hi = bound[s + 1];
+    std::vector<uint8_t> in(lo, 0);
+    auto need = [&](int x) {
+      if (x >= lo) p.lneed[x] = 1;
+      else in[x] = 1;
+    };
+    for (int i = hi - 1; i >= lo; --i) {
+      const int ar = arity(t.op[i]);
+      if (t.active[i] && ar > 0) {
+        const int r = rule_reads(t, i);
+        if (r & 1) need(t.a[i]);
+        if (r & 2) need(t.b[i]);
+        if (r & 4) need(i);
+      }
+      if (p.lneed[i] && ar >= 1) need(t.a[i]);
+      if (p.lneed[i] && ar >= 2) need(t.b[i]);
+    }
+    for (int x = 0; x < lo; ++x) {
+      if (!in[x]) continue;
+      p.lin[s].push_back(x);
+      if (!rematerialized(t, x)) stored[x] = 1;
+    }
+  }
+  int slots = 0;
+  for (int i = 0; i < n; ++i) {
+    if (stored[i]) p.lslot[i] = slots++;
+  }
+  p.lbound = std::move(bound);
+  p.seg = len;
+  p.nseg_full = S;
+  p.tail = 0;
+  p.ckpt = NT_CKPT_RECOMPUTE;
+  p.ck_slots = p.tape_slots = slots;
+}
+
 double rev_cost(int op, bool aa, bool ba) {
   const double A = aa ? 1 : 0, B = ba ? 1 : 0;
   switch (op) {
@@ -693,6 +884,12 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
     tan += tan_cost(t, p, i);
   }
   if (L.found) rev += store_cost(f32) * L.iters * p.n_stored;
+  if (!p.lbound.empty()) {
+    // the checkpointed straight line recomputes every segment once and
+    // stores each crossing value once
+    for (int i = 0; i < t.n; ++i) rev += fwd_cost(t.op[i], f32);
+    rev += store_cost(f32) * p.tape_slots;
+  }
   p.cost_reverse = rev;
   p.cost_tangent = tan;
   // Several markets per dispatch are priced in tangent mode (also price-only:
@@ -708,7 +905,19 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.store_index.assign(p.store_index.size(), -1);
   p.n_stored = 0;
   p.ck_slots = p.tape_slots = 0;
-  if (!L.found) return;
+  p.lbound.clear();
+  p.lseg.clear();
+  p.lslot.clear();
+  p.fslot.clear();
+  p.aslot.clear();
+  p.ahi.clear();
+  p.lneed.clear();
+  p.lin.clear();
+  p.kf = p.ka = 0;
+  if (!L.found) {
+    p.seg = p.nseg_full = p.tail = 0;
+    return;
+  }
   // Iterations per loop trip, by the registers the carried state and its
   // tangents hold (always an even count when a step draws an odd number of
   // normals, so both Box-Muller legs stay in one trip). Longer trips let the
@@ -756,9 +965,13 @@ class Emitter {
 
   // Counter high word of a stream: the path's for stream 0, xor s * 0x9E3779B1
   // for stream s (Philox.java:44-52); declared once per path.
-  static std::string rhi(int stream) { return stream == 0 ? std::string("rhi") : "rhi" + std::to_string(stream); }
+  // key_ names the copies of the Philox key that a recomputed segment of a
+  // checkpointed straight line draws from ("" elsewhere).
+  std::string key_;
+  std::string rhi(int stream) const { return (stream == 0 ? std::string("rhi") : "rhi" + std::to_string(stream)) + key_; }
+  std::string rlo() const { return "rlo" + key_; }
   std::string uniform_call(int stream, const std::string& ordinal) const {
-    return std::string(f32_ ? "nt_uniformf" : "nt_uniform") + "(rlo, " + rhi(stream) + ", " + ordinal + ")";
+    return std::string(f32_ ? "nt_uniformf" : "nt_uniform") + "(" + rlo() + ", " + rhi(stream) + ", " + ordinal + ")";
   }
 
   std::string lit(double v) const {
@@ -794,7 +1007,7 @@ class Emitter {
   std::string expr(int op, const std::string& x, const std::string& y, double c, int a) const {
     switch (op) {
       case NT_OP_CONST: return lit(c);
-      case NT_OP_INPUT: return "in" + std::to_string(a) + ms(true);
+      case NT_OP_INPUT: return "in" + std::to_string(a) + ms(true) + in_sfx_;
       case NT_OP_ADD: return x + " + " + y;
       case NT_OP_SUB: return x + " - " + y;
       case NT_OP_MUL: return x + " * " + y;
@@ -883,6 +1096,7 @@ class Emitter {
   void trip_counters(const std::string& ind);
   std::string body_draw(int u, int j, std::map<std::pair<int, int>, std::string>& pairs, const std::string& ind);
   void line_forward(int lo, int hi);
+  void line_node(int lo, int i);
   void line_reverse(int lo, int hi);
 
   // ---- loop ----
@@ -1131,6 +1345,9 @@ class Emitter {
   bool fallback() const { return exp_fallback() || nonfinite_fallback(); }
   void body_tangent();
   void body_reverse();
+  void body_reverse_segmented();
+  void line_case_head();
+  std::string in_sfx_;  // names the opaque copies of the inputs inside a case of a checkpointed straight line
 };
 
 std::string Emitter::vname(int node) const {
@@ -1163,7 +1380,7 @@ void Emitter::line_draw(int lo, int i) {
   if (it == pairs_.end()) {
     stem = "zl" + std::to_string(lo) + "_" + std::to_string(stream) + "_" + std::to_string(ctr);
     o_ << "    real " << stem << "c, " << stem << "s;\n";
-    o_ << "    nt_normal_pair(rlo, " << rhi(stream) << ", " << ctr << "u, " << stem << "c, " << stem << "s);\n";
+    o_ << "    nt_normal_pair(" << rlo() << ", " << rhi(stream) << ", " << ctr << "u, " << stem << "c, " << stem << "s);\n";
     pairs_[{stream, ctr}] = stem;
   } else {
     stem = it->second;
@@ -1209,16 +1426,144 @@ std::string Emitter::body_draw(int u, int j, std::map<std::pair<int, int>, std::
 
 void Emitter::line_forward(int lo, int hi) {
   pairs_.clear();
-  for (int i = lo; i < hi; ++i) {
-    const int op = t_.op[i];
-    if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
-      line_draw(lo, i);
-      continue;
+  for (int i = lo; i < hi; ++i) line_node(lo, i);
+}
+
+void Emitter::line_node(int lo, int i) {
+  const int op = t_.op[i];
+  if (op == NT_OP_RANDN || op == NT_OP_RANDU) {
+    line_draw(lo, i);
+    return;
+  }
+  const int ar = arity(op);
+  const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
+  const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
+  o_ << "    const real v" << i << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+}
+
+// The reverse sweep of a checkpointed straight line: two loops over the
+// segments, each a switch with one case per segment, so that each segment is
+// a basic block of its own (the compiler schedules and allocates registers
+// within a segment, and its passes stay fast on long tapes). Values cross
+// segments only through the carried slots nt_f<k> (forward) and nt_a<k>
+// (adjoints), so the live set at any point is one segment's plus the slots.
+//
+// Forward loop, segment s: read the values it needs from earlier segments
+// from their slots (constants and inputs re-emitted), compute its nodes,
+// store those a later segment's reverse reads (scratch[slot * T + lane]),
+// and leave those later segments read in their slots. Reverse loop, last
+// segment first: read back the stored values the segment needs, recompute
+// its needed nodes, take the carried adjoints from their slots, run its
+// rules, and leave in slots the adjoints that earlier segments continue. The
+// contributions reach each adjoint in the same order as in an uncut sweep.
+//
+// Every case starts from opaque copies (nt_opaque, nt_opaque_u) of the
+// segment index, the inputs, the Philox key and the lane index: the compiler
+// can see neither which case runs next nor that a case's work is the same on
+// every pass of the loop, so it keeps each segment's arithmetic, draws and
+// scratch addresses inside its case instead of hoisting them out of the
+// loops (where they would stay live for the whole path) or merging the
+// recomputation with the forward pass.
+void Emitter::line_case_head() {
+  o_ << "        const nt_u64 nt_ct = nt_opaque(tid);\n";
+  o_ << "        const nt_u32 rlo_o = nt_opaque(rlo);\n";
+  for (int st = 0; st < t_.n_streams; ++st) {
+    key_.clear();
+    const std::string h = rhi(st);
+    key_ = "_o";
+    o_ << "        const nt_u32 " << rhi(st) << " = nt_opaque(" << h << ");\n";
+  }
+  key_ = "_o";
+  for (int j = 0; j < t_.n_in; ++j) o_ << "        const real in" << j << "_o = nt_opaque_u(in" << j << ");\n";
+  in_sfx_ = "_o";
+}
+
+void Emitter::body_reverse_segmented() {
+  const int n = t_.n;
+  const auto& B = p_.lbound;
+  const auto& seg = p_.lseg;
+  const int S = static_cast<int>(B.size()) - 1;
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  const std::string one = f32_ ? "1.0f" : "1.0";
+  auto slotname = [](const char* stem, int k) { return std::string(stem) + std::to_string(k); };
+  o_ << "    {\n";
+  for (int k = 0; k < p_.kf; ++k) o_ << "    real nt_f" << k << " = " << zero << ";\n";
+  o_ << "    for (int nt_s = 0; nt_s < " << S << "; ++nt_s) {\n";
+  o_ << "      switch (nt_opaque_u(nt_s)) {\n";
+  for (int s = 0; s < S; ++s) {
+    const int lo = B[s], hi = B[s + 1];
+    o_ << "      case " << s << ": {  // nodes " << lo << " to " << hi - 1 << "\n";
+    line_case_head();
+    std::set<int> entering;
+    for (int i = lo; i < hi; ++i) {
+      const int ar = arity(t_.op[i]);
+      if (ar >= 1 && t_.a[i] < lo) entering.insert(t_.a[i]);
+      if (ar >= 2 && t_.b[i] < lo) entering.insert(t_.b[i]);
     }
-    const int ar = arity(op);
-    const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
-    const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
-    o_ << "    const real v" << i << " = " << expr(op, x, y, t_.c[i], t_.a[i]) << ";\n";
+    for (int x : entering) {
+      if (p_.fslot[x] >= 0) o_ << "    const real v" << x << " = " << slotname("nt_f", p_.fslot[x]) << ";\n";
+      else line_node(lo, x);  // a constant or an input
+    }
+    pairs_.clear();
+    for (int i = lo; i < hi; ++i) line_node(lo, i);
+    for (int i = lo; i < hi; ++i) {
+      if (p_.lslot[i] >= 0) o_ << "    scratch[(nt_u64)" << p_.lslot[i] << "u * T + nt_ct] = v" << i << ";\n";
+    }
+    if (t_.output >= lo && t_.output < hi) o_ << "    nt_y[0] = (double)" << vname(t_.output) << ";\n";
+    for (int i = lo; i < hi; ++i) {
+      if (p_.fslot[i] >= 0) o_ << "    " << slotname("nt_f", p_.fslot[i]) << " = v" << i << ";\n";
+    }
+    o_ << "        break;\n      }\n";
+    key_.clear();
+    in_sfx_.clear();
+  }
+  o_ << "      }\n    }\n    }\n";
+  for (int j = 0; j < t_.n_in; ++j) {
+    const int node = t_.input_node[j];
+    if (t_.active[node]) o_ << "    real d" << node << " = " << (node == t_.output ? one : zero) << ";\n";
+  }
+  for (int k = 0; k < p_.ka; ++k) o_ << "    real nt_a" << k << " = " << zero << ";\n";
+  o_ << "    for (int nt_s = " << S - 1 << "; nt_s >= 0; --nt_s) {\n";
+  o_ << "      switch (nt_opaque_u(nt_s)) {\n";
+  for (int s = S - 1; s >= 0; --s) {
+    const int lo = B[s], hi = B[s + 1];
+    o_ << "      case " << s << ": {  // nodes " << lo << " to " << hi - 1 << "\n";
+    line_case_head();
+    for (int x : p_.lin[s]) {
+      if (p_.lslot[x] >= 0) o_ << "    const real v" << x << " = scratch[(nt_u64)" << p_.lslot[x] << "u * T + nt_ct];\n";
+      else line_node(lo, x);  // a constant or an input
+    }
+    pairs_.clear();
+    for (int i = lo; i < hi; ++i) {
+      if (p_.lneed[i]) line_node(lo, i);
+    }
+    key_.clear();
+    in_sfx_.clear();
+    for (int x = 0; x < hi; ++x) {
+      if (p_.aslot[x] < 0) continue;
+      if (seg[x] <= s && s < p_.ahi[x]) {
+        o_ << "    real d" << x << " = " << slotname("nt_a", p_.aslot[x]) << ";\n";
+      } else if (seg[x] < s && p_.ahi[x] == s) {
+        o_ << "    real d" << x << " = " << (x == t_.output ? one : zero) << ";\n";
+      }
+    }
+    for (int i = lo; i < hi; ++i) {
+      if (!t_.active[i] || t_.op[i] == NT_OP_INPUT || arity(t_.op[i]) == 0 || p_.aslot[i] >= 0) continue;
+      o_ << "    real d" << i << " = " << (i == t_.output ? one : zero) << ";\n";
+    }
+    line_reverse(lo, hi);
+    for (int x = 0; x < lo; ++x) {
+      if (p_.aslot[x] >= 0 && seg[x] < s && s <= p_.ahi[x]) {
+        o_ << "    " << slotname("nt_a", p_.aslot[x]) << " = d" << x << ";\n";
+      }
+    }
+    o_ << "        break;\n      }\n";
+  }
+  o_ << "      }\n    }\n";
+  for (int j = 0; j < t_.n_in; ++j) {
+    const int node = t_.input_node[j];
+    o_ << "    nt_g[" << j << "] = " << (t_.active[node] ? "(double)d" + std::to_string(node) : std::string("0.0"))
+       << ";\n";
   }
 }
 
@@ -2011,6 +2356,10 @@ void Emitter::preamble() {
     o_ << "// loop: start " << L_.start << ", period " << L_.period << ", iterations " << L_.iters << ", draws/iter "
        << L_.draws << ", segment " << p_.seg << " (" << p_.nseg_full << " full + tail " << p_.tail
        << "), checkpoint policy " << p_.ckpt << ", stored/iter " << p_.n_stored << "\n";
+  } else if (!p_.lbound.empty() && !tangent) {
+    o_ << "// checkpointed straight line: " << p_.lbound.size() - 1 << " segments of about " << p_.seg
+       << " nodes, " << p_.tape_slots << " values stored per path, " << p_.kf << " values and " << p_.ka
+       << " adjoints carried\n";
   }
   if (tangent) {
     o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent basis="
@@ -2219,6 +2568,10 @@ void Emitter::body_tangent() {
 // Forward pass, then the reverse sweep; leaves the output in nt_y and the
 // adjoints of the inputs in nt_g.
 void Emitter::body_reverse() {
+  if (!p_.lbound.empty()) {
+    body_reverse_segmented();
+    return;
+  }
   const int n = t_.n;
   const bool loop = L_.found;
   const int ls = loop ? L_.start : n;

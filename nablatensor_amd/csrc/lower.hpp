@@ -93,6 +93,21 @@ struct Plan {
   std::vector<int> carries;               // carried positions (checkpointed)
   int n_stored = 0;
   int ck_slots = 0, tape_slots = 0;       // per-thread scratch slots
+  // Checkpointed straight line: the reverse sweep of a tape with no rolled
+  // loop, cut into segments lbound[s] .. lbound[s + 1] (lbound empty: not
+  // cut); lseg[node] is the node's segment. The forward pass runs segment
+  // by segment, passing each value a later segment reads in carried slot
+  // fslot[node] (kf slots), and stores each value that a later segment's
+  // reverse reads once, in tape slot lslot[node]. The reverse, last segment
+  // first, recomputes a segment's lneed nodes from lin[s] (stored values
+  // read back, constants and inputs re-emitted), then runs its rules; the
+  // adjoint of a node that a later segment's rules reach is carried in slot
+  // aslot[node] (ka slots) from segment ahi[node], the last such reader,
+  // down to its own.
+  std::vector<int> lbound, lseg, lslot, fslot, aslot, ahi;
+  std::vector<uint8_t> lneed;
+  std::vector<std::vector<int>> lin;
+  int kf = 0, ka = 0;
   int n_channels = 0;                     // 2 + n_inputs
 };
 

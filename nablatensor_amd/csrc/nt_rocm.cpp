@@ -253,7 +253,7 @@ void fill_static_info(const Lowered& l, nt_exec_info& info) {
   info.loop_carries = static_cast<int32_t>(l.plan.carries.size());
   info.seg_len = l.plan.seg;
   info.n_segments = l.plan.nseg_full + (l.plan.tail ? 1 : 0);
-  info.checkpoint = L.found ? l.plan.ckpt : 0;
+  info.checkpoint = (L.found || !l.plan.lbound.empty()) ? l.plan.ckpt : 0;
   info.tape_slots = l.plan.tape_slots;
   info.mode = l.plan.mode;
   info.block = l.plan.block;
@@ -280,7 +280,10 @@ int decline_spill(const nt_exec_info& info, const nt_options* opt) {
                 "the rocm engine declines this tape: its %s replay kernel (%d nodes, %s) would spill %d bytes per "
                 "lane to scratch memory at %d VGPRs; set nt_options.allow_spill to run it anyway",
                 info.mode == NT_MODE_TANGENT ? "tangent-mode" : "reverse-sweep", info.n_nodes,
-                info.loop_period ? "step loop rolled" : "no step loop found, straight-line", info.scratch_bytes,
+                info.loop_period    ? "step loop rolled"
+                : info.n_segments ? "no step loop found, straight line cut into checkpointed segments"
+                                  : "no step loop found, straight line",
+                info.scratch_bytes,
                 info.vgprs);
   return fail(NT_E_UNSUPPORTED, buf);
 }

@@ -65,6 +65,36 @@ __device__ __forceinline__ float nt_hw_cos2pif(float x) { return __builtin_amdgc
 // within 2 ulp of the rounded quotient, where a correctly rounded division
 // takes ten instructions.
 __device__ __forceinline__ float nt_rcpf(float x) { return __builtin_amdgcn_rcpf(x); }
+// Optimisation barriers: x comes back unchanged, but the compiler cannot
+// see that it equals the argument, and keeps the barriers in program order.
+// nt_opaque holds a per-lane value in a VGPR; nt_opaque_u a wave-uniform one
+// in SGPRs, so that it stays uniform (a switch on it is a scalar branch). A
+// checkpointed straight line starts each segment from such copies, so its
+// work is neither hoisted out of the segment loops nor merged with the
+// forward pass.
+template <typename T>
+__device__ __forceinline__ T nt_opaque(T x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ T nt_opaque_u(T x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "a 32- or 64-bit value");
+  // readfirstlane makes the value provably uniform (a value the compiler
+  // holds in a VGPR, such as a converted input, cannot be copied to SGPRs
+  // otherwise); on a value already in SGPRs it costs nothing
+  if constexpr (sizeof(T) == 4) {
+    int v = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x));
+    asm volatile("" : "+s"(v));
+    return __builtin_bit_cast(T, v);
+  } else {
+    const nt_u64 u = __builtin_bit_cast(nt_u64, x);
+    int lo = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<nt_u32>(u)));
+    int hi = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<nt_u32>(u >> 32)));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return __builtin_bit_cast(T, (static_cast<nt_u64>(static_cast<nt_u32>(hi)) << 32) | static_cast<nt_u32>(lo));
+  }
+}
 #endif
 
 // Strong-zero numbers for the tangents of the re-evaluation pass: a product

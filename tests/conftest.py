@@ -253,6 +253,24 @@ def sqrt_classes_tape(nt, s_val, floor=True, steps=16):
     return nt.AadRecorder.record(body)
 
 
+def branching_tape(nt, steps=24):
+    """The reference's random branching tape for its checkpoint parity test
+    (CudaCheckpointParityTest.java:75-85): a level driven by two normals per
+    step and floored at 0.01, then log, exp, sqrt and a division."""
+    def body(rec):
+        level = rec.input("level", 1.2)
+        scale = rec.input("scale", 0.1)
+        for _ in range(steps):
+            level = level.add(rec.randn().mul(scale)).add(rec.randn().mul(0.01)).max(0.01)
+        rec.output(level.log().exp().sqrt().div(scale.add(1.0)))
+    return nt.AadRecorder.record(body)
+
+
+def asian_tape(nt, steps):
+    """Products.asianCall on the ATM one-year market over `steps` uniform fixings."""
+    return nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(steps))
+
+
 MERTON_FIELDS = ("spot", "strike", "vol", "rate", "maturity", "jumpIntensity", "jumpMean", "jumpVol")
 
 

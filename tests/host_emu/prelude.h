@@ -26,6 +26,11 @@ inline double nt_mk(unsigned hi, unsigned lo) {
   return x;
 }
 inline unsigned nt_xor3(unsigned a, unsigned b, unsigned c) { return a ^ b ^ c; }
+// the device's optimisation barriers; on the host the value itself
+template <typename T>
+inline T nt_opaque(T x) { return x; }
+template <typename T>
+inline T nt_opaque_u(T x) { return x; }
 inline bool nt_zero_or_pos_normal(double x) {
   const int c = std::fpclassify(x);
   return c == FP_ZERO || (c == FP_NORMAL && !std::signbit(x));

@@ -117,15 +117,18 @@ def test_spilling_kernel_is_declined(rocm, nt):
     """A kernel that would spill to scratch is declined with NT_E_UNSUPPORTED,
     as the reference's engines decline a tape in compile() (AadEngine.java:50-59),
     unless the caller opts in with allow_spill. The tape: a 96-fixing Asian call
-    lowered without its step loop and swept in reverse, so every forward value
+    lowered without its step loop and swept in reverse with every forward
+    value kept (checkpoint policy "store all", no segments), so every value
     stays live until the sweep (600 nodes, more than 512 VGPRs hold)."""
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(96)).flat()
-    opts = dict(mode=rocm.NT_MODE_REVERSE, roll=-1)
+    opts = dict(mode=rocm.NT_MODE_REVERSE, roll=-1, checkpoint=rocm.NT_CKPT_STORE_ALL)
     with pytest.raises(rocm.NtError) as e:
         rocm.compile_check(flat, rocm.options("fp64", **opts))
     assert e.value.status == rocm.NT_E_UNSUPPORTED
     assert "declines" in str(e.value) and "spill" in str(e.value) and "allow_spill" in str(e.value)
     info = rocm.compile_check(flat, rocm.options("fp64", allow_spill=True, **opts))
     assert info["scratch_bytes"] > 0 and info["loop_period"] == 0
-    # the same tape with its step loop rolled needs no scratch
+    # the same tape with its step loop rolled, or cut into checkpointed segments, needs no scratch
     assert rocm.compile_check(flat, rocm.options("fp64", mode=rocm.NT_MODE_REVERSE))["scratch_bytes"] == 0
+    info = rocm.compile_check(flat, rocm.options("fp64", mode=rocm.NT_MODE_REVERSE, roll=-1))
+    assert info["scratch_bytes"] == 0 and info["n_segments"] == 13 and info["checkpoint"] == rocm.NT_CKPT_RECOMPUTE

@@ -341,3 +341,69 @@ def test_step_schedule_recorded_up_front_on_device(rocm, mode):
     print(check_per_path(v, g, flat, 2048, OFFSET, 42, min_strict=0.94))  # measured 0.943
     ref = oracle.replay_sums(flat, 200_000, 0, 42)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-10
+
+
+def _line_tape(nt, tapes, name):
+    from conftest import branching_tape
+    from nablatensor_amd import workloads
+    if name == "weekdays":
+        return workloads.schedule_tapes()["asian_weekdays"].flat()
+    if name == "branching":
+        return branching_tape(nt).flat()
+    return tapes[name]
+
+
+@pytest.mark.parametrize("name,libm,seg,paths,strict", [
+    ("C2", 0, 0, 2048, STRICT["C2"]), ("C2", 1, 0, 2048, STRICT["C2"]), ("C3", 0, 0, 1024, STRICT["C3"]),
+    ("weekdays", 0, 0, 2048, 0.94), ("branching", 0, 19, 4096, 1.0)])
+def test_checkpointed_straight_line_on_device(rocm, nt, tapes, name, libm, seg, paths, strict):
+    """Tapes lowered without a step loop and swept in reverse segment by
+    segment (the reference's segment-checkpoint plan, AadCheckpointPlan.java:95-172):
+    no scratch, per path within the bar, sums within 1e-10 of the oracle's.
+    With device libm Box-Muller the 252-fixing Asian is within 1e-12 on every
+    path."""
+    flat = _line_tape(nt, tapes, name)
+    print(f"case straight line {name} libm={libm} seg={seg} paths={paths}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", roll=-1, mode=1, libm=libm, seg_len=seg)) as x:
+        info = x.info()
+        assert info["scratch_bytes"] == 0 and info["loop_period"] == 0
+        assert info["n_segments"] > 1 and info["checkpoint"] == rocm.NT_CKPT_RECOMPUTE
+        v, g = x.replay_paths(paths, OFFSET, 42)
+        sums, _ = x.replay(100_000, 0, 42)
+    print(info["vgprs"], "VGPRs", info["n_segments"], "segments", info["tape_slots"], "stored")
+    out = check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=strict)
+    print(out)
+    if libm:
+        assert out["max_err"] <= 1e-12, out
+    ref = oracle.replay_sums(flat, 100_000, 0, 42)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-10
+
+
+def test_checkpointed_straight_line_exception_kernel_on_device(rocm, nt):
+    """The 32-step Merton jump tape without its loop, in 40-node segments:
+    the paths whose indicator overflows exp go to the exception kernel, which
+    re-evaluates them segment by segment; per path within the bar."""
+    from conftest import merton_call_tape
+    flat = merton_call_tape(nt, MERTON, steps=32).flat()
+    print("case straight line merton seg=40 paths=2048", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", roll=-1, mode=1, seg_len=40)) as x:
+        assert x.info()["n_segments"] > 1
+        v, g = x.replay_paths(2048, OFFSET, 42)
+    assert np.all(np.isfinite(g))
+    print(check_per_path(v, g, flat, 2048, OFFSET, 42, min_strict=0.98))  # measured 0.985
+
+
+def test_checkpointed_straight_line_fp32_reconciles(rocm, tapes):
+    """fp32, the 252-fixing Asian without its loop, reverse sweep in segments:
+    price and each Greek within 1e-5 of the fp64 oracle (floored at the
+    Greek's standard error)."""
+    t = tapes["C2"]
+    paths = 200_000
+    print(f"case straight line C2 fp32 paths={paths}", flush=True)
+    with rocm.Executable(t, rocm.options("fp32", roll=-1, mode=1)) as x:
+        assert x.info()["n_segments"] > 1 and x.info()["scratch_bytes"] == 0
+        sums, _ = x.replay(paths, 0, 42)
+    ref = oracle.replay_sums(t, paths, 0, 42)
+    r = reconcile(sums, ref, paths, t, 42)
+    print(r)
+    assert r["ok"]

@@ -113,6 +113,98 @@ def test_unrolled_straight_line_matches(rocm, tapes):
     check_per_path(v, g, flat, 64, OFFSET, 42, min_strict=STRICT["C2"])
 
 
+def line_plan(src):
+    """The checkpointed straight line's plan line of a generated kernel."""
+    m = re.search(r"// checkpointed straight line: (\d+) segments of about (\d+) nodes, (\d+) values stored per path, "
+                  r"(\d+) values and (\d+) adjoints carried", src)
+    return None if m is None else dict(zip(("segments", "seg_len", "stored", "values", "adjoints"),
+                                           map(int, m.groups())))
+
+
+@pytest.mark.parametrize("which,seg", [("asian120", 48), ("asian120", 96), ("asian32", 17), ("branching", 19)])
+def test_checkpointed_straight_line_is_bit_exact(nt, rocm, which, seg):
+    """The reference's checkpoint parity cases (CudaCheckpointParityTest.java:61-85:
+    Asian 120 fixings at 48 and 96 nodes per segment, Asian 32 at 17, the
+    branching tape at 19), lowered without their step loop and swept in reverse
+    segment by segment: with libm Box-Muller every value and adjoint equals the
+    oracle's bit for bit (the rules run in the uncut sweep's order), for 513
+    paths at a 32-bit-crossing offset, both of the reference's seeds, and a
+    moved input."""
+    from conftest import asian_tape, branching_tape
+    tape = {"asian120": lambda: asian_tape(nt, 120), "asian32": lambda: asian_tape(nt, 32),
+            "branching": lambda: branching_tape(nt)}[which]()
+    flat = tape.flat()
+    opts = rocm.options("fp64", roll=-1, mode=1, libm=1, seg_len=seg)
+    src = rocm.lower(flat, opts)
+    plan = line_plan(src)
+    n = len(flat["op"])
+    assert plan is not None and plan["seg_len"] == seg and plan["segments"] == -(-n // seg)
+    k = emu.EmulatedKernel(src, len(flat["input_node"]), tape_slots(src))
+    moved = list(flat["recorded_inputs"])
+    moved[0] = {"asian120": 101.0, "asian32": 98.0, "branching": 1.5}[which]
+    for seed in (42, 0x12345678FEDCBA98):
+        for x in (flat["recorded_inputs"], moved):
+            _, v, g = k.run(x, 513, OFFSET, seed, grid=3, block=64)
+            ov, og = oracle.replay_paths(flat, 513, OFFSET, seed, inputs=x, threads=1)
+            assert np.array_equal(v, ov) and np.array_equal(g, og), (seed, x[0])
+
+
+def test_checkpointed_straight_line_plan(rocm, tapes):
+    """The 252-fixing Asian lowered without its loop: sqrt(1536) < 48, so 32
+    segments of about 48 nodes, each boundary moved to where the fewest values
+    cross it. Each value a later segment's reverse reads is stored once (the
+    two loop-invariant step coefficients and the one or two values that cross
+    each boundary); four values and four adjoints are carried."""
+    src = rocm.lower(tapes["C2"], rocm.options("fp64", roll=-1, mode=1))
+    assert line_plan(src) == dict(segments=32, seg_len=48, stored=34, values=4, adjoints=4)
+    assert tape_plan(src)["tape_slots"] == "34"
+    # below 512 nodes, or with every value stored, no cut
+    assert line_plan(rocm.lower(tapes["C1"], rocm.options("fp64", roll=-1, mode=1))) is None
+    assert line_plan(rocm.lower(tapes["C2"], rocm.options("fp64", roll=-1, mode=1, checkpoint=3))) is None
+    # tangent mode carries no tape
+    assert line_plan(rocm.lower(tapes["C2"], rocm.options("fp64", roll=-1, mode=2))) is None
+
+
+def test_checkpointed_straight_line_sinks_a_schedule(rocm):
+    """The weekday-fixing Asian lowered without its loop: its step schedule
+    (computed before the first step) would be carried across every boundary;
+    moved next to the steps that read it, three values and three adjoints
+    cross a boundary. Per path within the bar (the moved nodes accumulate the
+    shared inputs' adjoints in another order)."""
+    from nablatensor_amd import workloads
+    flat = workloads.schedule_tapes()["asian_weekdays"].flat()
+    opts = rocm.options("fp64", roll=-1, mode=1, libm=1)
+    src = rocm.lower(flat, opts)
+    assert line_plan(src) == dict(segments=53, seg_len=53, stored=54, values=3, adjoints=3)
+    _, v, g = run_emulated(flat, opts, 200, rocm=rocm)
+    ov, _ = oracle.replay_paths(flat, 200, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov)
+    check_per_path(v, g, flat, 200, OFFSET, 42, min_strict=0.95)
+
+
+@pytest.mark.parametrize("precision", ["fp64", "fp32"])
+def test_checkpointed_straight_line_exception_kernel(nt, rocm, precision):
+    """The Merton jump tape (its saturating indicator overflows exp on most
+    paths) lowered without its loop and cut into 40-node segments: the
+    exception kernel re-evaluates the flagged paths segment by segment with
+    the oracle's zero-adjoint rule; no NaN, per path within the bar (fp64),
+    sums within 1e-5 of the fp32 oracle (fp32)."""
+    from conftest import merton_call_tape
+    m = dict(spot=100.0, strike=100.0, vol=0.18, rate=0.03, maturity=1.0, jumpIntensity=0.75, jumpMean=-0.05,
+             jumpVol=0.15)
+    flat = merton_call_tape(nt, m, steps=32).flat()
+    opts = rocm.options(precision, roll=-1, mode=1, seg_len=40)
+    src = rocm.lower(flat, opts)
+    assert line_plan(src)["seg_len"] == 40 and "void nt_replay_slow(" in src
+    sums, v, g = run_emulated(flat, opts, 256, rocm=rocm)
+    assert np.all(np.isfinite(sums)) and np.all(np.isfinite(g))
+    if precision == "fp64":
+        check_per_path(v, g, flat, 256, OFFSET, 42, min_strict=0.98)
+    else:
+        ref = oracle.replay_sums(flat, 256, OFFSET, 42, f32=True)
+        assert rel_err(sums, ref, floor=1.0) <= 1e-5
+
+
 def test_price_only_and_moved_inputs(rocm, tapes):
     flat = tapes["C3"]
     x = [95.0, 101.0, 0.3, 0.01, 0.75]
