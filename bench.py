@@ -47,27 +47,40 @@ def workload_tape(name: str):
     return workloads.workload_tapes()[name].flat()
 
 
-def measured_traffic(precision: str, info: dict) -> dict | None:
-    """HBM bytes per launch of this kernel configuration, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (copy-calibrated), if one matches."""
-    path = ROOT / "profiles" / f"nt_replay_asian252_{precision}_counters.md"
+# The committed counter summary of each workload's replay kernel (profiles/).
+COUNTER_FILES = {"C1": "european1", "C2": "asian252", "C3": "barrier252", "C4": "heston_asian504",
+                 "C5": "worstof16", "asian_weekdays": "asian_weekdays252"}
+
+
+def measured_counters(workload: str, precision: str, info: dict) -> dict:
+    """From the committed rocprofv3 summary of this workload and precision, the
+    lines that match this kernel (derivative mode, checkpoint policy, segment
+    length, straight-line segments and VGPRs): `traffic` (HBM bytes per
+    dispatch, FETCH_SIZE and WRITE_SIZE copy-calibrated) and `executed`
+    (executed FLOPs per scenario from the VALU counters)."""
+    out = {}
+    path = ROOT / "profiles" / f"nt_replay_{COUNTER_FILES.get(workload, workload)}_{precision}_counters.md"
     if not path.exists():
-        return None
+        return out
+    want = {"mode": info["mode"], "checkpoint": info["checkpoint"], "seg_len": info["seg_len"],
+            "segments": info["n_segments"], "vgprs": info["vgprs"]}
     for line in path.read_text().splitlines():
-        if line.startswith("traffic:"):
-            kv = dict(item.split("=") for item in line.split()[1:])
-            if (int(kv.get("mode", 1)) == info["mode"] and int(kv["checkpoint"]) == info["checkpoint"]
-                    and int(kv["seg_len"]) == info["seg_len"]):
-                return {"bytes": float(kv["bytes"]), "source": str(path.relative_to(ROOT))}
-    return None
+        kind = line.split(":", 1)[0]
+        if kind not in ("traffic", "executed"):
+            continue
+        kv = dict(item.split("=") for item in line.split()[1:])
+        if all(int(kv[k]) == v for k, v in want.items() if k in kv):
+            out[kind] = {k: float(v) for k, v in kv.items() if k not in want}
+            out[kind]["source"] = str(path.relative_to(ROOT))
+    return out
 
 
 def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
-            waves=0, max_blocks=0, basis=0):
+            waves=0, max_blocks=0, basis=0, roll=1):
     from nablatensor_amd import flops
 
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves,
-                                                max_blocks=max_blocks, basis=basis)) as x:
+                                                max_blocks=max_blocks, basis=basis, roll=roll)) as x:
         info = x.info()
         # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
         # (untimed) before the warmup steps, so a short --warmup does not time
@@ -86,10 +99,15 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
         wall = time.perf_counter() - t0
     fl = flops.flops_per_scenario(flat, precision)
     avg_replay_s = sum(replay_ms) / len(replay_ms) / 1e3
-    # The committed counter summaries cover the Asian 252-fixing tape at 2,000,000 scenarios.
-    traffic = measured_traffic(precision, info) if workload == "C2" and paths == 2_000_000 else None
+    # The committed counter summaries are per workload at the scenarios per dispatch it names.
+    from nablatensor_amd import workloads
+
+    counted = measured_counters(workload, precision, info) if paths == workloads.DESCRIPTIONS[workload][1] else {}
+    traffic = counted.get("traffic")
+    executed = counted.get("executed")
     achieved = fl * paths / avg_replay_s / 1e12
     peak = flops.PEAK_TFLOPS[precision]
+    ex_achieved = None if executed is None else executed["flops_per_scenario"] * paths / avg_replay_s / 1e12
     return {
         "value": paths * steps / wall,
         "ms_per_step": wall / steps * 1e3,
@@ -100,10 +118,16 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
                      "unit": "TFLOP/s", "frac": achieved / peak,
                      "traffic": None if traffic is None else traffic["bytes"],
                      "traffic_source": None if traffic is None else traffic["source"],
+                     "executed_flops_per_scenario": None if executed is None else executed["flops_per_scenario"],
+                     "executed_achieved": ex_achieved,
+                     "executed_frac": None if ex_achieved is None else ex_achieved / peak,
+                     "valu_issue": None if executed is None else executed.get("valu_issue"),
+                     "executed_source": None if executed is None else executed["source"],
                      "algorithmic_bytes": 8 * (len(flat["input_node"]) + info["grid_cap"] * (2 + len(flat["input_node"]))),
                      "flops_per_scenario": fl, "convention": "NT-FLOP v1"},
         "kernel": {**{k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
-                                           "loop_iters", "seg_len", "checkpoint", "tape_slots", "grid_cap")},
+                                           "loop_iters", "seg_len", "n_segments", "checkpoint", "tape_slots",
+                                           "grid_cap")},
                    "mode": MODES[info["mode"]]},
     }
 
@@ -135,19 +159,40 @@ def measure_markets(rocm, flat, precision, paths, steps, warmup, seed, markets, 
             "speedup_vs_separate": markets * single / avg}
 
 
+def host_cpu() -> dict:
+    """The host's CPUs: the count the OS reports, the ones this process may
+    run on, the thread budget the environment sets, and the model name."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"nproc": os.cpu_count(), "usable": usable, "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "model": model}
+
+
 def cpu_baseline(flat, sample, seed):
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    cpu = host_cpu()
+    # Every CPU this process may use, unless the environment sets a smaller thread budget (a shared host
+    # gives each GPU a share of its cores through OMP_NUM_THREADS).
+    threads = cpu["usable"]
+    if cpu["omp_num_threads"] and cpu["omp_num_threads"].isdigit():
+        threads = min(threads, int(cpu["omp_num_threads"]))
     oracle.replay_sums(flat, 4096, 0, seed, threads=threads)  # load + warm
     t0 = time.perf_counter()
     oracle.replay_sums(flat, sample, 0, seed, threads=threads)
     secs = time.perf_counter() - t0
-    return {"value": sample / secs, "unit": "scenarios/s", "cores": threads, "kind": "port",
+    return {"value": sample / secs, "unit": "scenarios/s", "cores": threads, "kind": "port", "host": cpu,
             "sample": f"{WORKLOAD}, fp64, {sample:,} scenarios, seed {seed}: C restatement of the reference "
-                      f"scalar cpu engine (oracle/nt_oracle.c), OpenMP, {secs:.2f} s; reference cpu-jit/simd "
-                      "not run (no JDK on this host)"}
+                      f"scalar cpu engine (oracle/nt_oracle.c), OpenMP over {threads} threads, {secs:.2f} s; "
+                      "reference cpu-jit/simd not run (no JDK on this host)"}
 
 
 def copy_calibration(mib: int) -> int:
@@ -186,7 +231,7 @@ def other_workload(rocm, args) -> int:
         print(json.dumps(out), flush=True)
         return 0
     m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp,
-                args.workload, args.waves, args.max_blocks, args.basis)
+                args.workload, args.waves, args.max_blocks, args.basis, args.roll)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -195,8 +240,50 @@ def other_workload(rocm, args) -> int:
                       "nodes": len(flat["op"]), "inputs": len(flat["input_node"])},
            "roofline": m["roofline"], "kernel_ms": m["kernel_ms"], "replay_kernel_ms": m["replay_kernel_ms"],
            "kernel": m["kernel"]}
-    if args.workload == "C5":
-        out["projection_1e10_seconds"] = 1e10 / m["value"]
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def risk_run(rocm, args) -> int:
+    """The worst-of risk run: 10^4 launches of 10^6 scenarios each (fp32, seed
+    42, launch k over scenarios [k 10^6, (k + 1) 10^6), so the Philox counter
+    crosses 2^32 from launch 4,295 on), timed end to end on the host, raw sums
+    added in launch order. Prints one JSON line with the total time, the
+    throughput, the price and Greeks of the 10^10 scenarios and their standard
+    errors."""
+    import numpy as np
+
+    from nablatensor_amd import workloads
+
+    desc, per, seed, prec = workloads.DESCRIPTIONS["C5"]
+    prec = args.precision or prec
+    launches = args.risk_launches
+    flat = workload_tape("C5")
+    print(f"[bench] C5 risk run: {launches:,} launches x {per:,} scenarios, {prec}", file=sys.stderr, flush=True)
+    with rocm.Executable(flat, rocm.options(prec)) as x:
+        x.replay(per, 0, seed)  # load the module, clocks up
+        total = None
+        kernel_ms = 0.0
+        t0 = time.perf_counter()
+        for k in range(launches):
+            sums, tm = x.replay(per, k * per, seed)
+            total = sums if total is None else total + sums
+            kernel_ms += tm["replay_ms"]
+            if k % 1000 == 999:
+                print(f"[bench] {k + 1:,} launches, {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+        secs = time.perf_counter() - t0
+    n = launches * per
+    nin = len(flat["input_node"])
+    mean = total / n
+    var = np.maximum(mean[1] - mean[0] ** 2, 0.0)
+    out = {"metric": f"scenarios/sec for value+all Greeks ({prec}), worst-of risk run end to end",
+           "value": n / secs, "unit": "scenarios/s", "n_gpus": 1, "steps": launches, "warmup": 1,
+           "ms_per_step": secs / launches * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f64" if prec == "fp64" else "f32", "data": f"synthetic (Philox2x32-10 normals, seed {seed})",
+           "config": {"workload": f"C5: {desc}", "scenarios": n, "launches": launches, "scenarios_per_launch": per,
+                      "offsets": "launch k at k x scenarios_per_launch"},
+           "seconds": secs, "replay_kernel_seconds": kernel_ms / 1e3, "price": float(mean[0]),
+           "price_stderr": float(np.sqrt(var / n)), "greeks": [float(g) for g in mean[2:2 + nin]]}
     print(json.dumps(out), flush=True)
     return 0
 
@@ -215,9 +302,11 @@ def other_workloads(rocm, steps: int = 5, warmup: int = 1, ramp: float = 0.2) ->
     for name, prec in OTHER_WORKLOADS:
         desc, paths, seed, _ = workloads.DESCRIPTIONS[name]
         m = measure(rocm, workload_tape(name), prec, paths, steps, warmup, seed, 0, 0, 0, ramp, name)
+        ex = m["roofline"]["executed_frac"]
         out[f"{name}_{prec}"] = {"workload": desc, "scenarios_per_step": paths, "seed": seed,
                                  "value": m["value"], "unit": "scenarios/s", "ms_per_step": m["ms_per_step"],
                                  "replay_kernel_ms": m["replay_kernel_ms"], "frac": m["roofline"]["frac"],
+                                 "executed_frac": ex, "traffic": m["roofline"]["traffic"],
                                  "peak_tflops": m["roofline"]["peak"], "mode": m["kernel"]["mode"],
                                  "vgprs": m["kernel"]["vgprs"], "scratch_bytes": m["kernel"]["scratch_bytes"]}
         print(f"[bench] {name} {prec} {m['value']:.3e} scen/s, {100 * m['roofline']['frac']:.1f} % of peak",
@@ -341,6 +430,12 @@ def main() -> int:
                          "code-object cache, per-dispatch host time, a chunked replaySafe request) and print its line")
     ap.add_argument("--host-paths", type=int, default=4_000_000_000,
                     help="scenarios in the --host replaySafe request")
+    ap.add_argument("--roll", type=int, default=1, choices=(1, -1),
+                    help="with --workload/--precision: -1 lowers the tape without its step loop (a checkpointed "
+                         "straight line in reverse mode)")
+    ap.add_argument("--risk-run", action="store_true",
+                    help="only run the worst-of risk run (10^4 launches of 10^6 scenarios, fp32) and print its line")
+    ap.add_argument("--risk-launches", type=int, default=10_000, help="launches in --risk-run")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
@@ -357,7 +452,9 @@ def main() -> int:
         return 1
     if args.host:
         return host_overheads(rocm, args)
-    if args.workload != "C2" or args.precision or args.markets > 1:
+    if args.risk_run:
+        return risk_run(rocm, args)
+    if args.workload != "C2" or args.precision or args.markets > 1 or args.roll != 1:
         return other_workload(rocm, args)
     flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(252)).flat()
     print(f"[bench] {WORKLOAD}: {len(flat['op'])} nodes, {args.paths:,} scenarios/step", file=sys.stderr, flush=True)

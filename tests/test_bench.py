@@ -14,13 +14,15 @@ import bench  # noqa: E402
 
 
 def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
-                 waves=0, max_blocks=0, basis=0):
+                 waves=0, max_blocks=0, basis=0, roll=1):
     ms = 2.0 if precision == "fp64" else 1.0
     resolved = "reverse" if mode == 1 else "tangent"
     return {"value": paths / (ms / 1e3), "ms_per_step": ms, "kernel_ms": ms, "replay_kernel_ms": ms,
             "kernel_scenarios_per_s": paths / (ms / 1e3),
             "roofline": {"bound": "valu", "kernel": "nt_replay", "achieved": 10.0, "peak": 78.6, "unit": "TFLOP/s",
                          "frac": 10.0 / 78.6, "traffic": None, "traffic_source": None, "algorithmic_bytes": 1,
+                         "executed_flops_per_scenario": 15000, "executed_achieved": 8.0, "executed_frac": 8.0 / 78.6,
+                         "valu_issue": 0.85, "executed_source": "fake",
                          "flops_per_scenario": 18723, "convention": "NT-FLOP v1"},
             "kernel": {"vgprs": 100, "scratch_bytes": 0, "mode": resolved}}
 
@@ -65,8 +67,39 @@ def test_other_workloads_print_one_line(patched, monkeypatch, capsys, workload):
     out = run_main(monkeypatch, capsys, ["--workload", workload, "--steps", "1", "--warmup", "0"])
     assert out["config"]["workload"].startswith(workload)
     assert out["value"] > 0
-    if workload == "C5":
-        assert out["projection_1e10_seconds"] > 0
+
+
+def test_risk_run_line(patched, monkeypatch, capsys):
+    """--risk-run adds the raw sums of every launch (launch k over scenarios
+    k x 10^6 onwards) and reports the time and the 10^10-scenario result."""
+    import numpy as np
+
+    from nablatensor_amd import rocm
+
+    offsets = []
+
+    class FakeExecutable:
+        def __init__(self, flat, opts):
+            self.n = len(flat["input_node"])
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *exc):
+            return False
+
+        def replay(self, paths, offset, seed):
+            offsets.append(offset)
+            sums = np.zeros(2 + self.n)
+            sums[0], sums[1] = 2.0 * paths, 5.0 * paths
+            return sums, {"kernel_ms": 1.0, "wall_ms": 1.0, "replay_ms": 1.0}
+
+    monkeypatch.setattr(rocm, "Executable", FakeExecutable)
+    out = run_main(monkeypatch, capsys, ["--risk-run", "--risk-launches", "3"])
+    assert offsets == [0, 0, 1_000_000, 2_000_000]
+    assert out["config"]["scenarios"] == 3_000_000 and out["steps"] == 3
+    assert out["price"] == 2.0 and out["price_stderr"] == pytest.approx(1.0 / np.sqrt(3e6))
+    assert out["dtype"] == "f32" and len(out["greeks"]) == 33
 
 
 def test_more_than_one_gpu_is_refused(monkeypatch, capsys):
@@ -83,21 +116,21 @@ def test_markets_line(patched, monkeypatch, capsys):
     assert out["unit"] == "market-scenarios/s" and out["config"]["markets"] == 4
 
 
-def plan_of(source: str) -> dict:
-    line = next(ln for ln in source.splitlines() if ln.startswith("// nt-plan:"))
-    return dict(kv.split("=") for kv in line.split()[2:])
+COUNTED = [("C2", "fp64", 0, 1), ("C2", "fp64", 1, 1), ("C2", "fp32", 0, 1), ("C2", "fp64", 1, -1),
+           *[(w, p, 0, 1) for w, p in bench.OTHER_WORKLOADS]]
 
 
-@pytest.mark.parametrize("precision,mode", [("fp64", 0), ("fp64", 1), ("fp32", 0)])
-def test_committed_counters_cover_the_planned_headline_kernels(tapes, precision, mode):
-    """The traffic figure bench.py reports comes from the committed rocprofv3
-    summary of the exact kernel configuration the engine plans today; a change
-    of plan that leaves it unmeasured fails here rather than printing null."""
+@pytest.mark.parametrize("workload,precision,mode,roll", COUNTED)
+def test_committed_counters_cover_the_planned_kernels(workload, precision, mode, roll):
+    """The traffic and executed-FLOP figures bench.py reports come from the
+    committed rocprofv3 summary of the exact kernel the engine builds today
+    (derivative mode, checkpoint policy, segment length, segments, VGPRs from
+    the compiled code object); a change of plan or of register allocation
+    that leaves a reported kernel unmeasured fails here rather than printing
+    null."""
     from nablatensor_amd import rocm
 
-    plan = plan_of(rocm.lower(tapes["C2"], rocm.options(precision, mode=mode)))
-    info = {"mode": 2 if plan["mode"] == "tangent" else 1, "checkpoint": int(plan["ckpt"]),
-            "seg_len": int(plan["seg"])}
-    traffic = bench.measured_traffic(precision, info)
-    assert traffic is not None, (precision, plan)
-    assert traffic["bytes"] > 0
+    info = rocm.compile_check(bench.workload_tape(workload), rocm.options(precision, mode=mode, roll=roll))
+    got = bench.measured_counters(workload, precision, info)
+    assert set(got) == {"traffic", "executed"}, (workload, precision, info)
+    assert got["traffic"]["bytes"] > 0 and got["executed"]["flops_per_scenario"] > 0
