@@ -412,7 +412,8 @@ def main() -> int:
     ap.add_argument("--no-reverse", action="store_true", help="skip the reverse-sweep comparison run")
     ap.add_argument("--markets", type=int, default=1,
                     help="with --workload/--precision: price this many input sets per dispatch from shared draws")
-    ap.add_argument("--cpu-sample", type=int, default=1_000_000)
+    ap.add_argument("--cpu-sample", type=int, default=3_000_000,
+                    help="scenarios in the CPU baseline's timed sample (about 25 CPU-seconds on 16 threads)")
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",

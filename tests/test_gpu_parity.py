@@ -136,6 +136,27 @@ def test_dispatch_split_is_additive(rocm, tapes):
     assert rel_err(first + second, whole, floor=1e-300) <= 1e-12
 
 
+def test_worst_of_launches_past_2_pow_32_are_additive(rocm, tapes):
+    """The worst-of risk run (launch k over scenarios [k 10^6, (k + 1) 10^6))
+    reaches counter offsets past 2^32 from launch 4,295 on. Launches 4,294
+    (which straddles 2^32) and 4,295 add up to one dispatch over both ranges,
+    and 20,000 fp32 paths on either side of 2^32 reconcile with the fp64
+    oracle (price and each Greek within 1e-5, floored at the Greek's standard
+    error)."""
+    t = tapes["C5"]
+    print("case C5 fp32 launches 4294, 4295 and 2^32 - 10^4", flush=True)
+    with rocm.Executable(t, rocm.options("fp32")) as x:
+        a, _ = x.replay(1_000_000, 4294 * 10**6, 42)
+        b, _ = x.replay(1_000_000, 4295 * 10**6, 42)
+        ab, _ = x.replay(2_000_000, 4294 * 10**6, 42)
+        near, _ = x.replay(20_000, 2**32 - 10_000, 42)
+    assert rel_err(a + b, ab, floor=1e-300) <= 1e-12
+    ref = oracle.replay_sums(t, 20_000, 2**32 - 10_000, 42)
+    r = reconcile(near, ref, 20_000, t, 42, offset=2**32 - 10_000)
+    print(r)
+    assert r["ok"]
+
+
 def test_set_inputs_moves_the_market(rocm, tapes):
     t = tapes["C1"]
     with rocm.Executable(t, rocm.options("fp64")) as x:
