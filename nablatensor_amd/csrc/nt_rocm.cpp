@@ -113,9 +113,24 @@ std::vector<std::string> source_features(const std::string& src) {
   return out;
 }
 
+// Byte alignment of every loop's first instruction (clang's -falign-loops).
+// The replay kernels are one hot loop that issues a VALU instruction on most
+// cycles, and where that loop starts relative to the instruction cache lines
+// is worth up to 8 % (the barrier fp32 kernel: the same instructions ran 4.02
+// or 4.34 ms per 2x10^7 paths depending on the loop's offset within its 64-byte
+// line). NABLATENSOR_ROCM_ALIGN_LOOPS sets it (a power of two; 0 leaves
+// placement to the compiler).
+int loop_alignment() {
+  const char* env = std::getenv("NABLATENSOR_ROCM_ALIGN_LOOPS");
+  if (!env || !*env) return 64;
+  const int v = std::atoi(env);
+  return (v > 0 && (v & (v - 1)) == 0 && v <= 4096) ? v : 0;
+}
+
 std::vector<std::string> compile_options(const std::string& src, bool dump) {
   std::vector<std::string> o = {std::string("--offload-arch=") + kArch, "-O3", "-std=c++17",
                                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  if (const int align = loop_alignment()) o.push_back("-falign-loops=" + std::to_string(align));
   for (const auto& f : source_features(src)) {
     o.insert(o.end(), {"-Xclang", "-target-feature", "-Xclang", f});
   }
