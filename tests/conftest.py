@@ -266,6 +266,51 @@ def branching_tape(nt, steps=24):
     return nt.AadRecorder.record(body)
 
 
+def random_tape(nt, seed: int, steps: int, outputs: int = 2):
+    """A tape of random shape: two inputs, normals on two streams, uniforms,
+    every operation, and one or two outputs."""
+    rng = np.random.default_rng(seed)
+
+    def body(rec):
+        x = rec.input("x", 1.0 + rng.random())
+        y = rec.input("y", 0.5 + rng.random())
+        other = rec.stream("other")
+        vals = [x, y]
+        for _ in range(steps):
+            a = vals[rng.integers(len(vals))]
+            b = vals[rng.integers(len(vals))]
+            k = rng.integers(12)
+            if k == 0:
+                v = a.add(rec.randn())
+            elif k == 1:
+                v = a.mul(other.randn())
+            elif k == 2:
+                v = a.sub(other.randu())
+            elif k == 3:
+                v = a.add(b)
+            elif k == 4:
+                v = a.mul(b)
+            elif k == 5:
+                v = a.div(b.abs().add(1.0))
+            elif k == 6:
+                v = a.mul(0.1).exp()
+            elif k == 7:
+                v = a.abs().add(1.0).log()
+            elif k == 8:
+                v = a.abs().sqrt()
+            elif k == 9:
+                v = a.max(b)
+            elif k == 10:
+                v = a.min(b).neg()
+            else:
+                v = a.sub(b.mul(0.5))
+            vals.append(v)
+        rec.output("first", vals[-1].add(vals[len(vals) // 3]))
+        if outputs > 1:
+            rec.output("second", vals[-2].add(vals[len(vals) // 2]))
+    return nt.AadRecorder.record(body)
+
+
 def asian_tape(nt, steps):
     """Products.asianCall on the ATM one-year market over `steps` uniform fixings."""
     return nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(steps))

@@ -182,6 +182,23 @@ def test_checkpointed_straight_line_sinks_a_schedule(rocm):
     check_per_path(v, g, flat, 200, OFFSET, 42, min_strict=0.95)
 
 
+@pytest.mark.parametrize("seed,seg", [(0, 9), (1, 17), (2, 31), (3, 48)])
+def test_checkpointed_straight_line_random_tapes(nt, rocm, seed, seg):
+    """Random single-output tapes (two inputs, normals on two streams,
+    uniforms, every operation) lowered without a loop and cut into short
+    segments: with libm Box-Muller every value and adjoint equals the
+    oracle's bit for bit."""
+    from conftest import random_tape
+    flat = random_tape(nt, 10 + seed, 80 + 70 * seed, outputs=1).flat()
+    opts = rocm.options("fp64", roll=-1, mode=1, libm=1, seg_len=seg)
+    src = rocm.lower(flat, opts)
+    assert line_plan(src)["seg_len"] == seg
+    k = emu.EmulatedKernel(src, len(flat["input_node"]), tape_slots(src))
+    _, v, g = k.run(flat["recorded_inputs"], 300, OFFSET, 42, grid=3, block=64)
+    ov, og = oracle.replay_paths(flat, 300, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov) and np.array_equal(g, og)
+
+
 @pytest.mark.parametrize("precision", ["fp64", "fp32"])
 def test_checkpointed_straight_line_exception_kernel(nt, rocm, precision):
     """The Merton jump tape (its saturating indicator overflows exp on most
