@@ -84,21 +84,23 @@ def noalloc(rocm, hip, x, inputs, paths, offset, seed, stream=None):
         hip.L.hipFree(d_sums)
 
 
-# (workload, precision, derivative mode, path counts of three consecutive calls). The
-# reverse sweep (mode 1) keeps 288 bytes of tape per lane in device memory, so its
-# dispatches stay within the lanes whose tape fits the static array.
-CASES = [("C2", "fp64", 0, (200_001, 4_097, 65_536)), ("C3", "fp32", 0, (200_001, 4_097, 65_536)),
-         ("C2", "fp64", 1, (20_001, 4_097, 16_384))]
+# (workload, precision, derivative mode, loop rolling, path counts of three consecutive
+# calls). The reverse sweep (mode 1) keeps its tape per lane in device memory (288 bytes
+# rolled, 272 bytes as a checkpointed straight line with roll -1), so its dispatches stay
+# within the lanes whose tape fits the static array.
+CASES = [("C2", "fp64", 0, 1, (200_001, 4_097, 65_536)), ("C3", "fp32", 0, 1, (200_001, 4_097, 65_536)),
+         ("C2", "fp64", 1, 1, (20_001, 4_097, 16_384)), ("C2", "fp64", 1, -1, (20_001, 4_097, 16_384))]
 
 
-@pytest.mark.parametrize("name,prec,mode,counts", CASES)
-def test_noalloc_matches_replay(rocm, hip, tapes, name, prec, mode, counts):
+@pytest.mark.parametrize("name,prec,mode,roll,counts", CASES)
+def test_noalloc_matches_replay(rocm, hip, tapes, name, prec, mode, roll, counts):
     t = tapes[name]
     recorded = np.asarray(t["recorded_inputs"], dtype=np.float64)
     moved = recorded.copy()
     moved[0] *= 1.05
-    print(f"case noalloc {name} {prec} mode={mode}", flush=True)
-    with rocm.Executable(t, rocm.options(prec, mode=mode)) as x:
+    print(f"case noalloc {name} {prec} mode={mode} roll={roll}", flush=True)
+    with rocm.Executable(t, rocm.options(prec, mode=mode, roll=roll)) as x:
+        assert roll == 1 or x.info()["n_segments"] > 1
         # two calls in a row, the second smaller; then other inputs on a caller stream
         for paths, inputs, own_stream in zip(counts, (recorded, recorded, moved), (False, False, True)):
             x.set_inputs(inputs)
