@@ -866,6 +866,9 @@ double tan_cost(const TapeIR& t, const Plan& p, int i) {
 void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   p.mode = NT_MODE_REVERSE;
   const bool multi = t.outputs.size() > 1;
+  double fwd = 0;
+  for (int i = 0; i < t.n; ++i) fwd += fwd_cost(t.op[i], p.precision == NT_FP32);
+  p.path_cost = fwd;
   if (!p.adjoints && p.markets == 1 && !multi) return;
   compute_deps(t, p);
   const LoopPlan& L = p.loop;
@@ -898,6 +901,7 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   // reverse sweep here follows one output).
   const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || multi ||
                        (p.adjoints && o.mode == NT_MODE_AUTO && tan < rev);
+  p.path_cost = fwd + (tangent ? tan : rev);
   if (!tangent) return;
   p.mode = NT_MODE_TANGENT;
   p.ckpt = 0;

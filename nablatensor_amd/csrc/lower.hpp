@@ -78,6 +78,8 @@ struct Plan {
   std::vector<uint64_t> deps;             // node -> inputs it depends on (bitset), tangent mode
   std::vector<uint64_t> posdeps;          // loop position -> union over the iterations
   double cost_reverse = 0, cost_tangent = 0;  // estimated extra VALU work per path of each mode
+  double path_cost = 0;                   // estimated VALU instructions per path: the forward plus the chosen
+                                          // mode's extra work
   int adjoints = 1;
   int block = 256;
   bool contract = false;                  // FMA contraction allowed in the generated code

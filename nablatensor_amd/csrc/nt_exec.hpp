@@ -68,6 +68,8 @@ struct nt_exec {
   size_t flags_bytes = 0;
   int dev = 0;
   int grid_cap = 1;
+  int cus = 0;          // compute units of the device
+  bool fixed_grid = false;  // the caller capped the grid (nt_options.max_blocks)
   std::vector<double> inputs;
   bool dirty = true;
   std::map<int, ntr::MarketVariant> markets;  // by set count
