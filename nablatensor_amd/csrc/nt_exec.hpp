@@ -60,6 +60,7 @@ struct nt_exec {
   double* d_inputs = nullptr;
   double* d_partials = nullptr;
   double* h_sums = nullptr;  // pinned host rows the finishing kernels write the sums to
+  uint32_t* h_deferred = nullptr;  // pinned host word: the finishing pass found flagged lanes (nt_exec_replay)
   size_t h_cap = 0;          // doubles in h_sums
   void* d_scratch = nullptr;
   size_t scratch_bytes = 0;  // bytes of d_scratch: the reverse sweep's per-lane tape at the resident grid
@@ -109,11 +110,19 @@ int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFuncti
                      double* d_partials, int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset,
                      uint64_t seed, double* out_v, double* out_g, int grid, hipEvent_t between = nullptr);
 
+// The exception kernel alone, as launch_kernel_on launches it after the replay kernel.
+int launch_slow_on(nt_exec* x, hipStream_t stream, hipFunction_t fn_slow, const double* d_inputs, double* d_partials,
+                   int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset, uint64_t seed,
+                   double* out_v, double* out_g, int grid);
+
 // Finishing pass on `stream` over the `grid` rows of the replay kernel and,
 // when the count at `d_flags` (null: none) is nonzero, the `slow_grid` rows of
 // the exception kernel after them: `nch` sums written to `out` (device or
-// pinned host memory); the count is reset to zero.
+// pinned host memory); the count is reset to zero. With `deferred` (pinned
+// host memory) set, the exception kernel has not run: when the count is
+// nonzero the pass only writes 1 there and changes nothing else (else 0 and
+// the sums as above).
 int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int slow_grid, int nch,
-                     double* out, uint64_t* d_flags);
+                     double* out, uint64_t* d_flags, uint32_t* deferred = nullptr);
 
 }  // namespace ntr

@@ -333,6 +333,7 @@ nt_exec::~nt_exec() {
   if (d_scratch) (void)hipFree(d_scratch);
   if (d_flags) (void)hipFree(d_flags);
   if (h_sums) (void)hipHostFree(h_sums);
+  if (h_deferred) (void)hipHostFree(h_deferred);
   if (d_partials) (void)hipFree(d_partials);
   if (d_inputs) (void)hipFree(d_inputs);
   for (auto& kv : markets) {
@@ -394,6 +395,14 @@ int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFuncti
          "hipModuleLaunchKernel(nt_replay)");
   if (between) NT_HIP(hipEventRecord(between, stream), "hipEventRecord");
   if (!fn_slow) return NT_OK;
+  return launch_slow_on(x, stream, fn_slow, d_inputs, d_partials, nch, d_tape, d_flags, paths, offset, seed, out_v,
+                        out_g, grid);
+}
+
+int launch_slow_on(nt_exec* x, hipStream_t stream, hipFunction_t fn_slow, const double* d_inputs, double* d_partials,
+                   int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset, uint64_t seed,
+                   double* out_v, double* out_g, int grid) {
+  const int block = x->low.plan.block;
   double* slow_rows = d_partials + static_cast<size_t>(grid) * static_cast<size_t>(nch);
   void* sargs[] = {&d_inputs, &paths, &offset, &seed, &slow_rows, &d_tape, &out_v, &out_g, &d_flags};
   NT_HIP(hipModuleLaunchKernel(fn_slow, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0,
@@ -403,11 +412,11 @@ int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFuncti
 }
 
 int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_partials, int grid, int slow_grid, int nch,
-                     double* out, uint64_t* d_flags) {
+                     double* out, uint64_t* d_flags, uint32_t* deferred) {
   unsigned blocks = static_cast<unsigned>(grid), slow_blocks = static_cast<unsigned>(slow_grid);
   unsigned nchu = static_cast<unsigned>(nch);
   const unsigned threads = 64u * static_cast<unsigned>(std::min(std::max(nch, 1), 16));
-  void* args[] = {&d_partials, &blocks, &slow_blocks, &nchu, &out, &d_flags};
+  void* args[] = {&d_partials, &blocks, &slow_blocks, &nchu, &out, &d_flags, &deferred};
   NT_HIP(hipModuleLaunchKernel(fn, 1, 1, 1, threads, 1, 1, 0, stream, args, nullptr),
          "hipModuleLaunchKernel(nt_finish)");
   return NT_OK;
@@ -516,6 +525,8 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
          "hipMalloc(partials)");
   NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_sums), sizeof(double) * nch, hipHostMallocDefault),
          "hipHostMalloc(sums)");
+  NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_deferred), sizeof(uint32_t), hipHostMallocDefault),
+         "hipHostMalloc(deferred)");
   x->h_cap = static_cast<size_t>(nch);
   const size_t scratch = ntr::tape_bytes_per_lane(x.get()) * x->grid_cap * x->low.plan.block;
   if (scratch > 0) NT_HIP(hipMalloc(&x->d_scratch, scratch), "hipMalloc(scratch)");
@@ -598,12 +609,32 @@ int nt_exec_replay(nt_exec* x, uint64_t paths, uint64_t offset, uint64_t seed, d
   NT_HIP(hipSetDevice(x->dev), "hipSetDevice");
   NT_HIP(hipEventRecord(x->ev[0], x->stream), "hipEventRecord");
   int grid = 0;
-  int rc = launch_replay(x, x->fn, x->fn_slow, paths, offset, seed, nullptr, nullptr, grid, x->ev[1]);
+  // The exception kernel runs only when the replay kernel left paths to it:
+  // the finishing pass, launched right after the replay kernel, reports that
+  // (a rare event) instead of finishing, and the exception kernel and the
+  // pass follow once the stream has drained. Sums, rows and their order are
+  // those of the three kernels launched back to back.
+  int rc = launch_replay(x, x->fn, nullptr, paths, offset, seed, nullptr, nullptr, grid, x->ev[1]);
   if (rc != NT_OK) return rc;
-  rc = launch_finish(x, x->fn_finish, x->fn_slow, x->d_partials, grid, nch, x->h_sums);
+  if (x->fn_slow) {
+    *x->h_deferred = 0;
+    rc = ntr::launch_finish_on(x->stream, x->fn_finish, x->d_partials, grid, grid, nch, x->h_sums, x->d_flags,
+                               x->h_deferred);
+  } else {
+    rc = launch_finish(x, x->fn_finish, nullptr, x->d_partials, grid, nch, x->h_sums);
+  }
   if (rc != NT_OK) return rc;
   NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
   NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  if (x->fn_slow && *x->h_deferred != 0) {
+    rc = ntr::launch_slow_on(x, x->stream, x->fn_slow, x->d_inputs, x->d_partials, nch, x->d_scratch, x->d_flags,
+                             paths, offset, seed, nullptr, nullptr, grid);
+    if (rc != NT_OK) return rc;
+    rc = launch_finish(x, x->fn_finish, x->fn_slow, x->d_partials, grid, nch, x->h_sums);
+    if (rc != NT_OK) return rc;
+    NT_HIP(hipEventRecord(x->ev[2], x->stream), "hipEventRecord");
+    NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  }
   std::memcpy(sums, x->h_sums, sizeof(double) * nch);
   if (timing) {
     float all = 0, rep = 0;

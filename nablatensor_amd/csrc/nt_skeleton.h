@@ -418,11 +418,21 @@ __device__ __forceinline__ void nt_block_store(const double (&acc)[NCH], double*
 // kernel's) are added only when `count`, the number of lanes that left paths
 // to it, is nonzero (an exception kernel that found it zero wrote no rows);
 // the pass then sets `count` back to zero for the next dispatch.
+// With `deferred` set (host memory), the exception kernel has not run yet:
+// the pass writes whether it is needed (count nonzero) there and, if it is,
+// returns at once, changing nothing; the caller then runs the exception
+// kernel and this pass again without `deferred`. The sums are the same bits
+// either way.
 extern "C" __global__ __launch_bounds__(1024) void nt_finish(const double* __restrict__ partials, nt_u32 blocks,
                                                            nt_u32 slow_blocks, nt_u32 nch, double* __restrict__ out,
-                                                           nt_u64* __restrict__ count) {
+                                                           nt_u64* __restrict__ count, nt_u32* __restrict__ deferred) {
   const nt_u32 lane = threadIdx.x & 63;
   const nt_u32 waves = blockDim.x >> 6;
+  if (deferred) {
+    const bool flagged = count[0] != 0;  // the same value in every thread
+    if (threadIdx.x == 0) deferred[0] = flagged ? 1u : 0u;
+    if (flagged) return;
+  }
   if (count && count[0] != 0) blocks += slow_blocks;
   for (nt_u32 c = threadIdx.x >> 6; c < nch; c += waves) {
     double s = 0.0;
