@@ -76,11 +76,11 @@ def measured_counters(workload: str, precision: str, info: dict) -> dict:
 
 
 def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
-            waves=0, max_blocks=0, basis=0, roll=1):
+            waves=0, max_blocks=0, basis=0, roll=1, block=0):
     from nablatensor_amd import flops
 
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves,
-                                                max_blocks=max_blocks, basis=basis, roll=roll)) as x:
+                                                max_blocks=max_blocks, basis=basis, roll=roll, block=block)) as x:
         info = x.info()
         # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
         # (untimed) before the warmup steps, so a short --warmup does not time
@@ -231,7 +231,7 @@ def other_workload(rocm, args) -> int:
         print(json.dumps(out), flush=True)
         return 0
     m = measure(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.policy, args.seg, args.mode, args.ramp,
-                args.workload, args.waves, args.max_blocks, args.basis, args.roll)
+                args.workload, args.waves, args.max_blocks, args.basis, args.roll, args.block)
     out = {"metric": f"scenarios/sec for value+all Greeks ({prec})", "value": m["value"], "unit": "scenarios/s",
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": m["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -431,6 +431,8 @@ def main() -> int:
                          "code-object cache, per-dispatch host time, a chunked replaySafe request) and print its line")
     ap.add_argument("--host-paths", type=int, default=4_000_000_000,
                     help="scenarios in the --host replaySafe request")
+    ap.add_argument("--block", type=int, default=0,
+                    help="threads per block (0: the engine's choice)")
     ap.add_argument("--roll", type=int, default=1, choices=(1, -1),
                     help="with --workload/--precision: -1 lowers the tape without its step loop (a checkpointed "
                          "straight line in reverse mode)")

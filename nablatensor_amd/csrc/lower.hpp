@@ -92,9 +92,15 @@ struct Plan {
   std::vector<uint8_t> taped;             // body value read by the reverse (in-body or as carry-in)
   std::vector<uint8_t> stored;            // body value stored per iteration
   std::vector<int> store_index;           // position -> index among stored, -1 otherwise
-  std::vector<int> carries;               // carried positions (checkpointed)
+  std::vector<int> carries;               // carried positions
+  // Reverse sweep of a rolled loop: the positions a segment's recompute
+  // produces (the values its rules read and what they are computed from; a
+  // stored value is read back instead), and the carries whose value at the
+  // segment's start it reads, checkpointed once per segment.
+  std::vector<uint8_t> rneed;
+  std::vector<int> ck_carries;
   int n_stored = 0;
-  int ck_slots = 0, tape_slots = 0;       // per-thread scratch slots
+  int ck_slots = 0, tape_slots = 0;       // per-thread scratch slots: checkpoints; checkpoints + stored values
   // Checkpointed straight line: the reverse sweep of a tape with no rolled
   // loop, cut into segments lbound[s] .. lbound[s + 1] (lbound empty: not
   // cut); lseg[node] is the node's segment. The forward pass runs segment

@@ -14,7 +14,7 @@ import bench  # noqa: E402
 
 
 def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
-                 waves=0, max_blocks=0, basis=0, roll=1):
+                 waves=0, max_blocks=0, basis=0, roll=1, block=0):
     ms = 2.0 if precision == "fp64" else 1.0
     resolved = "reverse" if mode == 1 else "tangent"
     return {"value": paths / (ms / 1e3), "ms_per_step": ms, "kernel_ms": ms, "replay_kernel_ms": ms,

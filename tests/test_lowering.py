@@ -715,3 +715,15 @@ def test_uniform_workloads_keep_their_exact_loops(rocm, tapes):
     by tests/golden/tape_digests.json), with no literal tables."""
     for name in ("C2", "C3", "C4", "C5"):
         assert "nt_lit" not in rocm.lower(tapes[name], rocm.options("fp64"))
+
+
+@pytest.mark.parametrize("name,slots", [("C2", 18), ("C3", 84), ("C4", 336)])
+def test_reverse_checkpoints_only_what_the_recompute_reads(rocm, tapes, name, slots):
+    """A segment's recompute produces only the values its rules read and what
+    they are computed from, so only the carries it reads are checkpointed: the
+    Asian's running sum (read by no rule, its adjoint flows through additions)
+    is not, leaving one slot per segment for the spot (C2: 18 segments of 14
+    steps), two for the barrier and two of Heston's three carries."""
+    src = rocm.lower(tapes[name], rocm.options("fp64", mode=1))
+    plan = tape_plan(src)
+    assert int(plan["tape_slots"]) == slots, plan
