@@ -1302,6 +1302,19 @@ class Emitter {
   // step-by-step product anyway), does not resolve.
   std::vector<int> fused_exp_;  // per loop position: the exponential whose argument this sum is, or -1
   void plan_fused_exponents();
+  // Step schedules, once per block (tangent loops). A step that reads a
+  // schedule recorded up front (per-step literals combined with loop-invariant
+  // values: a non-uniform grid's drift (r - s^2/2) T f_i and volatility
+  // s sqrt(T f_i), GbmPath.java:58-64) computes the same values for every
+  // path. The block computes them once, for every iteration, with their
+  // tangents over the inputs and the reference's rules, into LDS, and each
+  // path's step reads them: the step's work is then a uniform step's.
+  bool sched_on_ = false;
+  std::vector<char> sched_;       // per loop position: depends on no draw and no carried value
+  std::vector<int> sched_slot_;   // per loop position: its first LDS row (the value, then its tangents), or -1
+  int sched_rows_ = 0;
+  void plan_schedule();
+  void schedule_prologue();
   std::string l2e_name(int node) const { return "v" + std::to_string(node) + "_l2e" + ms(t_.active[node]); }
   void tangent(const std::string& ind, int op, const std::string& tn, const std::string& sfx, const std::vector<int>& D,
                const std::string& Vi, const std::string& Va, const std::string& Vb,
@@ -1309,6 +1322,16 @@ class Emitter {
   void tline(int lo, int hi);
   void tsegment(int U, const std::string& sg);
   int trip_ = 1;  // loop steps per trip of the pass being emitted
+  // Trips start at iteration it_base_ + sg * trip_. A stream that draws an
+  // odd number of normals per step, from an odd ordinal in the loop's first
+  // iteration (its first step was recorded before the loop), would split
+  // every Box-Muller pair across two trips, each computing the pair for one
+  // leg: the loop then runs its first iteration alone and its trips from
+  // iteration 1, where draw_shift_[stream] = 1 moves the trip's counter base
+  // (it0 * step + 1, even) and the draws' trip-relative ordinals down by one.
+  int it_base_ = 0;
+  std::map<int, int> draw_shift_;
+  int draw_lead() const;
   void body_tangent_operand(int u, int kind, int ref, std::function<std::string(int)>& fn) const;
 
   // ---- markets (tangent mode): several input sets share each path's draws ----
@@ -1424,8 +1447,29 @@ void Emitter::line_draw(int lo, int i) {
 // it0 * step_s (even, since the trip length times an odd step is even).
 void Emitter::trip_counters(const std::string& ind) {
   for (const auto& kv : L_.normal_step) {
-    o_ << ind << "const nt_u32 kb" << kv.first << " = it0 * " << kv.second << "u;\n";
+    auto sh = draw_shift_.find(kv.first);
+    o_ << ind << "const nt_u32 kb" << kv.first << " = it0 * " << kv.second << "u"
+       << (sh != draw_shift_.end() && sh->second ? " + " + std::to_string(sh->second) + "u" : std::string()) << ";\n";
   }
+}
+
+// 1 when every stream that draws an odd number of normals per step starts
+// the loop at an odd ordinal (and some does), 0 otherwise.
+int Emitter::draw_lead() const {
+  std::map<int, int> first;  // stream -> lowest normal ordinal in iteration 0
+  for (int j = 0; j < L_.period; ++j) {
+    const int i = L_.start + j;
+    if (t_.op[i] != NT_OP_RANDN) continue;
+    auto it = first.find(t_.b[i]);
+    if (it == first.end() || L_.rand_base[j] < it->second) first[t_.b[i]] = L_.rand_base[j];
+  }
+  bool odd = false;
+  for (const auto& kv : L_.normal_step) {
+    if (!(kv.second & 1)) continue;
+    if (!(first[kv.first] & 1)) return 0;
+    odd = true;
+  }
+  return odd && L_.iters > 1 ? 1 : 0;
 }
 
 // Value of loop draw position j in iteration u of a trip: both legs of a
@@ -1440,7 +1484,8 @@ std::string Emitter::body_draw(int u, int j, std::map<std::pair<int, int>, std::
     return uniform_call(stream, "(it0 + " + std::to_string(u) + "u) * " + std::to_string(step) + "u + " +
                                     std::to_string(L_.rand_base[j]) + "u");
   }
-  const int rel = L_.rand_base[j] + u * step;
+  auto sh = draw_shift_.find(stream);
+  const int rel = L_.rand_base[j] + u * step - (sh != draw_shift_.end() ? sh->second : 0);
   const int key = rel >> 1;
   auto it = pairs.find({stream, key});
   std::string stem;
@@ -1989,7 +2034,8 @@ void Emitter::tsegment(int U, const std::string& sg) {
   const std::string ind = "      ";
   const auto outer_scalars = scal_;  // scalars declared in this block end with it
   o_ << "    {\n";
-  o_ << ind << "const nt_u32 it0 = (" << sg << ") * " << trip_ << "u;\n";
+  o_ << ind << "const nt_u32 it0 = " << (it_base_ ? std::to_string(it_base_) + "u + " : std::string()) << "(" << sg
+     << ") * " << trip_ << "u;\n";
   trip_counters(ind);
   std::map<std::pair<int, int>, std::string> pairs;
   for (int u = 0; u < U; ++u) {
@@ -2004,6 +2050,21 @@ void Emitter::tsegment(int U, const std::string& sg) {
       }
       const int ar = arity(op);
       const bool act = t_.active[i] != 0;
+      if (sched_on_ && !slow_ && sched_[j] && op != NT_OP_CONST) {
+        // computed once per block (schedule_prologue)
+        const int row = sched_slot_[j];
+        if (row < 0) continue;  // read only by other schedule values
+        const std::string at = "u * " + std::to_string(L_.iters) + "u + it0 + " + std::to_string(u) + "u]";
+        o_ << ind << "const real " << name << " = nt_sch[" << row << at << ";\n";
+        if (!p_.adjoints) continue;
+        int r = row + 1;
+        for (int k : posdeplist(j)) {
+          const std::string tn = "tr" + std::to_string(u) + "_" + std::to_string(j) + "_" + std::to_string(k);
+          lazy_.erase(tn);
+          o_ << ind << "const real " << tn << " = nt_sch[" << r++ << at << ";\n";
+        }
+        continue;
+      }
       for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
         m_ = m;
         exp_active_ = act;
@@ -2170,7 +2231,8 @@ void Emitter::plan_parameters() {
   par_node_.clear();
   par_of_.clear();
   par_deps_.clear();
-  if (!L_.found || p_.mode != NT_MODE_TANGENT || !p_.adjoints || p_.basis == 1) return;
+  // a schedule computed once per block carries its tangents over the inputs
+  if (!L_.found || p_.mode != NT_MODE_TANGENT || !p_.adjoints || p_.basis == 1 || sched_on_) return;
   const int P = L_.period, s = L_.start;
   auto add = [&](int node) {
     if (node < 0 || !t_.active[node] || par_of_.count(node)) return;
@@ -2341,6 +2403,182 @@ void Emitter::plan_fused_exponents() {
   }
 }
 
+void Emitter::plan_schedule() {
+  sched_on_ = false;
+  sched_rows_ = 0;
+  sched_.assign(L_.found ? L_.period : 0, 0);
+  sched_slot_.assign(L_.found ? L_.period : 0, -1);
+  if (!L_.found || p_.mode != NT_MODE_TANGENT || p_.markets > 1) return;
+  const int P = L_.period, s = L_.start;
+  std::vector<char> drawfree(s, 1);
+  for (int i = 0; i < s; ++i) {
+    const int op = t_.op[i], ar = arity(op);
+    if (op == NT_OP_RANDN || op == NT_OP_RANDU) drawfree[i] = 0;
+    if (ar >= 1 && !drawfree[t_.a[i]]) drawfree[i] = 0;
+    if (ar >= 2 && !drawfree[t_.b[i]]) drawfree[i] = 0;
+  }
+  std::vector<char> vary(P, 0);  // reads a per-step literal
+  for (int j = 0; j < P; ++j) {
+    const int op = t_.op[s + j], ar = arity(op);
+    if (op == NT_OP_RANDN || op == NT_OP_RANDU) continue;
+    if (op == NT_OP_CONST) {
+      sched_[j] = 1;
+      vary[j] = L_.table_lit(j);
+      continue;
+    }
+    bool ok = true;
+    for (int slot = 0; slot < ar; ++slot) {
+      const int kind = slot == 0 ? L_.kind_a[j] : L_.kind_b[j];
+      const int ref = slot == 0 ? L_.ref_a[j] : L_.ref_b[j];
+      if (kind == ARG_BODY) {
+        ok = ok && sched_[ref];
+        vary[j] = vary[j] || vary[ref];
+      } else if (kind == ARG_INV) {
+        ok = ok && drawfree[ref];
+      } else {
+        ok = false;
+      }
+    }
+    sched_[j] = ok;
+  }
+  // the schedule values the rest of the step reads
+  std::vector<char> out(P, 0);
+  for (int k = 0; k < P; ++k) {
+    if (sched_[k]) continue;
+    const int ar = arity(t_.op[s + k]);
+    for (int slot = 0; slot < ar; ++slot) {
+      const int kind = slot == 0 ? L_.kind_a[k] : L_.kind_b[k];
+      const int ref = slot == 0 ? L_.ref_a[k] : L_.ref_b[k];
+      if (kind == ARG_BODY && sched_[ref] && t_.op[s + ref] != NT_OP_CONST) out[ref] = 1;
+    }
+  }
+  int rows = 0;
+  bool any = false;
+  for (int j = 0; j < P; ++j) {
+    if (!sched_[j] || t_.op[s + j] == NT_OP_CONST) continue;
+    if (L_.is_carry[j] || L_.is_liveout[j]) return;
+    if (!out[j]) continue;
+    any = any || vary[j];
+    sched_slot_[j] = rows;
+    rows += 1 + (p_.adjoints ? static_cast<int>(posdeplist(j).size()) : 0);
+  }
+  const long bytes = static_cast<long>(rows) * L_.iters * (f32_ ? 4 : 8);
+  if (!any || bytes > 32 * 1024) {
+    sched_slot_.assign(P, -1);
+    return;
+  }
+  sched_on_ = true;
+  sched_rows_ = rows;
+}
+
+// The block's schedule: the pre-loop values it reads (the same for every
+// iteration), then every iteration's schedule values and tangents, threads
+// striding over the iterations, stored in LDS rows of nt_sch[row][iteration].
+// Values use correctly rounded or device-libm functions, so they are the
+// oracle's; tangents follow the reference's local rules (ScalarReplay.java:
+// 129-183, taken forward).
+void Emitter::schedule_prologue() {
+  if (!sched_on_ || slow_) return;
+  const int P = L_.period, s = L_.start, I = L_.iters;
+  const std::string zero = f32_ ? "0.0f" : "0.0", one = f32_ ? "1.0f" : "1.0", half = f32_ ? "0.5f" : "0.5";
+  std::vector<char> cone(s, 0);
+  std::function<void(int)> need = [&](int node) {
+    if (node < 0 || node >= s || cone[node]) return;
+    cone[node] = 1;
+    const int ar = arity(t_.op[node]);
+    if (ar >= 1) need(t_.a[node]);
+    if (ar >= 2) need(t_.b[node]);
+  };
+  for (int j = 0; j < P; ++j) {
+    if (!sched_[j]) continue;
+    const int ar = arity(t_.op[s + j]);
+    if (ar >= 1 && L_.kind_a[j] == ARG_INV) need(L_.ref_a[j]);
+    if (ar >= 2 && L_.kind_b[j] == ARG_INV) need(L_.ref_b[j]);
+  }
+  // value and tangent names: pre-loop node q<node>, schedule position qs<j>
+  auto val = [&](int kind, int ref) { return kind == ARG_BODY ? "qs" + std::to_string(ref) : "q" + std::to_string(ref); };
+  auto tan = [&](int kind, int ref, int k) -> std::string {
+    const int node = kind == ARG_BODY ? s + ref : ref;
+    if (!p_.adjoints || !has(node, k)) return "";
+    if (t_.op[node] == NT_OP_INPUT) return one;
+    return val(kind, ref) + "_" + std::to_string(k);
+  };
+  auto plus = [&](const std::string& x, const std::string& y, bool minus) -> std::string {
+    if (y.empty()) return x;
+    if (x.empty()) return minus ? "(-" + y + ")" : y;
+    return "(" + x + (minus ? " - " : " + ") + y + ")";
+  };
+  auto times = [&](const std::string& t, const std::string& factor) -> std::string {
+    return t.empty() ? "" : "(" + t + " * " + factor + ")";
+  };
+  auto emit = [&](const std::string& ind, int node, int op, const std::string& name, int ka, int ra, int kb, int rb,
+                  const std::string& value) {
+    o_ << ind << "const real " << name << " = " << value << ";\n";
+    if (!p_.adjoints || op == NT_OP_CONST || op == NT_OP_INPUT) return;
+    const std::string va = arity(op) >= 1 ? val(ka, ra) : "", vb = arity(op) >= 2 ? val(kb, rb) : "";
+    for (int k : deplist(node)) {
+      const std::string ta = arity(op) >= 1 ? tan(ka, ra, k) : "", tb = arity(op) >= 2 ? tan(kb, rb, k) : "";
+      std::string e;
+      switch (op) {
+        case NT_OP_ADD: e = plus(ta, tb, false); break;
+        case NT_OP_SUB: e = plus(ta, tb, true); break;
+        case NT_OP_MUL: e = plus(times(ta, vb), times(tb, va), false); break;
+        case NT_OP_DIV: e = plus(ta.empty() ? "" : "(" + ta + " / " + vb + ")",
+                                 tb.empty() ? "" : "(" + tb + " * " + name + " / " + vb + ")", true); break;
+        case NT_OP_NEG: e = ta.empty() ? "" : "(-" + ta + ")"; break;
+        case NT_OP_EXP: e = times(ta, name); break;
+        case NT_OP_LOG: e = ta.empty() ? "" : "(" + ta + " / " + va + ")"; break;
+        case NT_OP_SQRT: e = ta.empty() ? "" : "(" + ta + " * " + half + " / " + name + ")"; break;
+        case NT_OP_ABS: e = ta.empty() ? "" : "(" + va + " < " + zero + " ? -" + ta + " : " + ta + ")"; break;
+        case NT_OP_MAX: case NT_OP_MIN: {
+          const std::string cmp = op == NT_OP_MAX ? " >= " : " <= ";
+          e = "(" + va + cmp + vb + " ? " + (ta.empty() ? zero : ta) + " : " + (tb.empty() ? zero : tb) + ")";
+          break;
+        }
+        default: break;
+      }
+      o_ << ind << "const real " << name << "_" << k << " = " << (e.empty() ? zero : e) << ";\n";
+    }
+  };
+  auto fn_value = [&](int op, const std::string& x, const std::string& y, const std::string& lit_value, int a) {
+    switch (op) {
+      case NT_OP_EXP: return std::string(f32_ ? "expf(" : "exp(") + x + ")";
+      case NT_OP_LOG: return std::string(f32_ ? "logf(" : "log(") + x + ")";
+      case NT_OP_SQRT: return std::string(f32_ ? "sqrtf(" : "sqrt(") + x + ")";
+      case NT_OP_DIV: return x + " / " + y;
+      case NT_OP_CONST: return lit_value;
+      default: return expr(op, x, y, 0.0, a);
+    }
+  };
+  o_ << "  __shared__ real nt_sch[" << sched_rows_ << " * " << I << "];\n";
+  o_ << "  {\n";
+  for (int i = 0; i < s; ++i) {
+    if (!cone[i]) continue;
+    const int op = t_.op[i], ar = arity(op);
+    const std::string x = ar >= 1 ? val(ARG_INV, t_.a[i]) : "", y = ar >= 2 ? val(ARG_INV, t_.b[i]) : "";
+    emit("    ", i, op, "q" + std::to_string(i), ARG_INV, ar >= 1 ? t_.a[i] : -1, ARG_INV, ar >= 2 ? t_.b[i] : -1,
+         fn_value(op, x, y, lit(t_.c[i]), t_.a[i]));
+  }
+  o_ << "#ifdef NT_HOST_EMU\n    for (nt_u32 it = 0; it < " << I << "u; ++it) {\n#else\n";
+  o_ << "    for (nt_u32 it = threadIdx.x; it < " << I << "u; it += blockDim.x) {\n#endif\n";
+  o_ << "      const nt_u32 it0 = it;\n";
+  for (int j = 0; j < P; ++j) {
+    if (!sched_[j]) continue;
+    const int op = t_.op[s + j], ar = arity(op);
+    const std::string x = ar >= 1 ? val(L_.kind_a[j], L_.ref_a[j]) : "";
+    const std::string y = ar >= 2 ? val(L_.kind_b[j], L_.ref_b[j]) : "";
+    const std::string lv = L_.table_lit(j) ? "nt_lit" + std::to_string(j) + "[it0]" : lit(t_.c[s + j]);
+    emit("      ", s + j, op, "qs" + std::to_string(j), L_.kind_a[j], L_.ref_a[j], L_.kind_b[j], L_.ref_b[j],
+         fn_value(op, x, y, lv, t_.a[s + j]));
+    if (sched_slot_[j] < 0) continue;
+    int row = sched_slot_[j];
+    o_ << "      nt_sch[" << row++ << "u * " << I << "u + it] = qs" << j << ";\n";
+    if (!p_.adjoints) continue;
+    for (int k : posdeplist(j)) o_ << "      nt_sch[" << row++ << "u * " << I << "u + it] = qs" << j << "_" << k << ";\n";
+  }
+  o_ << "    }\n  }\n  __syncthreads();\n";
+}
+
 void Emitter::exp_bound_checks() {
   if (slow_) return;
   for (int j = 0; j < static_cast<int>(bound_.size()); ++j) {
@@ -2398,7 +2636,8 @@ void Emitter::preamble() {
   }
   if (tangent) {
     o_ << "// nt-plan: tape_slots=0 seg=" << p_.seg << " ckpt=0 mode=tangent basis="
-       << (use_par_ ? "params" : "inputs") << " params=" << (use_par_ ? par_node_.size() : 0) << "\n";
+       << (use_par_ ? "params" : "inputs") << " params=" << (use_par_ ? par_node_.size() : 0)
+       << " schedule=" << (sched_on_ ? sched_rows_ : 0) << "\n";
     // Polynomial constants held in VGPRs make v_fmac_f64 (accumulator tied to
     // the destination) cost a 64-bit copy per term; the three-source v_fma_f64
     // needs none. (The reverse sweep below asks for the same.)
@@ -2465,6 +2704,7 @@ void Emitter::kernel_head(bool slow) {
   if (!slow && fallback()) {
     for (int m = 0; m < M; ++m) o_ << "  bool nt_lane_bad" << m << " = false;\n";
   }
+  if (!slow) schedule_prologue();
   o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
   if (slow) {
     for (int m = 0; m < M; ++m) {
@@ -2536,12 +2776,20 @@ void Emitter::body_tangent() {
     // register needs stay below the fast pass's: the kernel's register budget
     // is the larger of the two.
     trip_ = slow_ ? (L_.need_even ? 2 : 1) : p_.seg;
-    const int nfull = L_.iters / trip_, tail = L_.iters % trip_;
+    const int lead = trip_ > 1 ? draw_lead() : 0;
+    if (lead) tsegment(1, "0");  // the first iteration alone
+    it_base_ = lead;
+    if (lead) {
+      for (const auto& kv : L_.normal_step) draw_shift_[kv.first] = kv.second & 1;
+    }
+    const int nfull = (L_.iters - lead) / trip_, tail = (L_.iters - lead) % trip_;
     if (nfull > 0) {
       o_ << "    for (nt_u32 sg = 0; sg < " << nfull << "u; ++sg)\n";
       tsegment(trip_, "sg");
     }
     if (tail) tsegment(tail, std::to_string(nfull) + "u");
+    it_base_ = 0;
+    draw_shift_.clear();
     for (int j = 0; j < L_.period; ++j) {
       if (!geo(j)) continue;
       for (int m = mlo_; m < mhi_; ++m) {
@@ -2784,6 +3032,7 @@ void Emitter::kernel(bool slow) {
 
 std::string Emitter::run() {
   count_uses();
+  plan_schedule();
   plan_exp2_folds();
   plan_exp_bounds();
   plan_parameters();

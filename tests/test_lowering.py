@@ -727,3 +727,25 @@ def test_reverse_checkpoints_only_what_the_recompute_reads(rocm, tapes, name, sl
     src = rocm.lower(tapes[name], rocm.options("fp64", mode=1))
     plan = tape_plan(src)
     assert int(plan["tape_slots"]) == slots, plan
+
+
+def test_step_schedule_computed_once_per_block_and_pairs_aligned(rocm, tapes):
+    """The weekday Asian's tangent kernel computes the step schedule (drift and
+    volatility per step, with their tangents over the inputs: 7 rows) once per
+    block, so its step loop takes no square root; and since its loop's draws
+    start at ordinal 1 (the first step is recorded before the loop), the loop
+    runs its first step alone and then trips of two steps from step 1, each
+    trip one whole Box-Muller pair. The uniform Asian (draws from ordinal 0,
+    no schedule) keeps trips from step 0."""
+    from nablatensor_amd import workloads
+    flat = workloads.schedule_tapes()["asian_weekdays"].flat()
+    src = rocm.lower(flat, rocm.options("fp64", mode=2))
+    assert tape_plan(src)["schedule"] == "7"
+    fast = src[:src.index("nt_replay_slow")]
+    loop = fast[fast.index("for (nt_u32 sg = 0; sg < 125u; ++sg)"):]
+    loop = loop[:loop.index("\n    }\n")]  # the trip's block
+    assert "it0 = 1u + (sg) * 2u" in loop and "kb0 = it0 * 1u + 1u" in loop
+    assert loop.count("nt_normal_pair(") == 1
+    assert "sqrt" not in loop
+    c2 = rocm.lower(tapes["C2"], rocm.options("fp64", mode=2))
+    assert tape_plan(c2)["schedule"] == "0" and "it0 = 1u +" not in c2
