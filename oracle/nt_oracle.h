@@ -32,9 +32,14 @@
  * deviation); the Merton jump tape (uniform draws) against the exact Poisson
  * series within 1.5% (JumpModelsTest.java:46-53), its no-jump limit against
  * Black-Scholes, its adjoint delta against a bump; uniform and named-stream
- * moments as RandomStreamsTest.java:51-103. The named-stream multiplier
- * 0x9E3779B1 (Philox.java:48-50) is restated from the source text: only the
- * streams' independence is pinned, not the literal.
+ * moments as RandomStreamsTest.java:51-103.
+ *
+ * Parity unpinned: the named-stream key multiplier 0x9E3779B1 of nto_normal
+ * and nto_uniform for a stream other than the default (Philox.java:48-50,
+ * the same literal in JitPhilox.java:107). No reference file holds a value
+ * drawn from a named stream, and independence (what the tests check) holds
+ * for any odd multiplier, so the literal is restated from the source text
+ * only. The default stream (every workload tape) is pinned as above.
  */
 #ifndef NT_ORACLE_H
 #define NT_ORACLE_H
