@@ -1243,6 +1243,19 @@ class Emitter {
   // sum G after the loop. Per step that drops the carry's own multiply and,
   // for an input whose sigma is constant 1 (c's own start value), the sum of
   // tangents is that same sum of G.
+  // A carry kept as G alone whose factor is exp(x) (the worst-of basket's
+  // spots): G = exp(sum of x) needs no exponential per step. The loop adds
+  // the exponents and the exponential is taken once, after the loop (the
+  // fast pass; the re-evaluation pass keeps the product). exp of the sum and
+  // the product of the exponentials agree to the rounding of the sum (about
+  // sqrt(steps) ulps of the exponent), like G itself against the oracle's
+  // step-by-step product.
+  std::vector<char> geo_log_;  // per loop position
+  void plan_geo_logs();
+  bool geo_log(int pos) const {
+    return !slow_ && pos >= 0 && pos < static_cast<int>(geo_log_.size()) && geo_log_[pos];
+  }
+  std::string geo_factor_exponent(int u, int j) const;
   std::vector<int> gsum_;     // per loop position: the geo carry a sum accumulates, or -1
   std::vector<int> gsum_of_;  // per loop position: the sum that accumulates this geo carry, or -1
   void plan_geo_sums();
@@ -2106,9 +2119,15 @@ void Emitter::tsegment(int U, const std::string& sg) {
           const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
           const std::string m = ms(true), sj = std::to_string(j), su = std::to_string(u);
           const std::string prev = u > 0 ? std::to_string(u - 1) : "";
-          o_ << ind << "const real gq" << su << "_" << sj << m << " = "
-             << (u > 0 ? "gq" + prev + "_" + sj + m : "gs" + sj + m) << " * " << body_value(u, ARG_BODY, e, false)
-             << ";\n";
+          if (geo_log(j)) {
+            // log G: the sum of the factors' exponents
+            o_ << ind << "const real gq" << su << "_" << sj << m << " = "
+               << (u > 0 ? "gq" + prev + "_" + sj + m : "gs" + sj + m) << " + " << geo_factor_exponent(u, j) << ";\n";
+          } else {
+            o_ << ind << "const real gq" << su << "_" << sj << m << " = "
+               << (u > 0 ? "gq" + prev + "_" + sj + m : "gs" + sj + m) << " * " << body_value(u, ARG_BODY, e, false)
+               << ";\n";
+          }
           // the factor's log-derivative per input: tx for exp(x), -tb m for m = 1 / b
           const bool recip = t_.op[s + e] == NT_OP_DIV;
           std::function<std::string(int)> tx;
@@ -2306,6 +2325,32 @@ void Emitter::plan_geo_sums() {
     gsum_[a] = j;
     gsum_of_[j] = a;
   }
+}
+
+void Emitter::plan_geo_logs() {
+  geo_log_.assign(L_.found ? L_.period : 0, 0);
+  if (!L_.found) return;
+  for (int j = 0; j < L_.period; ++j) {
+    if (!geo(j) || !geo_free(j) || gsum_of_[j] >= 0) continue;
+    const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+    const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
+    if (t_.op[L_.start + e] == NT_OP_EXP && single_body_exp(e)) geo_log_[j] = 1;
+  }
+}
+
+// Exponent of geo carry j's factor in iteration u of the trip (log2 units
+// where the fp32 factor is a folded exp2).
+std::string Emitter::geo_factor_exponent(int u, int j) const {
+  const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+  const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
+  if (fold_[e].on) {
+    const Exp2Fold& f = fold_[e];
+    const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
+    if (f.p < 0) return l2e_name(f.r) + " * " + sv;
+    return !p_.fuse ? l2e_name(f.r) + " * " + sv + " + " + l2e_name(f.p)
+                    : "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")";
+  }
+  return body_value(u, L_.kind_a[e], L_.ref_a[e], false);
 }
 
 void Emitter::plan_exp2_folds() {
@@ -2765,7 +2810,7 @@ void Emitter::body_tangent() {
              << (tin.empty() ? zero : tin == "#1" ? one : tin) << ";\n";
         }
         if (geo(j)) {
-          o_ << "    real gs" << j << ms(true) << " = " << one << ";\n";
+          o_ << "    real gs" << j << ms(true) << " = " << (geo_log(j) ? zero : one) << ";\n";
           o_ << "    const real c0_" << j << ms(true) << " = st" << j << ms(true) << ";\n";
         }
       }
@@ -2794,6 +2839,15 @@ void Emitter::body_tangent() {
       if (!geo(j)) continue;
       for (int m = mlo_; m < mhi_; ++m) {
         m_ = m;
+        if (geo_log(j)) {
+          const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+          const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
+          const std::string g = "gs" + std::to_string(j) + ms(true);
+          std::string ex;
+          if (f32_) ex = fold_[e].on ? "nt_hw_exp2f(" + g + ")" : "nt_expf(" + g + ")";
+          else ex = p_.libm == 1 ? "exp(" + g + ")" : "nt_exp_fast(" + g + ", nt_slow" + ms(true) + ")";
+          o_ << "    " << g << " = " << ex << ";\n";
+        }
         if (geo_free(j)) o_ << "    st" << j << ms(true) << " = c0_" << j << ms(true) << " * gs" << j << ms(true) << ";\n";
         if (gsum_of_[j] >= 0) {
           const int a = gsum_of_[j];
@@ -3039,6 +3093,7 @@ std::string Emitter::run() {
   par_on_ = use_par_;
   plan_geo_carries();
   plan_geo_sums();
+  plan_geo_logs();
   plan_fused_exponents();
   par_on_ = false;
   preamble();
