@@ -749,3 +749,24 @@ def test_step_schedule_computed_once_per_block_and_pairs_aligned(rocm, tapes):
     assert "sqrt" not in loop
     c2 = rocm.lower(tapes["C2"], rocm.options("fp64", mode=2))
     assert tape_plan(c2)["schedule"] == "0" and "it0 = 1u +" not in c2
+
+
+def test_exp_factor_carries_sum_their_exponents(rocm, tapes):
+    """A carry kept as G alone whose factor is exp(x) (the worst-of's 16 spots)
+    adds its step exponents (gq = gs + x) and takes one exponential after the
+    loop, in the fast pass only; a carry whose G is read every step (the
+    Asian spot, summed into the average) keeps the product, and so does the
+    barrier's survival product (its factor is 1 / b, not an exponential)."""
+    for prec in ("fp64", "fp32"):
+        src = rocm.lower(tapes["C5"], rocm.options(prec, mode=2))
+        fast = src[:src.index("nt_replay_slow")]
+        logged = set(re.findall(r"real gq0_(\d+) = gs\1 \+ ", fast))
+        assert len(logged) == 16, prec
+        exp_after = r"nt_hw_exp2f\(gs{0}\)" if prec == "fp32" else r"nt_exp_fast\(gs{0}, nt_slow\)"
+        for j in logged:
+            assert re.search(r"gs{0} = ".format(j) + exp_after.format(j), fast), (prec, j)
+        slow = src[src.index("nt_replay_slow"):]
+        assert not re.search(r"real gq0_\d+ = gs\d+ \+ ", slow)
+    for name in ("C2", "C3", "C4"):
+        src = rocm.lower(tapes[name], rocm.options("fp64", mode=2))
+        assert not re.search(r"real gq0_\d+ = gs\d+ \+ ", src), name
