@@ -770,3 +770,22 @@ def test_exp_factor_carries_sum_their_exponents(rocm, tapes):
     for name in ("C2", "C3", "C4"):
         src = rocm.lower(tapes[name], rocm.options("fp64", mode=2))
         assert not re.search(r"real gq0_\d+ = gs\d+ \+ ", src), name
+
+
+@pytest.mark.parametrize("fixings", [63, 64])
+@pytest.mark.parametrize("libm", [0, 1])
+def test_weekday_grids_with_a_lead_step_and_tails(rocm, nt, fixings, libm):
+    """Asian calls on weekday grids of 63 and 64 fixings: the loop's draws
+    start at ordinal 1, so the tangent kernel runs the first loop step alone,
+    then trips of two steps (61 steps after the lead: a tail trip of one; 62:
+    none), with the step schedule computed once per block. Per path within the
+    oracle's bar, sums within 1e-12."""
+    from nablatensor_amd import workloads
+    grid = nt.TimeGrid.of(workloads.weekday_fixings(fixings))
+    flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), grid).flat()
+    src = rocm.lower(flat, rocm.options("fp64", mode=2, libm=libm))
+    assert "it0 = 1u + (sg) * 2u" in src and int(tape_plan(src)["schedule"]) > 0
+    sums, v, g = run_emulated(flat, rocm.options("fp64", mode=2, libm=libm), 200, rocm=rocm)
+    check_per_path(v, g, flat, 200, OFFSET, 42, min_strict=0.9)
+    ref = oracle.replay_sums(flat, 200, OFFSET, 42, threads=1)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-12
