@@ -367,8 +367,10 @@ def test_step_schedule_recorded_up_front_on_device(rocm, mode):
 def test_step_schedule_per_block_fp32_and_a_tail_trip(rocm, nt):
     """The weekday Asian's tangent kernels with the step schedule computed once
     per block: fp32 reconciles with the fp64 oracle (price and each Greek within
-    1e-5, floored at the Greek's standard error); a 64-fixing grid (a lead step,
-    30 trips of two and a tail of one) is per path within the bar in fp64."""
+    1e-5, floored at the Greek's standard error); a 64-fixing grid (a lead step
+    and 31 trips of two) and a 400-fixing grid (399 loop steps, more than a
+    block's 256 threads, so threads stride over the schedule's steps; a lead
+    step, 199 trips and a tail of one) are per path within the bar in fp64."""
     from nablatensor_amd import workloads
     flat = workloads.schedule_tapes()["asian_weekdays"].flat()
     print("case asian_weekdays fp32 tangent, 20000 paths", flush=True)
@@ -377,15 +379,17 @@ def test_step_schedule_per_block_fp32_and_a_tail_trip(rocm, nt):
     errs = reconcile(sums, oracle.replay_sums(flat, 20_000, 0, 42), 20_000, flat, 42)
     print(errs)
     assert errs["ok"], errs
-    grid = nt.TimeGrid.of(workloads.weekday_fixings(64))
-    flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), grid).flat()
-    print("case weekday 64 fixings fp64 tangent, 1000 paths", flush=True)
-    with rocm.Executable(flat, rocm.options("fp64", mode=2)) as x:
-        assert "it0 = 1u + (sg) * 2u" in x.source()
-        v, g = x.replay_paths(1000, OFFSET, 42)
-        sums, _ = x.replay(1000, OFFSET, 42)
-    print(check_per_path(v, g, flat, 1000, OFFSET, 42, min_strict=0.9))
-    assert rel_err(sums, oracle.replay_sums(flat, 1000, OFFSET, 42), floor=1e-300) <= 1e-10
+    for fixings in (64, 400):
+        grid = nt.TimeGrid.of(workloads.weekday_fixings(fixings))
+        flat = nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), grid).flat()
+        print(f"case weekday {fixings} fixings fp64 tangent, 1000 paths", flush=True)
+        with rocm.Executable(flat, rocm.options("fp64", mode=2)) as x:
+            src = x.source()
+            assert "it0 = 1u + (sg) * 2u" in src and "schedule=0" not in src
+            v, g = x.replay_paths(1000, OFFSET, 42)
+            sums, _ = x.replay(1000, OFFSET, 42)
+        print(check_per_path(v, g, flat, 1000, OFFSET, 42, min_strict=0.9))
+        assert rel_err(sums, oracle.replay_sums(flat, 1000, OFFSET, 42), floor=1e-300) <= 1e-10
 
 
 def _line_tape(nt, tapes, name):
