@@ -2334,6 +2334,9 @@ void Emitter::plan_geo_logs() {
     if (!geo(j) || !geo_free(j) || gsum_of_[j] >= 0) continue;
     const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
     const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
+    // a factor from the block's schedule (a deterministic growth exp(r dt_i))
+    // is read from LDS whole: its exponent is not in the step
+    if (sched_on_ && sched_[e]) continue;
     if (t_.op[L_.start + e] == NT_OP_EXP && single_body_exp(e)) geo_log_[j] = 1;
   }
 }
