@@ -2506,6 +2506,10 @@ void Emitter::plan_schedule() {
     if (!sched_[j] || t_.op[s + j] == NT_OP_CONST) continue;
     if (L_.is_carry[j] || L_.is_liveout[j]) return;
     if (!out[j]) continue;
+    // its tangents are stored for the inputs its first iteration depends on
+    // and read for those the loop position depends on: the same set for a
+    // value no carried state reaches
+    if (p_.adjoints && deplist(s + j) != posdeplist(j)) return;
     any = any || vary[j];
     sched_slot_[j] = rows;
     rows += 1 + (p_.adjoints ? static_cast<int>(posdeplist(j).size()) : 0);
