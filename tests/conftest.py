@@ -385,3 +385,30 @@ def merton_series_call(spot, strike, maturity, rate, vol, lam, mu_j, dl_j):
             break
         weight *= lam_t / (n + 1)
     return total
+
+
+def discounted_weekday_asian_tape(nt, fixings: int = 252):
+    """An Asian call on a weekday grid, each fixing discounted by a bank account
+    that grows by exp(r dt_i) per step (a deterministic factor from the step
+    schedule, read by the average every step): S_i / B_i averaged, minus the
+    strike, floored at zero."""
+    from nablatensor_amd import workloads
+    times = workloads.weekday_fixings(fixings)
+
+    def body(rec):
+        s = rec.input("S0", 100.0)
+        k = rec.input("K", 100.0)
+        vol = rec.input("sigma", 0.2)
+        r = rec.input("r", 0.03)
+        t_mat = rec.input("T", 1.0)
+        b = r.mul(0.0).add(1.0)
+        acc = r.mul(0.0)
+        prev = 0.0
+        for t in times:
+            dt = t_mat.mul(t - prev)
+            prev = t
+            s = s.mul(r.sub(vol.mul(vol).mul(0.5)).mul(dt).add(vol.mul(dt.sqrt()).mul(rec.randn())).exp())
+            b = b.mul(r.mul(dt).exp())
+            acc = acc.add(s.div(b))
+        rec.output(acc.mul(1.0 / fixings).sub(k).max(rec.constant(0.0)))
+    return nt.AadRecorder.record(body).flat()

@@ -789,3 +789,19 @@ def test_weekday_grids_with_a_lead_step_and_tails(rocm, nt, fixings, libm):
     check_per_path(v, g, flat, 200, OFFSET, 42, min_strict=0.9)
     ref = oracle.replay_sums(flat, 200, OFFSET, 42, threads=1)
     assert rel_err(sums, ref, floor=1e-300) <= 1e-12
+
+
+def test_discounted_weekday_asian_reads_its_growth_from_the_schedule(rocm, nt):
+    """A bank account growing by exp(r dt_i) on a weekday grid, read by the
+    average every step: its factor is a schedule value (with its tangents for
+    r and T) computed once per block; per path within the oracle's bar."""
+    from conftest import discounted_weekday_asian_tape
+    flat = discounted_weekday_asian_tape(nt, 48)
+    src = rocm.lower(flat, rocm.options("fp64", mode=2))
+    plan = tape_plan(src)
+    assert plan["mode"] == "tangent" and int(plan["schedule"]) >= 10, plan
+    for libm in (0, 1):
+        sums, v, g = run_emulated(flat, rocm.options("fp64", mode=2, libm=libm), 150, rocm=rocm)
+        check_per_path(v, g, flat, 150, OFFSET, 42, min_strict=0.85)  # measured 0.873
+        # (the rate's pathwise sensitivity of a discounted average nearly cancels: floor 1)
+        assert rel_err(sums, oracle.replay_sums(flat, 150, OFFSET, 42, threads=1), floor=1.0) <= 1e-12
