@@ -392,6 +392,22 @@ def test_step_schedule_per_block_fp32_and_a_tail_trip(rocm, nt):
         assert rel_err(sums, oracle.replay_sums(flat, 1000, OFFSET, 42), floor=1e-300) <= 1e-10
 
 
+def test_discounted_weekday_asian_growth_from_the_schedule(rocm, nt):
+    """A bank account b <- b * exp(r * dt_i) on a 48-fixing weekday grid: the
+    growth factor is path-invariant, so the tangent kernel reads it (and its
+    rate tangent) from the per-block schedule. Per path within the bar, sums
+    within 1e-10 (the rate sensitivity nearly cancels, so floored at 1)."""
+    from conftest import discounted_weekday_asian_tape
+    flat = discounted_weekday_asian_tape(nt, 48)
+    print("case discounted weekday asian, 48 fixings fp64 tangent, 1000 paths", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=2)) as x:
+        assert "schedule=0" not in x.source()
+        v, g = x.replay_paths(1000, OFFSET, 42)
+        sums, _ = x.replay(1000, OFFSET, 42)
+    print(check_per_path(v, g, flat, 1000, OFFSET, 42, min_strict=0.85))
+    assert rel_err(sums, oracle.replay_sums(flat, 1000, OFFSET, 42), floor=1.0) <= 1e-10
+
+
 def _line_tape(nt, tapes, name):
     from conftest import branching_tape
     from nablatensor_amd import workloads
