@@ -1256,6 +1256,27 @@ class Emitter {
     return !slow_ && pos >= 0 && pos < static_cast<int>(geo_log_.size()) && geo_log_[pos];
   }
   std::string geo_factor_exponent(int u, int j) const;
+  // Such a carry whose exponent is p + r s (or p - r s, r s - p, r s), with p
+  // and r loop-invariant and s a value with no tangent (a normal, or a
+  // correlated normal: a literal row of a Cholesky factor times the step's
+  // normals): over N steps the exponents sum to N p + r S, S the sum of s, and
+  // their tangents for input k to N tp_k + tr_k S. The loop adds s alone, one
+  // add per carry and step in place of the exponent, its sum and a fma per
+  // input; N p + r S and the tangents are formed once, after the loop (the
+  // fast pass; the sum differs from the step-by-step one in its roundings
+  // only, a few ulps of the exponent).
+  struct GeoAffine {
+    bool on = false;
+    int p = -1, r = -1;  // invariant nodes (p = -1: no offset)
+    int s_kind = ARG_NONE, s_ref = -1;
+    bool neg_p = false, neg_r = false;
+  };
+  std::vector<GeoAffine> gaff_;  // per loop position (the carry)
+  void plan_geo_affine();
+  bool gaff(int pos) const { return geo_log(pos) && pos < static_cast<int>(gaff_.size()) && gaff_[pos].on; }
+  void geo_affine_finish(int j);
+  void l2e_copies();
+  void remat_open(int ls);
   std::vector<int> gsum_;     // per loop position: the geo carry a sum accumulates, or -1
   std::vector<int> gsum_of_;  // per loop position: the sum that accumulates this geo carry, or -1
   void plan_geo_sums();
@@ -1295,15 +1316,18 @@ class Emitter {
   std::vector<Exp2Fold> fold_;  // per loop position
   void plan_exp2_folds();
   // fp64 loop bodies: an EXP of p + r z, p - r z or r z, with p and r
-  // loop-invariant and z a normal draw, cannot leave the fast exp's range if
-  // |p| + Z_MAX |r| <= 708, |z| <= Z_MAX for every Box-Muller draw (u1 >=
-  // 2^-33, so |z| <= sqrt(66 ln 2) = 6.764). That is checked once per path,
-  // before the loop, and the loop's exponentials skip their own check.
+  // loop-invariant and |z| <= Z_MAX on every step, cannot leave the fast exp's
+  // range if |p| + Z_MAX |r| <= 708. z is a normal draw (|z| <= sqrt(66 ln 2)
+  // = 6.764 for every Box-Muller draw, u1 >= 2^-33: Z_MAX 6.77) or a value
+  // built from draws and literals alone, bounded through its operands. That is
+  // checked once per path, before the loop, and the loop's exponentials skip
+  // their own check.
   struct ExpBound {
     bool on = false;
     int p = -1, r = -1;  // invariant nodes (p = -1: no offset)
     int sum = -1, mul = -1, draw = -1;  // loop positions of p +- r z, r z and z
     bool p_first = true;                // p - r z (or a sum) rather than r z - p
+    double zmax = 6.77;                 // Z_MAX
   };
   std::vector<ExpBound> bound_;  // per loop position
   void plan_exp_bounds();
@@ -1382,6 +1406,13 @@ class Emitter {
   // and tangent factor from one nt_sqrt_q (a path whose argument it does not
   // cover is evaluated again with device libm).
   bool fast_sqrt() const { return !f32_ && p_.libm == 0 && p_.mode == NT_MODE_TANGENT; }
+  // fp64 tangent loops, fast pass: x + a b, x - a b and a b - x of values
+  // with no tangent (draws and literals alone: a correlated normal, a row of
+  // a Cholesky factor times the step's normals), the product used nowhere
+  // else, are one fma. Such a value moves by an ulp at most, and it feeds the
+  // path only through exponents whose own rounding is of that size.
+  bool draw_fma() const { return fast_sqrt() && p_.fuse && !slow_; }
+  std::string draw_fma_expr(int u, int j, int op) const;
   // Forward value of a SQRT node; `q` names its tangent factor when the
   // tangent rule below should take it from here.
   std::string sqrt_expr(const std::string& x, const std::string& q, bool act) {
@@ -2084,6 +2115,10 @@ void Emitter::tsegment(int U, const std::string& sg) {
         const std::string x = ar >= 1 ? body_value(u, L_.kind_a[j], L_.ref_a[j], false) : "";
         const std::string y = ar >= 2 ? body_value(u, L_.kind_b[j], L_.ref_b[j], false) : "";
         std::string val = body_expr(j, u, op, x, y);
+        if (!act && draw_fma() && (op == NT_OP_ADD || op == NT_OP_SUB)) {
+          const std::string fm = draw_fma_expr(u, j, op);
+          if (!fm.empty()) val = fm;
+        }
         if (op == NT_OP_EXP && fold_[j].on) {
           const Exp2Fold& f = fold_[j];
           const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
@@ -2119,6 +2154,14 @@ void Emitter::tsegment(int U, const std::string& sg) {
           const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
           const std::string m = ms(true), sj = std::to_string(j), su = std::to_string(u);
           const std::string prev = u > 0 ? std::to_string(u - 1) : "";
+          if (gaff(j)) {
+            // the sum of s; exponents and tangents follow after the loop
+            const GeoAffine& g = gaff_[j];
+            o_ << ind << "const real zq" << su << "_" << sj << m << " = "
+               << (u > 0 ? "zq" + prev + "_" + sj + m : "zs" + sj + m) << " + "
+               << body_value(u, g.s_kind, g.s_ref, false) << ";\n";
+            continue;
+          }
           if (geo_log(j)) {
             // log G: the sum of the factors' exponents
             o_ << ind << "const real gq" << su << "_" << sj << m << " = "
@@ -2187,6 +2230,10 @@ void Emitter::tsegment(int U, const std::string& sg) {
       const std::string sm = ms(act);
       if (!(geo_free(j) && act && p_.adjoints)) o_ << ind << "st" << j << sm << " = r" << (U - 1) << "_" << j << sm << ";\n";
       if (!act || !p_.adjoints) continue;
+      if (gaff(j)) {
+        o_ << ind << "zs" << j << sm << " = zq" << (U - 1) << "_" << j << sm << ";\n";
+        continue;
+      }
       if (geo(j)) o_ << ind << "gs" << j << sm << " = gq" << (U - 1) << "_" << j << sm << ";\n";
       for (int k : posdeplist(j)) {
         o_ << ind << "ts" << j << "_" << k << sm << " = tr" << (U - 1) << "_" << j << "_" << k << sm << ";\n";
@@ -2356,6 +2403,87 @@ std::string Emitter::geo_factor_exponent(int u, int j) const {
   return body_value(u, L_.kind_a[e], L_.ref_a[e], false);
 }
 
+std::string Emitter::draw_fma_expr(int u, int j, int op) const {
+  for (int side = 1; side >= 0; --side) {
+    const int mk = side ? L_.kind_b[j] : L_.kind_a[j], mr = side ? L_.ref_b[j] : L_.ref_a[j];
+    if (mk != ARG_BODY || t_.op[L_.start + mr] != NT_OP_MUL || body_uses_[mr] != 1 || t_.active[L_.start + mr] ||
+        L_.is_liveout[mr] || L_.is_carry[mr])
+      continue;
+    const int ok = side ? L_.kind_a[j] : L_.kind_b[j], orf = side ? L_.ref_a[j] : L_.ref_b[j];
+    const std::string a = body_value(u, L_.kind_a[mr], L_.ref_a[mr], false);
+    const std::string b = body_value(u, L_.kind_b[mr], L_.ref_b[mr], false);
+    const std::string o = body_value(u, ok, orf, false);
+    if (op == NT_OP_ADD) return "fma(" + a + ", " + b + ", " + o + ")";
+    return side ? "fma(-(" + a + "), " + b + ", " + o + ")" : "fma(" + a + ", " + b + ", -(" + o + "))";
+  }
+  return std::string();
+}
+
+void Emitter::plan_geo_affine() {
+  gaff_.assign(L_.found ? L_.period : 0, GeoAffine());
+  if (!L_.found || !p_.fuse) return;
+  for (int j = 0; j < L_.period; ++j) {
+    if (!geo_log_[j]) continue;
+    const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
+    const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
+    GeoAffine g;
+    if (f32_) {
+      const Exp2Fold& f = fold_[e];
+      if (!f.on) continue;
+      g.p = f.p;
+      g.r = f.r;
+      g.s_kind = f.s_kind;
+      g.s_ref = f.s_ref;
+    } else {
+      const ExpBound& b = bound_[e];
+      if (!b.on) continue;
+      if (b.sum >= 0 ? fused_exp_[b.sum] != e
+                     : !(L_.kind_a[e] == ARG_BODY && L_.ref_a[e] == b.mul && body_uses_[b.mul] == 1))
+        continue;
+      const bool sub = b.sum >= 0 && t_.op[L_.start + b.sum] == NT_OP_SUB;
+      g.p = b.p;
+      g.r = b.r;
+      g.s_kind = ARG_BODY;
+      g.s_ref = b.draw;
+      g.neg_r = sub && b.p_first;
+      g.neg_p = sub && !b.p_first;
+    }
+    // s must carry no tangent: only then is the exponent's tangent affine in s
+    if (g.s_kind != ARG_BODY || t_.active[L_.start + g.s_ref]) continue;
+    g.on = true;
+    gaff_[j] = g;
+  }
+}
+
+// After the loop: geo carry j's exponent sum N p + r S (log2 units where the
+// fp32 factor is a folded exp2) and sigma_k += c0 (N tp_k + tr_k S).
+void Emitter::geo_affine_finish(int j) {
+  const GeoAffine& g = gaff_[j];
+  const std::string m = ms(true), sj = std::to_string(j);
+  const std::string S = "zs" + sj + m, N = lit(static_cast<double>(L_.iters));
+  const bool fold = f32_;  // fp32 factors are folded exp2s: p and r scaled by log2(e)
+  const std::string rv = (g.neg_r ? "-" : "") + (fold ? l2e_name(g.r) : vname(g.r));
+  std::string e = rv + " * " + S;
+  if (g.p >= 0) {
+    const std::string pv = (g.neg_p ? "-" : "") + (fold ? l2e_name(g.p) : vname(g.p));
+    e = f("fma") + "(" + rv + ", " + S + ", " + N + " * " + pv + ")";
+  }
+  o_ << "    gs" << sj << m << " = " << e << ";\n";
+  for (int k : posdeplist(j)) {
+    const std::string tp = g.p >= 0 ? inv_tname(g.p, k) : std::string(), tr = inv_tname(g.r, k);
+    std::string x;
+    if (!tp.empty()) x = tp == "#1" ? N : N + " * " + tp;
+    if (g.neg_p && !x.empty()) x = "-(" + x + ")";
+    if (!tr.empty()) {
+      const std::string rs = tr == "#1" ? S : tr + " * " + S;
+      x = x.empty() ? (g.neg_r ? "-(" + rs + ")" : rs) : x + (g.neg_r ? " - " : " + ") + rs;
+    }
+    if (x.empty()) continue;
+    const std::string ts = "ts" + sj + "_" + std::to_string(k) + m;
+    o_ << "    " << ts << " = " << f("fma") << "(c0_" << sj << m << ", " << x << ", " << ts << ");\n";
+  }
+}
+
 void Emitter::plan_exp2_folds() {
   fold_.assign(L_.found ? L_.period : 0, Exp2Fold());
   if (!f32_ || !L_.found || p_.mode != NT_MODE_TANGENT) return;
@@ -2393,21 +2521,52 @@ void Emitter::plan_exp2_folds() {
 void Emitter::plan_exp_bounds() {
   bound_.assign(L_.found ? L_.period : 0, ExpBound());
   if (f32_ || p_.libm == 1 || !L_.found || p_.mode != NT_MODE_TANGENT) return;
-  auto is_normal_draw = [&](int kind, int ref) {
-    return kind == ARG_BODY && t_.op[L_.start + ref] == NT_OP_RANDN;
+  // Largest magnitude a body value built from draws and literals alone can
+  // take (a correlated normal: a literal row of a Cholesky factor times the
+  // step's normals), or -1: a normal is at most 6.77, a uniform at most 1,
+  // sums and products bound by the sums and products of their operands' bounds.
+  std::vector<double> zb(L_.period, -2.0);  // -2: not yet known
+  std::function<double(int, int)> zbound = [&](int kind, int ref) -> double {
+    if (kind == ARG_INV) return t_.op[ref] == NT_OP_CONST ? std::fabs(t_.c[ref]) : -1.0;
+    if (kind != ARG_BODY) return -1.0;
+    if (zb[ref] > -2.0) return zb[ref];
+    double v = -1.0;
+    const int op = t_.op[L_.start + ref];
+    if (op == NT_OP_RANDN) v = 6.77;
+    else if (op == NT_OP_RANDU) v = 1.0;
+    else if (op == NT_OP_CONST) {
+      v = std::fabs(t_.c[L_.start + ref]);
+      if (L_.table_lit(ref)) {
+        for (double x : L_.lit_values[ref]) v = std::max(v, std::fabs(x));
+      }
+    } else if (op == NT_OP_NEG) {
+      v = zbound(L_.kind_a[ref], L_.ref_a[ref]);
+    } else if (op == NT_OP_ADD || op == NT_OP_SUB || op == NT_OP_MUL) {
+      const double a = zbound(L_.kind_a[ref], L_.ref_a[ref]), b = zbound(L_.kind_b[ref], L_.ref_b[ref]);
+      if (a >= 0.0 && b >= 0.0) v = op == NT_OP_MUL ? a * b : a + b;
+    }
+    // the bound of the computed value, not only of the exact one: a margin
+    // far above the roundings of a few dozen operations
+    if (v >= 0.0 && op != NT_OP_RANDN && op != NT_OP_RANDU && op != NT_OP_CONST) v *= 1.0 + 1e-9;
+    if (!(v <= 1e300)) v = -1.0;
+    return zb[ref] = v;
   };
-  // r z with r invariant: the node at loop position m; sets r and the draw's position
+  // r z with r invariant and z bounded: the node at loop position m; sets r,
+  // z's position and its bound
   int draw = -1;
+  double zmax = 0.0;
   auto scaled_draw = [&](int m, int& r) {
     if (t_.op[L_.start + m] != NT_OP_MUL) return false;
     for (int side = 0; side < 2; ++side) {
       const int ik = side ? L_.kind_b[m] : L_.kind_a[m], ir = side ? L_.ref_b[m] : L_.ref_a[m];
       const int dk = side ? L_.kind_a[m] : L_.kind_b[m], dr = side ? L_.ref_a[m] : L_.ref_b[m];
-      if (ik == ARG_INV && is_normal_draw(dk, dr)) {
-        r = ir;
-        draw = dr;
-        return true;
-      }
+      if (ik != ARG_INV || dk != ARG_BODY) continue;
+      const double zm = zbound(dk, dr);
+      if (zm < 0.0) continue;
+      r = ir;
+      draw = dr;
+      zmax = zm;
+      return true;
     }
     return false;
   };
@@ -2432,6 +2591,7 @@ void Emitter::plan_exp_bounds() {
     }
     if (b.on) {
       b.draw = draw;
+      b.zmax = zmax;
       bound_[j] = b;
     }
   }
@@ -2640,7 +2800,8 @@ void Emitter::exp_bound_checks() {
     for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
       m_ = m;
       const std::string off = b.p >= 0 ? "fabs(" + vname(b.p) + ") + " : std::string();
-      o_ << "    nt_slow" << ms(act) << " |= !(" << off << "6.77 * fabs(" << vname(b.r) << ") <= 708.0);\n";
+      const std::string zm = b.zmax == 6.77 ? std::string("6.77") : lit(b.zmax);
+      o_ << "    nt_slow" << ms(act) << " |= !(" << off << zm << " * fabs(" << vname(b.r) << ") <= 708.0);\n";
     }
   }
 }
@@ -2787,20 +2948,9 @@ void Emitter::body_tangent() {
   const std::string zero = f32_ ? "0.0f" : "0.0";
   const std::string one = f32_ ? "1.0f" : "1.0";
   tline(0, ls);
+  bool remat = false;
   if (loop) {
-    std::set<int> scaled;
-    for (const auto& f : fold_) {
-      if (!f.on) continue;
-      if (f.p >= 0) scaled.insert(f.p);
-      scaled.insert(f.r);
-    }
-    for (int node : scaled) {
-      const bool act = t_.active[node] != 0;
-      for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
-        m_ = m;
-        o_ << "    const real " << l2e_name(node) << " = " << vname(node) << " * 1.44269504088896341f;\n";
-      }
-    }
+    l2e_copies();
     par_on_ = use_par_;
     for (int j = 0; j < L_.period; ++j) {
       if (!(L_.is_carry[j] || L_.is_liveout[j])) continue;
@@ -2819,6 +2969,7 @@ void Emitter::body_tangent() {
         if (geo(j)) {
           o_ << "    real gs" << j << ms(true) << " = " << (geo_log(j) ? zero : one) << ";\n";
           o_ << "    const real c0_" << j << ms(true) << " = st" << j << ms(true) << ";\n";
+          if (gaff(j)) o_ << "    real zs" << j << ms(true) << " = " << zero << ";\n";
         }
       }
     }
@@ -2842,10 +2993,13 @@ void Emitter::body_tangent() {
     if (tail) tsegment(tail, std::to_string(nfull) + "u");
     it_base_ = 0;
     draw_shift_.clear();
+    for (int j = 0; j < L_.period && !slow_; ++j) remat |= gaff(j);
+    if (remat) remat_open(ls);
     for (int j = 0; j < L_.period; ++j) {
       if (!geo(j)) continue;
       for (int m = mlo_; m < mhi_; ++m) {
         m_ = m;
+        if (gaff(j)) geo_affine_finish(j);
         if (geo_log(j)) {
           const bool a_self = L_.kind_a[j] == ARG_CARRY && L_.ref_a[j] == j;
           const int e = a_self ? L_.ref_b[j] : L_.ref_a[j];
@@ -2904,6 +3058,63 @@ void Emitter::body_tangent() {
         const std::string g = tname(out, j);
         o_ << "    nt_g" << msuf(m) << "[" << o * nin + j << "] = "
            << (g.empty() ? std::string("0.0") : g == "#1" ? std::string("1.0") : "(double)" + g) << ";\n";
+      }
+    }
+  }
+  if (remat) o_ << "    }\n";
+}
+
+// fp32 exp2 folds: p log2(e) and r log2(e) of every folded exponent
+void Emitter::l2e_copies() {
+  std::set<int> scaled;
+  for (const auto& f : fold_) {
+    if (!f.on) continue;
+    if (f.p >= 0) scaled.insert(f.p);
+    scaled.insert(f.r);
+  }
+  for (int node : scaled) {
+    const bool act = t_.active[node] != 0;
+    for (int m = act ? mlo_ : 0; m < (act ? mhi_ : 1); ++m) {
+      m_ = m;
+      o_ << "    const real " << l2e_name(node) << " = " << vname(node) << " * 1.44269504088896341f;\n";
+    }
+  }
+}
+
+// After the step loop: a scope that computes the values before the loop
+// again, from opaque copies of the inputs, so the code after the loop reads
+// these copies and the compiler keeps nothing of the path's set-up live
+// through the loop but what the loop itself reads. The inputs are uniform, so
+// the copies stay in SGPRs; the set-up is a few hundred operations per path,
+// against the loop's hundreds per step.
+void Emitter::remat_open(int ls) {
+  const std::string zero = f32_ ? "0.0f" : "0.0";
+  const std::string one = f32_ ? "1.0f" : "1.0";
+  o_ << "    {\n";
+  for (int m = mlo_; m < mhi_; ++m) {
+    for (int j = 0; j < t_.n_in; ++j) {
+      o_ << "    const real in" << j << msuf(m) << "_r = nt_opaque_u(in" << j << msuf(m) << ");\n";
+    }
+  }
+  const bool par = par_on_;
+  par_on_ = false;
+  scal_.clear();
+  in_sfx_ = "_r";
+  tline(0, ls);
+  in_sfx_.clear();
+  l2e_copies();
+  par_on_ = par;
+  for (int j = 0; j < L_.period; ++j) {
+    if (!geo(j) || !t_.active[L_.start + j] || !p_.adjoints) continue;
+    const int init = L_.carry_init[j];
+    for (int m = mlo_; m < mhi_; ++m) {
+      m_ = m;
+      o_ << "    const real c0_" << j << ms(true) << " = " << (init >= 0 ? vname(init) : zero) << ";\n";
+      if (!gaff(j)) continue;
+      // the loop leaves these tangents at their start values
+      for (int k : posdeplist(j)) {
+        const std::string tin = init >= 0 ? inv_tname(init, k) : "";
+        o_ << "    ts" << j << "_" << k << ms(true) << " = " << (tin.empty() ? zero : tin == "#1" ? one : tin) << ";\n";
       }
     }
   }
@@ -3102,6 +3313,7 @@ std::string Emitter::run() {
   plan_geo_sums();
   plan_geo_logs();
   plan_fused_exponents();
+  plan_geo_affine();
   par_on_ = false;
   preamble();
   kernel(false);

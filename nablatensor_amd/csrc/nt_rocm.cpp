@@ -303,6 +303,44 @@ int decline_spill(const nt_exec_info& info, const nt_options* opt) {
   return fail(NT_E_UNSUPPORTED, buf);
 }
 
+// Compiles the lowered replay kernel. A kernel at one wave per SIMD cannot
+// hide the latency of its own dependent fp64 instructions (the VALU issues on
+// about half the cycles); one that needs at most 16 VGPRs more than two waves
+// allow (256) is compiled again with launch bounds asking for two, and that
+// code is kept when it fits without scratch (the 16-asset worst-of in fp64:
+// 270 VGPRs, one wave, 9.07 ms; 254 VGPRs, two waves, 7.12 ms). An explicit
+// nt_options.waves is left as asked.
+int compile_replay(const nt_tape* tape, const nt_options* options, Lowered& low, std::vector<char>& code,
+                   nt_exec_info& info) {
+  double secs = 0;
+  int rc = compile_hiprtc(low.source, false, code, secs);
+  if (rc != NT_OK) return rc;
+  fill_static_info(low, info);
+  kernel_resources(code, "nt_replay", info);
+  info.compile_seconds = secs;
+  const bool asked = options && options->waves > 0;
+  if (asked || info.vgprs <= 256 || info.vgprs > 256 + 16) return NT_OK;
+  nt_options o = options ? *options : nt_options{};
+  o.waves = 2;
+  Lowered low2;
+  std::vector<char> code2;
+  double secs2 = 0;
+  if (lower(tape, &o, low2) != NT_OK || compile_hiprtc(low2.source, false, code2, secs2) != NT_OK) {
+    (void)fail(NT_OK, std::string());  // the first compile stands; drop the retry's message
+    return NT_OK;
+  }
+  nt_exec_info info2{};
+  fill_static_info(low2, info2);
+  kernel_resources(code2, "nt_replay", info2);
+  info.compile_seconds += secs2;
+  if (info2.scratch_bytes != 0 || info2.vgprs < 0 || info2.vgprs > 256) return NT_OK;
+  info2.compile_seconds = info.compile_seconds;
+  low = std::move(low2);
+  code = std::move(code2);
+  info = info2;
+  return NT_OK;
+}
+
 // A kernel the module may or may not hold (the exception kernel): null when absent.
 hipFunction_t optional_function(hipModule_t mod, const char* name) {
   hipFunction_t fn = nullptr;
@@ -471,13 +509,9 @@ int nt_compile_check(const nt_tape* tape, const nt_options* options, nt_exec_inf
   int rc = lower(tape, options, l);
   if (rc != NT_OK) return rc;
   std::vector<char> code;
-  double secs = 0;
-  rc = compile_hiprtc(l.source, false, code, secs);
-  if (rc != NT_OK) return rc;
   nt_exec_info res{};
-  fill_static_info(l, res);
-  kernel_resources(code, "nt_replay", res);
-  res.compile_seconds = secs;
+  rc = compile_replay(tape, options, l, code, res);
+  if (rc != NT_OK) return rc;
   if (info) *info = res;
   return decline_spill(res, options);
 }
@@ -492,12 +526,8 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   if (rc != NT_OK) return rc;
   rc = device_index(x->dev);
   if (rc != NT_OK) return rc;
-  double secs = 0;
-  rc = compile_hiprtc(x->low.source, false, x->code, secs);
+  rc = compile_replay(tape, options, x->low, x->code, x->info);
   if (rc != NT_OK) return rc;
-  fill_static_info(x->low, x->info);
-  kernel_resources(x->code, "nt_replay", x->info);
-  x->info.compile_seconds = secs;
   rc = decline_spill(x->info, options);
   if (rc != NT_OK) return rc;
   NT_HIP(hipModuleLoadData(&x->mod, x->code.data()), "hipModuleLoadData");

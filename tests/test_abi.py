@@ -113,6 +113,17 @@ def test_offline_gfx950_compile_has_no_scratch(rocm, tapes, name, precision):
     assert 0 < info["vgprs"] <= 512
 
 
+def test_one_wave_kernel_near_two_waves_is_compiled_for_two(rocm, tapes):
+    """A replay kernel that needs a little more than two waves' 256 VGPRs
+    (the 16-asset worst-of in fp64: 270) runs one wave per SIMD; the engine
+    compiles it again with launch bounds asking for two and keeps that code,
+    which fits without scratch. An explicit waves option is left as asked."""
+    info = rocm.compile_check(tapes["C5"], rocm.options("fp64"))
+    assert info["scratch_bytes"] == 0 and 0 < info["vgprs"] <= 256, info
+    one = rocm.compile_check(tapes["C5"], rocm.options("fp64", waves=1))
+    assert one["scratch_bytes"] == 0 and 256 < one["vgprs"] <= 256 + 16, one
+
+
 def test_spilling_kernel_is_declined(rocm, nt):
     """A kernel that would spill to scratch is declined with NT_E_UNSUPPORTED,
     as the reference's engines decline a tape in compile() (AadEngine.java:50-59),

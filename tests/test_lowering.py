@@ -241,11 +241,11 @@ def test_emulated_own_math_within_1e12(rocm, tapes, name, paths, mode):
 
 
 @pytest.mark.parametrize("mode", [1, 2])
-@pytest.mark.parametrize("name", ["C2", "C3"])
-def test_emulated_fp32_tracks_fp32_oracle(rocm, tapes, name, mode):
+@pytest.mark.parametrize("name,paths", [("C2", 300), ("C3", 300), ("C5", 40)])
+def test_emulated_fp32_tracks_fp32_oracle(rocm, tapes, name, paths, mode):
     flat = tapes[name]
-    sums, v, g = run_emulated(flat, rocm.options("fp32", mode=mode), 300, rocm=rocm)
-    ov, og = oracle.replay_paths(flat, 300, OFFSET, 42, f32=True, threads=1)
+    sums, v, g = run_emulated(flat, rocm.options("fp32", mode=mode), paths, rocm=rocm)
+    ov, og = oracle.replay_paths(flat, paths, OFFSET, 42, f32=True, threads=1)
     assert rel_err(v, ov) < 2e-4
     assert rel_err(g, og) < 2e-3
 
@@ -752,24 +752,33 @@ def test_step_schedule_computed_once_per_block_and_pairs_aligned(rocm, tapes):
 
 
 def test_exp_factor_carries_sum_their_exponents(rocm, tapes):
-    """A carry kept as G alone whose factor is exp(x) (the worst-of's 16 spots)
-    adds its step exponents (gq = gs + x) and takes one exponential after the
-    loop, in the fast pass only; a carry whose G is read every step (the
-    Asian spot, summed into the average) keeps the product, and so does the
+    """A carry kept as G alone whose factor is exp(p + r s), p and r
+    loop-invariant and s a correlated normal (the worst-of's 16 spots), adds s
+    alone each step (zq = zs + s); after the loop the exponents' sum is
+    N p + r S and one exponential follows, in the fast pass only. Without the
+    static bound on s (device libm) the fp64 kernel adds the exponents
+    themselves (gq = gs + x). A carry whose G is read every step (the Asian
+    spot, summed into the average) keeps the product, and so does the
     barrier's survival product (its factor is 1 / b, not an exponential)."""
     for prec in ("fp64", "fp32"):
         src = rocm.lower(tapes["C5"], rocm.options(prec, mode=2))
         fast = src[:src.index("nt_replay_slow")]
-        logged = set(re.findall(r"real gq0_(\d+) = gs\1 \+ ", fast))
-        assert len(logged) == 16, prec
+        summed = set(re.findall(r"real zq0_(\d+) = zs\1 \+ r0_\d+;", fast))
+        assert len(summed) == 16, prec
+        assert not re.search(r"real gq0_\d+ = gs\d+ \+ ", fast)
         exp_after = r"nt_hw_exp2f\(gs{0}\)" if prec == "fp32" else r"nt_exp_fast\(gs{0}, nt_slow\)"
-        for j in logged:
+        fma = "fmaf" if prec == "fp32" else "fma"
+        for j in summed:
+            assert re.search(r"gs{0} = {1}\(\S+, zs{0}, \(0x1\.f8p\+7f?\) \* \S+\);".format(j, fma), fast), (prec, j)
             assert re.search(r"gs{0} = ".format(j) + exp_after.format(j), fast), (prec, j)
         slow = src[src.index("nt_replay_slow"):]
-        assert not re.search(r"real gq0_\d+ = gs\d+ \+ ", slow)
+        assert not re.search(r"real (gq|zq)0_\d+ = (gs|zs)\d+ \+ ", slow)
+    src = rocm.lower(tapes["C5"], rocm.options("fp64", mode=2, libm=1))
+    fast = src[:src.index("nt_replay_slow")]
+    assert len(set(re.findall(r"real gq0_(\d+) = gs\1 \+ ", fast))) == 16 and "zq0_" not in fast
     for name in ("C2", "C3", "C4"):
         src = rocm.lower(tapes[name], rocm.options("fp64", mode=2))
-        assert not re.search(r"real gq0_\d+ = gs\d+ \+ ", src), name
+        assert not re.search(r"real (gq|zq)0_\d+ = (gs|zs)\d+ \+ ", src), name
 
 
 @pytest.mark.parametrize("fixings", [63, 64])
