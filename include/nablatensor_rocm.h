@@ -93,8 +93,10 @@ typedef struct nt_options {
   int32_t roll;             /* 1 (default): roll the step loop when one is found; -1: never */
   int32_t contract;         /* FMA contraction of the tape's own products and sums: 0 default (off for fp64, on for
                                fp32, plus the fused exponent of a step's multiplicative carry, whose value is
-                               rebuilt from a product of factors anyway), 1 on, -1 off (every product and sum of a
-                               node rounded separately). The skeleton's math routines and the tangent rules use
+                               rebuilt from a product of factors anyway, the fp64 tangent loop's sums of products
+                               of values with no tangent, such as correlated normals, and a carry's exponent sum
+                               taken as N p + r S after the loop), 1 on, -1 off (every product and sum of a node
+                               rounded separately). The skeleton's math routines and the tangent rules use
                                explicit fma either way */
   int32_t libm;             /* fp64 Box-Muller: 0 the skeleton's own log/sqrt/sincos, 1 device libm, 2 own log/sqrt + libm sincos */
   int32_t mode;             /* NT_MODE_* */

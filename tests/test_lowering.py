@@ -629,18 +629,22 @@ def test_parameter_basis_on_assorted_tapes(nt, rocm):
         assert eg.max() <= 1e-12, o
 
 
+@pytest.mark.parametrize("name", ["C2", "C5"])
 @pytest.mark.parametrize("precision", ["fp64", "fp32"])
-def test_contract_off_emits_no_fused_node_value(tapes, precision):
+def test_contract_off_emits_no_fused_node_value(tapes, precision, name):
     """contract=-1 keeps every product and sum of a tape node separately
-    rounded: the fused exponent of a G-carried step factor (an explicit fma in
-    the default kernel) becomes a rounded product and sum again."""
+    rounded: the fused exponent of a G-carried step factor and the worst-of's
+    correlated normals (explicit fmas in the default kernel) become rounded
+    products and sums again, and the worst-of's spots sum their exponents
+    step by step instead of their normals."""
     from nablatensor_amd import rocm
     fused = re.compile(r"const real r\d+_\d+\w* = .*fmaf?\(")
-    default = rocm.lower(tapes["C2"], rocm.options(precision))
-    off = rocm.lower(tapes["C2"], rocm.options(precision, contract=-1))
+    default = rocm.lower(tapes[name], rocm.options(precision))
+    off = rocm.lower(tapes[name], rocm.options(precision, contract=-1))
     assert any(fused.search(line) for line in default.splitlines())
     assert not any(fused.search(line) for line in off.splitlines())
     assert "#pragma clang fp contract(off)" in off
+    assert ("zq0_" in default) == (name == "C5") and "zq0_" not in off
 
 
 @pytest.mark.parametrize("mode", [1, 2])
