@@ -2576,6 +2576,7 @@ void Emitter::plan_exp_bounds() {
     ExpBound b;
     if (scaled_draw(a, b.r)) {
       b.on = true;
+      b.mul = a;
     } else if (t_.op[L_.start + a] == NT_OP_ADD || t_.op[L_.start + a] == NT_OP_SUB) {
       for (int side = 0; side < 2 && !b.on; ++side) {
         const int ik = side ? L_.kind_b[a] : L_.kind_a[a], ir = side ? L_.ref_b[a] : L_.ref_a[a];

@@ -412,3 +412,31 @@ def discounted_weekday_asian_tape(nt, fixings: int = 252):
             acc = acc.add(s.div(b))
         rec.output(acc.mul(1.0 / fixings).sub(k).max(rec.constant(0.0)))
     return nt.AadRecorder.record(body).flat()
+
+
+def signed_basket_tape(nt, steps=40):
+    """Three GBM spots read only by the payoff, each step's exponent in one of
+    the signed affine forms of a draw: p - r w (w = 0.6 z1 + 0.8 z2, a
+    correlated normal), r z1 - p and r z2 alone, with p and r computed from
+    the inputs before the steps; payoff max(a + b + c - K, 0)."""
+    dt = 1.0 / steps
+
+    def body(rec):
+        sa, sb, sc = rec.input("Sa", 100.0), rec.input("Sb", 90.0), rec.input("Sc", 110.0)
+        va, vb, vc = rec.input("sa", 0.2), rec.input("sb", 0.3), rec.input("sc", 0.25)
+        rate = rec.input("r", 0.03)
+        pa = rate.sub(va.mul(va).mul(0.5)).mul(dt)
+        ra = va.mul(dt ** 0.5)
+        pb = vb.mul(vb).mul(0.5).sub(rate).mul(dt)
+        rb = vb.mul(dt ** 0.5)
+        rc = vc.mul(dt ** 0.5)
+        a, b, c = sa, sb, sc
+        for _ in range(steps):
+            z1 = rec.randn()
+            z2 = rec.randn()
+            w = z1.mul(0.6).add(z2.mul(0.8))
+            a = a.mul(pa.sub(ra.mul(w)).exp())
+            b = b.mul(rb.mul(z1).sub(pb).exp())
+            c = c.mul(rc.mul(z2).exp())
+        rec.output(a.add(b).add(c).sub(300.0).max(rec.constant(0.0)))
+    return nt.AadRecorder.record(body).flat()

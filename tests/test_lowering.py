@@ -818,3 +818,28 @@ def test_discounted_weekday_asian_reads_its_growth_from_the_schedule(rocm, nt):
         check_per_path(v, g, flat, 150, OFFSET, 42, min_strict=0.85)  # measured 0.873
         # (the rate's pathwise sensitivity of a discounted average nearly cancels: floor 1)
         assert rel_err(sums, oracle.replay_sums(flat, 150, OFFSET, 42, threads=1), floor=1.0) <= 1e-12
+
+
+@pytest.mark.parametrize("precision", ["fp64", "fp32"])
+def test_signed_affine_exponents_summed_after_the_loop(rocm, nt, precision):
+    """Spots whose step exponents are p - r w (w a correlated normal), r z - p
+    and r z: each step adds its draw alone and N p + r S, with the signs, and
+    the tangents follow the loop (fp32 folds exp(r z) into exp2 and sums it
+    so; its signed forms keep their step exponents). Per path within the bar
+    of the oracle (fp64, own math), within fp32 rounding of the fp32 oracle."""
+    from conftest import signed_basket_tape
+    flat = signed_basket_tape(nt, 40)
+    src = rocm.lower(flat, rocm.options(precision, mode=2))
+    fast = src[:src.index("nt_replay_slow")]
+    summed = len(set(re.findall(r"real zq0_(\d+) = zs\1 \+ ", fast)))
+    assert summed == (3 if precision == "fp64" else 1), precision
+    if precision == "fp64":
+        assert re.search(r"gs\d+ = fma\(-v\d+, zs\d+, \(0x1\.4p\+5\) \* v\d+\);", fast)
+        assert re.search(r"gs\d+ = fma\(v\d+, zs\d+, \(0x1\.4p\+5\) \* -v\d+\);", fast)
+    assert re.search(r"gs\d+ = v\d+(_l2e)? \* zs\d+;", fast)
+    _, v, g = run_emulated(flat, rocm.options(precision, mode=2), 200, rocm=rocm)
+    if precision == "fp64":
+        check_per_path(v, g, flat, 200, OFFSET, 42, min_strict=0.9)
+    else:
+        ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, f32=True, threads=1)
+        assert rel_err(v, ov) < 2e-4 and rel_err(g, og) < 2e-3
