@@ -66,10 +66,16 @@ def test_per_path_fp64_heston_many_paths(rocm, tapes, mode):
 
 @pytest.mark.parametrize("mode", [1, 2])
 def test_per_path_fp64_worst_of_matches_oracle(rocm, tapes, mode):
+    """The worst-of per path in both modes; its fp64 tangent kernel is the one
+    compiled again for two waves per SIMD (at most 256 VGPRs, no scratch)."""
     t = tapes["C5"]
     print(f"case C5 mode={mode} paths=256", flush=True)
     with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         v, g = x.replay_paths(256, 7, 42)
+        info = x.info()
+        if mode == 2:
+            assert info["vgprs"] <= 256 and info["scratch_bytes"] == 0, info
+            assert "__launch_bounds__(256, 2)" in x.source()
     print(check_per_path(v, g, t, 256, 7, 42, min_strict=STRICT["C5"]))
 
 
