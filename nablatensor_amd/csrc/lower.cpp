@@ -1304,14 +1304,23 @@ class Emitter {
     const int ka = L_.kind_a[pos], ra = L_.ref_a[pos];
     return (ka == ARG_BODY && is_one(L_.start + ra)) || (ka == ARG_INV && is_one(ra));
   }
-  // fp32 tangent loops: exp(p + r s) (or exp(r s)) with p and r loop-invariant
-  // and the sum and product used nowhere else becomes exp2(p' + r' s) with
+  // fp32 tangent loops: exp(p + r s), exp(p - r s), exp(r s - p) (or exp(r s))
+  // with p and r loop-invariant and the sum (difference) and product used
+  // nowhere else becomes exp2(p' + r' s) (signs kept) with
   // p' = p log2(e) and r' = r log2(e) computed once per path, dropping the
   // per-step multiply by log2(e) that the hardware exp2 otherwise needs.
   struct Exp2Fold {
     bool on = false;
     int p = -1, r = -1;          // invariant nodes (p = -1: no sum)
     int s_kind = ARG_NONE, s_ref = -1;
+    bool neg_p = false, neg_r = false;  // r s - p, p - r s
+    // p' + r' s with the signs, as an fp32 expression
+    std::string arg(const std::string& lp, const std::string& lr, const std::string& sv, bool fuse) const {
+      const std::string r = (neg_r ? "-" : "") + lr;
+      if (p < 0) return r + " * " + sv;
+      const std::string q = (neg_p ? "-" : "") + lp;
+      return fuse ? "fmaf(" + r + ", " + sv + ", " + q + ")" : r + " * " + sv + " + " + q;
+    }
   };
   std::vector<Exp2Fold> fold_;  // per loop position
   void plan_exp2_folds();
@@ -2122,9 +2131,7 @@ void Emitter::tsegment(int U, const std::string& sg) {
         if (op == NT_OP_EXP && fold_[j].on) {
           const Exp2Fold& f = fold_[j];
           const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
-          const std::string arg = !p_.fuse ? l2e_name(f.r) + " * " + sv + " + " + l2e_name(f.p)
-                                           : "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")";
-          val = "nt_hw_exp2f(" + (f.p >= 0 ? arg : l2e_name(f.r) + " * " + sv) + ")";
+          val = "nt_hw_exp2f(" + f.arg(f.p >= 0 ? l2e_name(f.p) : "", l2e_name(f.r), sv, p_.fuse) + ")";
         }
         sqrt_q_.clear();
         if (op == NT_OP_SQRT && fast_sqrt() && !slow_) {
@@ -2396,9 +2403,7 @@ std::string Emitter::geo_factor_exponent(int u, int j) const {
   if (fold_[e].on) {
     const Exp2Fold& f = fold_[e];
     const std::string sv = body_value(u, f.s_kind, f.s_ref, false);
-    if (f.p < 0) return l2e_name(f.r) + " * " + sv;
-    return !p_.fuse ? l2e_name(f.r) + " * " + sv + " + " + l2e_name(f.p)
-                    : "fmaf(" + l2e_name(f.r) + ", " + sv + ", " + l2e_name(f.p) + ")";
+    return f.arg(f.p >= 0 ? l2e_name(f.p) : "", l2e_name(f.r), sv, p_.fuse);
   }
   return body_value(u, L_.kind_a[e], L_.ref_a[e], false);
 }
@@ -2434,6 +2439,8 @@ void Emitter::plan_geo_affine() {
       g.r = f.r;
       g.s_kind = f.s_kind;
       g.s_ref = f.s_ref;
+      g.neg_p = f.neg_p;
+      g.neg_r = f.neg_r;
     } else {
       const ExpBound& b = bound_[e];
       if (!b.on) continue;
@@ -2493,13 +2500,16 @@ void Emitter::plan_exp2_folds() {
     const int a = L_.ref_a[j];
     Exp2Fold f;
     int mul = -1;
-    if (t_.op[L_.start + a] == NT_OP_ADD) {
+    if (t_.op[L_.start + a] == NT_OP_ADD || t_.op[L_.start + a] == NT_OP_SUB) {
+      const bool sub = t_.op[L_.start + a] == NT_OP_SUB;
       for (int side = 0; side < 2 && mul < 0; ++side) {
         const int ik = side ? L_.kind_b[a] : L_.kind_a[a], ir = side ? L_.ref_b[a] : L_.ref_a[a];
         const int mk = side ? L_.kind_a[a] : L_.kind_b[a], mr = side ? L_.ref_a[a] : L_.ref_b[a];
         if (ik == ARG_INV && mk == ARG_BODY && t_.op[L_.start + mr] == NT_OP_MUL && body_only(mr)) {
           f.p = ir;
           mul = mr;
+          f.neg_r = sub && side == 0;  // p - r s
+          f.neg_p = sub && side == 1;  // r s - p
         }
       }
     } else if (t_.op[L_.start + a] == NT_OP_MUL) {

@@ -417,7 +417,8 @@ def test_discounted_weekday_asian_growth_from_the_schedule(rocm, nt):
 def test_signed_affine_exponents_on_device(rocm, nt):
     """Spots whose step exponents are p - r w (w a correlated normal), r z - p
     and r z, summed as their draws and formed after the loop: per path within
-    the bar (fp64), sums within 1e-10 of the oracle's."""
+    the bar (fp64), sums within 1e-10 of the oracle's; fp32 (exponents folded
+    into exp2) reconciles with the fp64 oracle."""
     from conftest import signed_basket_tape
     flat = signed_basket_tape(nt, 40)
     print("case signed basket, 40 steps fp64 tangent, 2048 paths", flush=True)
@@ -426,7 +427,15 @@ def test_signed_affine_exponents_on_device(rocm, nt):
         v, g = x.replay_paths(2048, OFFSET, 42)
         sums, _ = x.replay(2048, OFFSET, 42)
     print(check_per_path(v, g, flat, 2048, OFFSET, 42, min_strict=0.9))
+    ref = oracle.replay_sums(flat, 20_000, OFFSET, 42)
     assert rel_err(sums, oracle.replay_sums(flat, 2048, OFFSET, 42), floor=1.0) <= 1e-10
+    print("case signed basket, 40 steps fp32 tangent, 20000 paths", flush=True)
+    with rocm.Executable(flat, rocm.options("fp32", mode=2)) as x:
+        assert x.source().count("real zq0_") >= 3
+        sums, _ = x.replay(20_000, OFFSET, 42)
+    errs = reconcile(sums, ref, 20_000, flat, 42, offset=OFFSET)
+    print(errs)
+    assert errs["ok"], errs
 
 
 def _line_tape(nt, tapes, name):

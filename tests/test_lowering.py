@@ -824,18 +824,18 @@ def test_discounted_weekday_asian_reads_its_growth_from_the_schedule(rocm, nt):
 def test_signed_affine_exponents_summed_after_the_loop(rocm, nt, precision):
     """Spots whose step exponents are p - r w (w a correlated normal), r z - p
     and r z: each step adds its draw alone and N p + r S, with the signs, and
-    the tangents follow the loop (fp32 folds exp(r z) into exp2 and sums it
-    so; its signed forms keep their step exponents). Per path within the bar
-    of the oracle (fp64, own math), within fp32 rounding of the fp32 oracle."""
+    the tangents follow the loop (fp32: exponents folded into exp2, in log2
+    units). Per path within the bar of the oracle (fp64, own math), within
+    fp32 rounding of the fp32 oracle."""
     from conftest import signed_basket_tape
     flat = signed_basket_tape(nt, 40)
     src = rocm.lower(flat, rocm.options(precision, mode=2))
     fast = src[:src.index("nt_replay_slow")]
     summed = len(set(re.findall(r"real zq0_(\d+) = zs\1 \+ ", fast)))
-    assert summed == (3 if precision == "fp64" else 1), precision
-    if precision == "fp64":
-        assert re.search(r"gs\d+ = fma\(-v\d+, zs\d+, \(0x1\.4p\+5\) \* v\d+\);", fast)
-        assert re.search(r"gs\d+ = fma\(v\d+, zs\d+, \(0x1\.4p\+5\) \* -v\d+\);", fast)
+    assert summed == 3, precision
+    fma, n, l2e = ("fma", r"\(0x1\.4p\+5\)", "") if precision == "fp64" else ("fmaf", r"\(0x1\.4p\+5f\)", "_l2e")
+    assert re.search(r"gs\d+ = {0}\(-v\d+{2}, zs\d+, {1} \* v\d+{2}\);".format(fma, n, l2e), fast)
+    assert re.search(r"gs\d+ = {0}\(v\d+{2}, zs\d+, {1} \* -v\d+{2}\);".format(fma, n, l2e), fast)
     assert re.search(r"gs\d+ = v\d+(_l2e)? \* zs\d+;", fast)
     _, v, g = run_emulated(flat, rocm.options(precision, mode=2), 200, rocm=rocm)
     if precision == "fp64":
