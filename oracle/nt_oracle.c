@@ -175,6 +175,21 @@ static int validate(const nto_tape *t) {
   return 0;
 }
 
+/* Planted mistakes: a build with -DNTO_PLANT=n (1..12) gets reverse rule n
+ * wrong, in the way listed below; the default build (NTO_PLANT 0) has none.
+ * tests/test_oracle_plants.py builds each one and checks that the oracle's
+ * pins (central differences, the barrier bump) reject it.
+ *   1 ADD: second operand's adjoint subtracted   7 EXP: d * v_a for d * v_i
+ *   2 SUB: second operand's adjoint added        8 LOG: d / v_i for d / v_a
+ *   3 MUL: d * v_a for d * v_b on a              9 SQRT: d * 0.5 * v_i
+ *   4 DIV: first operand's sign flipped         10 ABS: sign of v_a inverted
+ *   5 DIV: second operand's sign flipped        11 MAX: the smaller operand
+ *   6 NEG: adjoint added, not subtracted        12 MIN: the larger operand */
+#ifndef NTO_PLANT
+#define NTO_PLANT 0
+#endif
+#define PLANTED(k) (NTO_PLANT == (k))
+
 /* The adjoint add of ScalarReplay.add, ScalarReplay.java:177-183. */
 static inline void adj_add(double *d, int32_t node, double contribution, int f32) {
   if (f32) {
@@ -257,20 +272,23 @@ static void run_range(const nto_tape *t, const uint8_t *active, const double *in
         }
         int32_t a = t->arg_a[i], b = t->arg_b[i];
         switch (t->op[i]) {
-          case NTO_ADD: adj_add(d, a, adjoint, f32); adj_add(d, b, adjoint, f32); break;
-          case NTO_SUB: adj_add(d, a, adjoint, f32); adj_add(d, b, -adjoint, f32); break;
-          case NTO_MUL: adj_add(d, a, adjoint * v[b], f32); adj_add(d, b, adjoint * v[a], f32); break;
-          case NTO_DIV:
-            adj_add(d, a, adjoint / v[b], f32);
-            adj_add(d, b, -adjoint * v[i] / v[b], f32);
+          case NTO_ADD: adj_add(d, a, adjoint, f32); adj_add(d, b, PLANTED(1) ? -adjoint : adjoint, f32); break;
+          case NTO_SUB: adj_add(d, a, adjoint, f32); adj_add(d, b, PLANTED(2) ? adjoint : -adjoint, f32); break;
+          case NTO_MUL:
+            adj_add(d, a, adjoint * (PLANTED(3) ? v[a] : v[b]), f32);
+            adj_add(d, b, adjoint * v[a], f32);
             break;
-          case NTO_NEG: adj_add(d, a, -adjoint, f32); break;
-          case NTO_EXP: adj_add(d, a, adjoint * v[i], f32); break;
-          case NTO_LOG: adj_add(d, a, adjoint / v[a], f32); break;
-          case NTO_SQRT: adj_add(d, a, adjoint * 0.5 / v[i], f32); break;
-          case NTO_ABS: adj_add(d, a, v[a] < 0.0 ? -adjoint : adjoint, f32); break;
-          case NTO_MAX: adj_add(d, v[a] >= v[b] ? a : b, adjoint, f32); break;
-          case NTO_MIN: adj_add(d, v[a] <= v[b] ? a : b, adjoint, f32); break;
+          case NTO_DIV:
+            adj_add(d, a, PLANTED(4) ? -adjoint / v[b] : adjoint / v[b], f32);
+            adj_add(d, b, PLANTED(5) ? adjoint * v[i] / v[b] : -adjoint * v[i] / v[b], f32);
+            break;
+          case NTO_NEG: adj_add(d, a, PLANTED(6) ? adjoint : -adjoint, f32); break;
+          case NTO_EXP: adj_add(d, a, adjoint * (PLANTED(7) ? v[a] : v[i]), f32); break;
+          case NTO_LOG: adj_add(d, a, adjoint / (PLANTED(8) ? v[i] : v[a]), f32); break;
+          case NTO_SQRT: adj_add(d, a, PLANTED(9) ? adjoint * 0.5 * v[i] : adjoint * 0.5 / v[i], f32); break;
+          case NTO_ABS: adj_add(d, a, (v[a] < 0.0) != PLANTED(10) ? -adjoint : adjoint, f32); break;
+          case NTO_MAX: adj_add(d, (v[a] >= v[b]) != PLANTED(11) ? a : b, adjoint, f32); break;
+          case NTO_MIN: adj_add(d, (v[a] <= v[b]) != PLANTED(12) ? a : b, adjoint, f32); break;
           default: break;
         }
       }

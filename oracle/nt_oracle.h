@@ -26,8 +26,14 @@
  *
  * Parity pins (tests/test_oracle.py): Random123 KATs for the round function;
  * the reference-held Asian-call aggregates (docs/validation.md:56-63);
- * Black-Scholes closed form; knock-out + knock-in = vanilla; central
- * differences on small tapes; per-path hand evaluation of the 1-step European;
+ * Black-Scholes closed form; knock-out + knock-in = vanilla; per-path central
+ * differences with common random numbers for every reverse rule (European,
+ * Asian, Heston, a down-and-in barrier for DIV's second operand, a 16-asset
+ * worst-of for MIN, random tapes for ABS, LOG and the rest; tests/pins.py),
+ * each rule's planted mistake rejected (NTO_PLANT, tests/test_oracle_plants.py);
+ * the reference's barrier adjoint-delta bump test (ExoticsTest.java:81-94) and
+ * cash digital closed form (ExoticsTest.java:96-107);
+ * per-path hand evaluation of the 1-step European;
  * sums and standard error against the per-path rows (sample standard
  * deviation); the Merton jump tape (uniform draws) against the exact Poisson
  * series within 1.5% (JumpModelsTest.java:46-53), its no-jump limit against

@@ -7,6 +7,7 @@ never a fallback for it.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 import subprocess
 from pathlib import Path
@@ -37,23 +38,46 @@ def lib() -> C.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
-        L = C.CDLL(str(LIB_PATH))
-        L.nto_philox2x32_10.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint32)]
-        L.nto_normal.argtypes = [C.c_uint64, C.c_uint64, C.c_int32, C.c_int32]
-        L.nto_normal.restype = C.c_double
-        L.nto_uniform.argtypes = [C.c_uint64, C.c_uint64, C.c_int32, C.c_int32]
-        L.nto_uniform.restype = C.c_double
-        L.nto_mark_active.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_uint8)]
-        L.nto_replay.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64, C.c_uint64,
-                                 C.c_int, C.c_int, C.c_int, C.POINTER(_Totals)]
-        L.nto_replay_paths.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
-                                       C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
-                                       C.POINTER(C.c_double)]
-        L.nto_replay_paths_perturbed.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
-                                                 C.c_uint64, C.c_int, C.c_uint64, C.POINTER(C.c_double),
-                                                 C.POINTER(C.c_double)]
-        _lib = L
+        _lib = _bind(C.CDLL(str(LIB_PATH)))
     return _lib
+
+
+def build_planted(plant: int, out: Path) -> Path:
+    """Builds the oracle with planted mistake `plant` (NTO_PLANT in
+    nt_oracle.c: reverse rule `plant` made wrong) into `out`."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "planted", f"PLANT={int(plant)}", f"OUT={out}"], check=True)
+    return Path(out)
+
+
+@contextlib.contextmanager
+def library(path):
+    """Every call inside the block goes to the oracle build at `path` (a
+    planted-mistake build from build_planted); the default build after it."""
+    global _lib
+    saved = _lib
+    _lib = _bind(C.CDLL(str(path)))
+    try:
+        yield
+    finally:
+        _lib = saved
+
+
+def _bind(L: C.CDLL) -> C.CDLL:
+    L.nto_philox2x32_10.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint32)]
+    L.nto_normal.argtypes = [C.c_uint64, C.c_uint64, C.c_int32, C.c_int32]
+    L.nto_normal.restype = C.c_double
+    L.nto_uniform.argtypes = [C.c_uint64, C.c_uint64, C.c_int32, C.c_int32]
+    L.nto_uniform.restype = C.c_double
+    L.nto_mark_active.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_uint8)]
+    L.nto_replay.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64, C.c_uint64,
+                             C.c_int, C.c_int, C.c_int, C.POINTER(_Totals)]
+    L.nto_replay_paths.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
+                                   C.c_uint64, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                   C.POINTER(C.c_double)]
+    L.nto_replay_paths_perturbed.argtypes = [C.POINTER(_Tape), C.POINTER(C.c_double), C.c_uint64, C.c_uint64,
+                                             C.c_uint64, C.c_int, C.c_uint64, C.POINTER(C.c_double),
+                                             C.POINTER(C.c_double)]
+    return L
 
 
 class Tape:

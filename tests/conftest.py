@@ -97,6 +97,16 @@ SENS_PATTERNS = (1, 2, 3)
 # money: A - K with A near 100 loses two digits against the floor of 1) or,
 # in the Heston tape, whose variance grazes the full-truncation floor.
 STRICT = {"C1": 1.0, "C2": 0.94, "C3": 0.84, "C4": 0.80, "C5": 0.95}
+# Fraction of paths allowed above TOL on some component, per workload: the
+# count measured on MI355X with about 1.5x margin (C3: 1 of 1,024 paths;
+# C4: 30 of 4,096 and 3 of 512; none on C1, C2, C5 and the other tapes).
+ABOVE = {"C1": 0.0, "C2": 0.001, "C3": 0.002, "C4": 0.01, "C5": 0.004}
+# Error over sensitivity on the components held to SENS_K x s: measured on
+# MI355X (every per-path test, both modes) at most 1.53 at the 99th percentile
+# and 2.92 at the maximum; these bars keep a regression that stays inside
+# SENS_K x s from passing unseen.
+RATIO_P99 = 2.0
+RATIO_MAX = 4.0
 
 
 def componentwise_errors(values, grads, ref_values, ref_grads):
@@ -127,15 +137,19 @@ def path_sensitivity(flat, paths, offset, seed, inputs=None):
     return ov, og, sv, sg
 
 
-def check_per_path(values, grads, flat, paths, offset, seed, tol=TOL, min_strict=1.0, inputs=None):
+def check_per_path(values, grads, flat, paths, offset, seed, tol=TOL, min_strict=1.0, inputs=None,
+                   max_above=0.002):
     """Compares per-path values and derivatives with the oracle, component by
     component, under the sensitivity-scaled bound above. `min_strict` is the
     fraction of paths that must be held to `tol` on every component (their
     sensitivity is below tol / SENS_K), set at the measured fraction of the
     call's path sample: the fraction is a property of the oracle alone, and
     pinning it keeps the sensitivity measurement from excusing paths it did
-    not excuse when the bar was set. Returns a summary, with the normwise
-    gradient error (max_j |dg_j| / max(1, max_j |g_j|)) beside."""
+    not excuse when the bar was set. At most `max_above` of the paths (rounded
+    up) may exceed `tol` on any component, and on the components held to SENS_K x s
+    the error over s stays within RATIO_P99 at the 99th percentile and
+    RATIO_MAX at the worst. Returns a summary, with the normwise gradient
+    error (max_j |dg_j| / max(1, max_j |g_j|)) beside."""
     import oracle
     ov, og, sv, sg = path_sensitivity(flat, paths, offset, seed, inputs)
     ev, eg = componentwise_errors(values, grads, ov, og)
@@ -144,27 +158,37 @@ def check_per_path(values, grads, flat, paths, offset, seed, tol=TOL, min_strict
     strict = (bv == tol) & (np.all(bg == tol, axis=1) if bg.size else True)
     err = np.maximum(ev, eg.max(axis=1)) if eg.size else ev
     _, normwise = oracle.path_errors(values, grads, ov, og)
+    # error over sensitivity on the components held to SENS_K x s rather than tol
+    e_all = np.concatenate([ev.ravel(), eg.ravel()])
+    s_all = np.concatenate([sv.ravel(), sg.ravel()])
+    loose = SENS_K * s_all > tol
+    ratio = e_all[loose] / s_all[loose]
     out = {"paths": paths, "violations": int(np.sum(bad)), "strict_fraction": float(np.mean(strict)),
            "paths_above_tol": int(np.sum(err > tol)), "max_err": float(err.max()),
            "max_err_strict": float(err[strict].max()) if strict.any() else 0.0,
-           "max_normwise": float(normwise.max()) if normwise.size else 0.0}
+           "max_normwise": float(normwise.max()) if normwise.size else 0.0,
+           "loose_components": int(loose.sum()),
+           "ratio_p99": float(np.percentile(ratio, 99)) if ratio.size else 0.0,
+           "ratio_max": float(ratio.max()) if ratio.size else 0.0}
     assert out["violations"] == 0, out
     assert out["strict_fraction"] >= min_strict, out
+    assert out["paths_above_tol"] <= int(np.ceil(max_above * paths)), out
+    assert out["ratio_p99"] <= RATIO_P99 and out["ratio_max"] <= RATIO_MAX, out
     return out
 
 
-def reconcile(got_sums, want_sums, paths, flat, seed, offset=0, sample=20_000, rel=1e-5, in_se=0.05):
-    """fp32 against fp64 aggregates. The price within `rel` relative; each
-    Greek within max(rel |g_j|, in_se se_j), se_j the Greek's own Monte-Carlo
-    standard error at `paths` scenarios (from the oracle's per-path rows of the
-    first `sample` paths): an fp32 engine may differ by a negligible fraction
-    of the Monte-Carlo error the result carries anyway. That floor matters
-    where a path's derivative jumps between Greeks on a rounding-level change:
-    a worst-of path on which two assets end within fp32 rounding of each other
-    credits its delta and vega to the other one, about 1 / n of a per-path
-    Greek in absolute terms, far above 1e-5 of a small mean. Returns the
-    per-Greek relative errors, the errors in standard errors, the Greeks held
-    by the floor, the normwise error max_j |dg_j| / max_j |g_j|, and `ok`."""
+def reconcile(got_sums, want_sums, paths, flat, seed, offset=0, sample=20_000, rel=1e-5, in_se=0.0):
+    """fp32 against fp64 aggregates: the price and each Greek within `rel`
+    relative, and `rel` normwise. `in_se` > 0 would let a Greek off at
+    in_se x se_j instead, se_j its own Monte-Carlo standard error at `paths`
+    scenarios (from the oracle's per-path rows of the first `sample` paths);
+    no test uses it, and `within_se_floor` lists the Greeks above `rel` that
+    0.05 se_j would have excused (a worst-of path whose two lowest assets end
+    within fp32 rounding of each other credits its delta and vega to the other
+    one, about 1 / n of a per-path Greek in absolute terms, which can exceed
+    1e-5 of a small mean). Returns the per-Greek relative errors, the errors in
+    standard errors, those Greeks, the normwise error max_j |dg_j| / max_j
+    |g_j|, and `ok`."""
     import oracle
     got, want = oracle.to_result(got_sums, paths), oracle.to_result(want_sums, paths)
     _, rows = oracle.replay_paths(flat, min(paths, sample), offset, seed)
@@ -173,10 +197,11 @@ def reconcile(got_sums, want_sums, paths, flat, seed, offset=0, sample=20_000, r
     d = np.abs(g - w)
     rel_err = d / np.abs(w)
     in_se_err = d / se
-    by_floor = [int(j) for j in np.nonzero((rel_err > rel) & (in_se_err <= in_se))[0]]
+    by_floor = [int(j) for j in np.nonzero((rel_err > rel) & (in_se_err <= 0.05))[0]]
     out = {"price": abs(got["price"] - want["price"]) / abs(want["price"]),
-           "greek_rel_max": float(rel_err.max()), "greek_se_max": float(in_se_err.max()),
-           "held_by_se_floor": by_floor, "normwise": float(d.max() / np.abs(w).max())}
+           "greek_rel_max": float(rel_err.max()), "greek_worst": int(np.argmax(rel_err)),
+           "greek_se_max": float(in_se_err.max()), "within_se_floor": by_floor,
+           "normwise": float(d.max() / np.abs(w).max())}
     out["ok"] = bool(out["price"] <= rel and np.all(d <= np.maximum(rel * np.abs(w), in_se * se))
                      and out["normwise"] <= rel)
     return out

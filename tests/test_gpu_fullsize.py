@@ -7,9 +7,8 @@ minutes, so it checks the same kernels at smaller sizes in test_gpu_parity):
 * a dispatch split into two path ranges sums to the whole (exactly up to the
   fp64 summation order), which pins the counter keying at every path index;
 * the two derivative modes (reverse sweep and tangent) agree on every sum;
-* fp32 reconciles with the fp64 kernel within 1e-5 on the price and, per
-  Greek, within 1e-5 relative or 0.05 of the Greek's standard error
-  (conftest.reconcile);
+* fp32 reconciles with the fp64 kernel within 1e-5 relative on the price and
+  on every Greek (conftest.reconcile);
 * the same dispatch twice gives the same bits;
 * path offsets near 2^64 wrap exactly as the oracle's.
 """

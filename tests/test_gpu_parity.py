@@ -6,8 +6,8 @@ component (the value and each Greek, relative with floor 1) within
 max(1e-12, 8 x the oracle's own sensitivity to one-unit moves of its
 transcendental results) (conftest.check_per_path), with the fraction of paths
 held to 1e-12 itself pinned; sums over paths within 1e-10. fp32 reconciles with
-the fp64 oracle within 1e-5 on price and on each first-order Greek (floored at
-that Greek's standard error, conftest.reconcile). The reference-held aggregates of the Asian call
+the fp64 oracle within 1e-5 relative on price and on each first-order Greek
+(conftest.reconcile). The reference-held aggregates of the Asian call
 (docs/validation.md:56-63) are reproduced at their printed precision.
 """
 from __future__ import annotations
@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import STRICT, check_per_path, reconcile, rel_err
+from conftest import ABOVE, STRICT, check_per_path, reconcile, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -50,7 +50,7 @@ def test_per_path_fp64_matches_oracle(rocm, tapes, name, paths, mode, ckpt, libm
         info = x.info()
     assert info["scratch_bytes"] == 0
     assert info["mode"] == mode
-    summary = check_per_path(v, g, t, paths, OFFSET, 42, min_strict=STRICT[name])
+    summary = check_per_path(v, g, t, paths, OFFSET, 42, min_strict=STRICT[name], max_above=ABOVE[name])
     print(summary)
 
 
@@ -61,7 +61,7 @@ def test_per_path_fp64_heston_many_paths(rocm, tapes, mode):
     print(f"case C4 mode={mode} paths=4096 seed=7", flush=True)
     with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
         v, g = x.replay_paths(4096, OFFSET, 7)
-    print(check_per_path(v, g, t, 4096, OFFSET, 7, min_strict=STRICT["C4"]))
+    print(check_per_path(v, g, t, 4096, OFFSET, 7, min_strict=STRICT["C4"], max_above=ABOVE["C4"]))
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -76,7 +76,7 @@ def test_per_path_fp64_worst_of_matches_oracle(rocm, tapes, mode):
         if mode == 2:
             assert info["vgprs"] <= 256 and info["scratch_bytes"] == 0, info
             assert "__launch_bounds__(256, 2)" in x.source()
-    print(check_per_path(v, g, t, 256, 7, 42, min_strict=STRICT["C5"]))
+    print(check_per_path(v, g, t, 256, 7, 42, min_strict=STRICT["C5"], max_above=ABOVE["C5"]))
 
 
 @pytest.mark.parametrize("mode", [1, 2])
@@ -147,8 +147,7 @@ def test_worst_of_launches_past_2_pow_32_are_additive(rocm, tapes):
     reaches counter offsets past 2^32 from launch 4,295 on. Launches 4,294
     (which straddles 2^32) and 4,295 add up to one dispatch over both ranges,
     and 20,000 fp32 paths on either side of 2^32 reconcile with the fp64
-    oracle (price and each Greek within 1e-5, floored at the Greek's standard
-    error)."""
+    oracle (price and each Greek within 1e-5 relative)."""
     t = tapes["C5"]
     print("case C5 fp32 launches 4294, 4295 and 2^32 - 10^4", flush=True)
     with rocm.Executable(t, rocm.options("fp32")) as x:
@@ -296,14 +295,13 @@ def test_loop_tangents_over_inputs_and_parameters_on_device(rocm, tapes, name, p
         v, g = x.replay_paths(paths, OFFSET, 42)
         info = x.info()
     assert info["scratch_bytes"] == 0
-    print(check_per_path(v, g, t, paths, OFFSET, 42, min_strict=STRICT[name]))
+    print(check_per_path(v, g, t, paths, OFFSET, 42, min_strict=STRICT[name], max_above=ABOVE[name]))
 
 
 def test_worst_of_fp32_over_parameters_reconciles(rocm, tapes):
     """The fp32 worst-of kernel (tangents over the loop's parameters) against
-    the fp64 oracle over 20,000 paths: price within 1e-5 relative, each of the
-    33 Greeks within 1e-5 relative or 0.05 of its standard error, and 1e-5
-    normwise (conftest.reconcile)."""
+    the fp64 oracle over 20,000 paths: price and each of the 33 Greeks within
+    1e-5 relative, and 1e-5 normwise (conftest.reconcile)."""
     t = tapes["C5"]
     print("case C5 fp32 paths=20000", flush=True)
     src = rocm.lower(t, rocm.options("fp32", mode=2))
@@ -373,7 +371,7 @@ def test_step_schedule_recorded_up_front_on_device(rocm, mode):
 def test_step_schedule_per_block_fp32_and_a_tail_trip(rocm, nt):
     """The weekday Asian's tangent kernels with the step schedule computed once
     per block: fp32 reconciles with the fp64 oracle (price and each Greek within
-    1e-5, floored at the Greek's standard error); a 64-fixing grid (a lead step
+    1e-5 relative); a 64-fixing grid (a lead step
     and 31 trips of two) and a 400-fixing grid (399 loop steps, more than a
     block's 256 threads, so threads stride over the schedule's steps; a lead
     step, 199 trips and a tail of one) are per path within the bar in fp64."""
@@ -490,8 +488,7 @@ def test_checkpointed_straight_line_exception_kernel_on_device(rocm, nt):
 
 def test_checkpointed_straight_line_fp32_reconciles(rocm, tapes):
     """fp32, the 252-fixing Asian without its loop, reverse sweep in segments:
-    price and each Greek within 1e-5 of the fp64 oracle (floored at the
-    Greek's standard error)."""
+    price and each Greek within 1e-5 relative of the fp64 oracle."""
     t = tapes["C2"]
     paths = 200_000
     print(f"case straight line C2 fp32 paths={paths}", flush=True)

@@ -10,12 +10,16 @@
 * Invariants: knock-out + knock-in = vanilla (ExoticsTest.java:55-62), adjoint
   price = price-only price (ModelsTest.java:67-68), additivity of path ranges,
   thread-count independence.
-* Brute force: central differences with common random numbers on small tapes.
+* Brute force: central differences with common random numbers on small tapes,
+  per path, for every reverse rule (tests/pins.py); the reference's barrier
+  adjoint-delta bump test (ExoticsTest.java:81-94) and cash digital closed
+  form (ExoticsTest.java:96-107).
 * Uniforms and named streams: the keying restated in numpy, and the reference's
   own statistical checks (RandomStreamsTest.java: E[U] = 1/2, E[U^4] = 1/5,
   independent streams); several outputs: sums that follow from a scaled copy.
 A planted mistake in the oracle (sign of a reverse rule, a leg swap, an input
-order slip) fails at least one of these.
+order slip) fails at least one of these; tests/test_oracle_plants.py builds
+the oracle with each reverse rule made wrong in turn and checks exactly that.
 """
 from __future__ import annotations
 
@@ -25,6 +29,7 @@ import numpy as np
 import pytest
 
 import oracle
+import pins
 from conftest import equity_tape, reference_values, rel_err, workload_tapes
 
 
@@ -207,6 +212,27 @@ def test_adjoint_matches_central_difference(nt, tapes, name, idx, bump):
     smooth = (np.abs(vals) > 1e-3) & (np.abs(vu - vd) < 0.5)  # away from the payoff kink
     assert smooth.sum() > 10
     assert np.max(np.abs(fd[smooth] - grads[smooth, idx]) / np.maximum(1.0, np.abs(grads[smooth, idx]))) < 1e-5
+
+
+@pytest.mark.parametrize("name", list(pins.DERIVATIVE_CHECKS))
+def test_derivative_pins(nt, name):
+    """The oracle's adjoints against what fixes them from outside the reverse
+    sweep (tests/pins.py): per-path central differences with common random
+    numbers on the European, an 8-fixing Asian, a 6-step Heston-Asian, a
+    16-monitor down-and-in barrier (DIV's second operand), an 8-step worst-of
+    on 16 assets (MIN) and random tapes using every operation (ABS, LOG, MIN,
+    MAX, DIV), each at 1e-5 relative; and the reference's barrier
+    adjoint-delta test (ExoticsTest.java:81-94)."""
+    ok, detail = pins.DERIVATIVE_CHECKS[name](nt)
+    print(name, detail)
+    assert ok, detail
+
+
+def test_digital_matches_closed_form(nt):
+    """ExoticsTest.cashDigitalMatchesBlackScholes (ExoticsTest.java:96-107):
+    the smoothed cash digital within 0.03 of e^{-rT} N(d2)."""
+    ok, detail = pins.check_digital_closed_form(nt)
+    assert ok, detail
 
 
 def test_fp32_mode_rounds_every_node(tapes):
