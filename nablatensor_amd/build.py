@@ -58,7 +58,7 @@ def build_engine(force: bool = True) -> Path:
     out = PKG / "libnt_rocm.so"
     srcs = [CSRC / "nt_rocm.cpp", CSRC / "lower.cpp"]
     hip_src = CSRC / "nt_noalloc.hip"
-    deps = srcs + [hip_src, CSRC / "lower.hpp", CSRC / "nt_exec.hpp", CSRC / "nt_skeleton.h",
+    deps = srcs + [hip_src, CSRC / "lower.hpp", CSRC / "nt_exec.hpp", CSRC / "nt_testing.h", CSRC / "nt_skeleton.h",
                    CSRC / "nt_math_tables.h", inc, ROOT / "include" / "nablatensor_rocm.h"]
     if not force and _newer(out, deps):
         return out

@@ -2887,11 +2887,12 @@ void Emitter::preamble() {
 // Signature and prologue of the replay kernel (nt_replay) or of the exception
 // kernel (nt_replay_slow), up to the path variables of the grid-stride loop.
 // Both take `flags`: word 0 counts the lanes that left paths to the exception
-// kernel, then one bitmap per market, bit p of word p / 64 for the dispatch's
-// path p. The exception kernel returns at once when the count is zero (the
-// finishing pass then skips its rows); otherwise it visits only the paths
-// whose bit is set, and a block with none loads no tables and writes a zero
-// row of partials.
+// kernel, then one lane bitmap per market, T / 64 words each (bit tid % 64 of
+// word tid / 64; the two kernels run on the same grid). The exception kernel
+// returns at once when the count is zero (the finishing pass then skips its
+// rows); otherwise each lane takes its bit (clearing the bitmap behind it),
+// visits its paths only if the bit is set, and a block with no such lane loads
+// no tables and writes a zero row of partials.
 void Emitter::kernel_head(bool slow) {
   const int nin = t_.n_in;
   const int M = p_.markets;
@@ -2904,19 +2905,19 @@ void Emitter::kernel_head(bool slow) {
   o_ << "  const nt_u64 T = (nt_u64)gridDim.x * blockDim.x;\n";
   o_ << "  const nt_u64 tid = (nt_u64)blockIdx.x * blockDim.x + threadIdx.x;\n";
   if (slow) o_ << "  if (flags[0] == 0) return;  // no lane left a path to this kernel\n";
-  o_ << "  const nt_u64 nt_words = (n_paths + 63) >> 6;  // bitmap words per market\n";
+  o_ << "  const nt_u64 nt_words = T >> 6;  // lane bitmap words per market\n";
   o_ << "  nt_u64* __restrict__ nt_bits = flags + 1;\n";
   o_ << "  (void)scratch; (void)out_v; (void)out_g; (void)nt_bits; (void)nt_words;\n";
   const int nacc = p_.n_channels * M;
   o_ << "  double acc[" << nacc << "];\n";
   o_ << "  for (int c = 0; c < " << nacc << "; ++c) acc[c] = 0.0;\n";
   if (slow) {
-    o_ << "  int nt_any = 0;\n";
-    o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
-    o_ << "    nt_u64 w = 0;\n";
-    for (int m = 0; m < M; ++m) o_ << "    w |= nt_bits[" << m << "u * nt_words + (p >> 6)];\n";
-    o_ << "    nt_any |= (int)((w >> (p & 63)) & 1);\n";
-    o_ << "  }\n";
+    for (int m = 0; m < M; ++m) {
+      o_ << "  const bool nt_f" << m << " = nt_take_lane_flag(nt_bits + " << m << "u * nt_words, tid);\n";
+    }
+    o_ << "  const bool nt_any = nt_f0";
+    for (int m = 1; m < M; ++m) o_ << " || nt_f" << m;
+    o_ << ";\n";
     o_ << "  if (__syncthreads_or(nt_any)) {\n";
   }
   if (needs_tables()) o_ << "  nt_tables_load();\n";
@@ -2929,15 +2930,8 @@ void Emitter::kernel_head(bool slow) {
     for (int m = 0; m < M; ++m) o_ << "  bool nt_lane_bad" << m << " = false;\n";
   }
   if (!slow) schedule_prologue();
-  o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) {\n";
-  if (slow) {
-    for (int m = 0; m < M; ++m) {
-      o_ << "    const bool nt_f" << m << " = (nt_bits[" << m << "u * nt_words + (p >> 6)] >> (p & 63)) & 1;\n";
-    }
-    o_ << "    if (!(nt_f0";
-    for (int m = 1; m < M; ++m) o_ << " || nt_f" << m;
-    o_ << ")) continue;\n";
-  }
+  // a lane of the exception kernel with no flag visits no path
+  o_ << "  for (nt_u64 p = " << (slow ? "nt_any ? tid : n_paths" : "tid") << "; p < n_paths; p += T) {\n";
   o_ << "    const nt_u64 path = p + path_offset;\n";
   o_ << "    const nt_u32 rlo = (nt_u32)path ^ (nt_u32)seed;\n";
   o_ << "    const nt_u32 rhi = (nt_u32)(path >> 32) ^ (nt_u32)(seed >> 32);\n";
@@ -3297,8 +3291,7 @@ void Emitter::kernel(bool slow) {
         o_ << "  for (int c = " << c0 << "; c < " << c1 << "; ++c) " << bad << " |= !__builtin_isfinite(acc[c]);\n";
       }
       o_ << "  if (" << bad << ") {\n    for (int c = " << c0 << "; c < " << c1 << "; ++c) acc[c] = 0.0;\n  }\n";
-      o_ << "  for (nt_u64 p = tid; p < n_paths; p += T) nt_flag_paths(nt_bits + " << m << "u * nt_words, p, " << bad
-         << ");\n";
+      o_ << "  nt_flag_lanes(nt_bits + " << m << "u * nt_words, tid, " << bad << ");\n";
     }
     o_ << "  if (nt_lane_bad0";
     for (int m = 1; m < M; ++m) o_ << " || nt_lane_bad" << m;

@@ -94,9 +94,17 @@ int grid_for(const nt_exec* x, uint64_t paths);
 // Bytes per lane of the reverse sweep's tape (checkpoints and stored values).
 size_t tape_bytes_per_lane(const nt_exec* x);
 
-// Bytes of the flags of a dispatch over `paths` pricing `markets` input sets:
-// a 64-bit count, then one bit per path and set in 64-bit words.
-size_t flags_bytes_for(uint64_t paths, int markets);
+// Bytes of the flags of a dispatch on `lanes` threads (grid x block) pricing
+// `markets` input sets: a 64-bit count, then one bit per lane and set in
+// 64-bit words (one word per wave). The words must be zero before the first
+// dispatch; every dispatch leaves them zero.
+size_t flags_bytes_for(uint64_t lanes, int markets);
+
+// Looks up, once per device and with that device current, the address of
+// the allocation-free entry point's static array on device `dev`, and clears
+// its flag region there (nt_noalloc.hip). Called when an executable is
+// created, so that entry point itself never has to.
+int noalloc_prepare(int dev);
 
 // Partial rows a dispatch over `grid` blocks may write: the replay kernel's
 // and, when there is an exception kernel, as many again.

@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "lower.hpp"
+#include "nt_testing.h"
 #include "nt_exec.hpp"
 #include "skeleton_src.inc"
 
@@ -138,7 +139,13 @@ std::vector<std::string> compile_options(const std::string& src, bool dump) {
   return o;
 }
 
-int compile_hiprtc(const std::string& src, bool dump, std::vector<char>& code, double& seconds) {
+// Text appended to every program this thread compiles (nt_testing.h): lets a
+// test make hipRTC fail on a real lowering and check the error path. Empty in
+// every other use.
+thread_local std::string t_test_source_suffix;
+
+int compile_hiprtc(const std::string& lowered, bool dump, std::vector<char>& code, double& seconds) {
+  const std::string& src = t_test_source_suffix.empty() ? lowered : lowered + t_test_source_suffix;
   const auto t0 = std::chrono::steady_clock::now();
   const std::vector<std::string> opts = compile_options(src, dump);
   int major = 0, minor = 0;
@@ -417,8 +424,8 @@ size_t tape_bytes_per_lane(const nt_exec* x) {
   return static_cast<size_t>(x->low.plan.tape_slots) * elem;
 }
 
-size_t flags_bytes_for(uint64_t paths, int markets) {
-  return (1 + static_cast<size_t>((paths + 63) / 64) * static_cast<size_t>(std::max(1, markets))) * sizeof(uint64_t);
+size_t flags_bytes_for(uint64_t lanes, int markets) {
+  return (1 + static_cast<size_t>((lanes + 63) / 64) * static_cast<size_t>(std::max(1, markets))) * sizeof(uint64_t);
 }
 
 int partial_rows(int grid, bool has_slow) { return has_slow ? 2 * grid : grid; }
@@ -465,6 +472,8 @@ int launch_finish_on(hipStream_t stream, hipFunction_t fn, const double* d_parti
 extern "C" {
 
 int nt_abi_version(void) { return NT_ABI_VERSION; }
+
+void nt_testing_append_source(const char* text) { t_test_source_suffix = text ? text : ""; }
 
 const char* nt_last_error(void) { return ntr::last_error(); }
 
@@ -516,6 +525,8 @@ int nt_compile_check(const nt_tape* tape, const nt_options* options, nt_exec_inf
   return decline_spill(res, options);
 }
 
+static int ensure_flags(nt_exec* x, int grid, int markets);
+
 int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out) {
   if (!out) return fail(NT_E_INVALID, "out is null");
   *out = nullptr;
@@ -561,6 +572,12 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   const size_t scratch = ntr::tape_bytes_per_lane(x.get()) * x->grid_cap * x->low.plan.block;
   if (scratch > 0) NT_HIP(hipMalloc(&x->d_scratch, scratch), "hipMalloc(scratch)");
   x->scratch_bytes = scratch;
+  rc = ensure_flags(x.get(), x->grid_cap, 1);  // every single-set dispatch fits these
+  if (rc != NT_OK) return rc;
+  // the allocation-free entry point's array on this device, looked up and
+  // its flags cleared here rather than in a call that may be under capture
+  rc = ntr::noalloc_prepare(x->dev);
+  if (rc != NT_OK) return rc;
   // inputs default to zero until bound; the reference starts from the recorded values (Java side)
   x->inputs.assign(static_cast<size_t>(x->low.ir.n_in), 0.0);
   for (int j = 0; j < x->low.ir.n_in; ++j) x->inputs[j] = x->low.ir.c[x->low.ir.input_node[j]];
@@ -578,20 +595,23 @@ int nt_exec_set_inputs(nt_exec* x, const double* inputs, int32_t n) {
 
 using ntr::grid_for;
 
-// Grows the flag bitmap to a dispatch over `paths` pricing `markets` sets.
-// The stream is drained first: the old bitmap may still be in use.
-static int ensure_flags(nt_exec* x, uint64_t paths, int markets) {
-  const size_t need = ntr::flags_bytes_for(paths, markets);
+// Grows the flags to a dispatch on `grid` blocks pricing `markets` sets: a
+// size set by the grid (at most the resident cap), not by the paths, so it
+// grows at most a few times per executable. The stream is drained first (the
+// old flags may still be in use) and the new ones are zeroed whole: every
+// dispatch leaves the count and the bitmap at zero after that.
+static int ensure_flags(nt_exec* x, int grid, int markets) {
+  const uint64_t lanes = static_cast<uint64_t>(grid) * static_cast<uint64_t>(x->low.plan.block);
+  const size_t need = ntr::flags_bytes_for(lanes, markets);
   if (need <= x->flags_bytes) return NT_OK;
   NT_HIP(hipStreamSynchronize(x->stream), "hipStreamSynchronize");
+  const size_t bytes = std::max(need, x->flags_bytes + x->flags_bytes / 2);
   if (x->d_flags) (void)hipFree(x->d_flags);
   x->d_flags = nullptr;
   x->flags_bytes = 0;
-  const size_t bytes = std::max(need, x->flags_bytes + x->flags_bytes / 2);
   NT_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_flags), bytes), "hipMalloc(flags)");
   x->flags_bytes = bytes;
-  // the count starts at zero; every finishing pass leaves it there
-  NT_HIP(hipMemsetAsync(x->d_flags, 0, sizeof(uint64_t), x->stream), "hipMemsetAsync(flags)");
+  NT_HIP(hipMemsetAsync(x->d_flags, 0, bytes, x->stream), "hipMemsetAsync(flags)");
   return NT_OK;
 }
 
@@ -601,7 +621,7 @@ static int launch_kernel(nt_exec* x, hipFunction_t fn, hipFunction_t fn_slow, do
                          int nch, int markets, uint64_t paths, uint64_t offset, uint64_t seed, double* out_v,
                          double* out_g, int& grid, hipEvent_t between = nullptr) {
   grid = grid_for(x, paths);
-  int rc = ensure_flags(x, paths, markets);
+  int rc = ensure_flags(x, grid, markets);
   if (rc != NT_OK) return rc;
   return ntr::launch_kernel_on(x, x->stream, fn, fn_slow, d_inputs, d_partials, nch, x->d_scratch, x->d_flags, paths,
                                offset, seed, out_v, out_g, grid, between);

@@ -374,16 +374,32 @@ __device__ __forceinline__ double nt_wave_sum(double x) {
   return x;
 }
 
-// Bitmap of the paths a replay kernel leaves to the exception kernel: bit
-// p % 64 of word p / 64 for the dispatch's path p. A wave's 64 lanes hold 64
-// consecutive paths starting at a multiple of 64 (blocks are whole waves and
-// the grid stride is a multiple of 64), so lane l is bit l of the wave's
-// ballot and the lowest active lane stores the whole word: no atomics, and
-// every word of the dispatch is written (zero where no path was flagged).
-__device__ __forceinline__ void nt_flag_paths(nt_u64* __restrict__ flags, nt_u64 p, bool flagged) {
+// Bitmap of the lanes whose paths a replay kernel leaves to the exception
+// kernel: bit tid % 64 of word tid / 64, one word per wave of the grid (blocks
+// are whole waves). A lane flags all of its paths or none, so one bit per lane
+// says it all, and the bitmap's size is the grid's, not the dispatch's. Only a
+// wave with a flagged lane stores its word (the ballot, from its lowest active
+// lane: no atomics); the words start at zero and the exception kernel, which
+// reads them on the same grid, sets every nonzero word back to zero
+// (nt_take_lane_flag), so the bitmap is zero again between dispatches.
+__device__ __forceinline__ void nt_flag_lanes(nt_u64* __restrict__ flags, nt_u64 tid, bool flagged) {
   const nt_u64 mask = __ballot(flagged);
   const nt_u64 active = __ballot(1);
-  if (__lane_id() == static_cast<unsigned>(__ffsll(static_cast<long long>(active)) - 1)) flags[p >> 6] = mask;
+  if (mask != 0 && __lane_id() == static_cast<unsigned>(__ffsll(static_cast<long long>(active)) - 1)) {
+    flags[tid >> 6] = mask;
+  }
+}
+
+// The exception kernel's read of this lane's bit. The wave's lowest active
+// lane then clears a nonzero word; the store depends on the loaded word, so
+// it follows the load every lane of the wave made with the same instruction.
+__device__ __forceinline__ bool nt_take_lane_flag(nt_u64* __restrict__ flags, nt_u64 tid) {
+  const nt_u64 w = flags[tid >> 6];
+  const nt_u64 active = __ballot(1);
+  if (w != 0 && __lane_id() == static_cast<unsigned>(__ffsll(static_cast<long long>(active)) - 1)) {
+    flags[tid >> 6] = 0;
+  }
+  return ((w >> (tid & 63)) & 1) != 0;
 }
 
 // Reduce NCH per-lane accumulators over the block and write one row of

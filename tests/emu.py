@@ -60,8 +60,10 @@ class EmulatedKernel:
         values = np.zeros(markets * paths * outputs)
         grads = np.zeros((markets * paths * outputs, max(1, ni)))
         p = lambda a: a.ctypes.data_as(C.POINTER(C.c_double))
-        self.lib.emu_run(paths, offset & (2**64 - 1), seed & (2**64 - 1), p(x), p(sums), p(values), p(grads),
-                         grid, block, self.slots)
+        rc = self.lib.emu_run(paths, offset & (2**64 - 1), seed & (2**64 - 1), p(x), p(sums), p(values), p(grads),
+                              grid, block, self.slots)
+        if rc != 0:
+            raise AssertionError("the exception kernel left lane flags set")
         grads = grads[:, :ni]
         if outputs > 1:
             sums = sums.reshape(markets, outputs, 2 + ni)

@@ -15,8 +15,9 @@ extern "C" int emu_run(nt_u64 n_paths, nt_u64 offset, nt_u64 seed, const double*
   nt_tables_load();
   blockDim.x = block;
   std::vector<real> scratch(static_cast<size_t>(grid) * block * (slots ? slots : 1));
-  // one bitmap per market (at most 64 markets)
-  std::vector<nt_u64> flags(1 + static_cast<size_t>((n_paths + 63) / 64) * 64, 0);  // count, then the bitmaps
+  // the count, then one lane bitmap per market (at most 64 markets)
+  const size_t lane_words = (static_cast<size_t>(grid) * block + 63) / 64;
+  std::vector<nt_u64> flags(1 + lane_words * 64, 0);
   for (unsigned b = 0; b < grid; ++b) {
     for (unsigned t = 0; t < block; ++t) {
       blockIdx.x = b;
@@ -31,6 +32,10 @@ extern "C" int emu_run(nt_u64 n_paths, nt_u64 offset, nt_u64 seed, const double*
       threadIdx.x = t;
       nt_replay_slow(inputs, n_paths, offset, seed, sums, scratch.data(), out_v, out_g, flags.data());
     }
+  }
+  // the exception kernel leaves the bitmap as it found it before the replay
+  for (size_t i = 1; i < flags.size(); ++i) {
+    if (flags[i] != 0) return 1;
   }
 #endif
   return 0;

@@ -71,16 +71,23 @@ inline void sincospif(float x, float* s, float* c) {
 }
 
 // The emulated threads of a block run one after another: every block is taken
-// to hold a flagged path, and each thread sets its own bits in a bitmap the
-// driver zeroed.
+// to hold a flagged lane, and each thread sets, and takes back, its own bit of
+// a lane bitmap the driver zeroed (on the device a wave stores and clears a
+// whole word; the bits read and the bitmap left behind are the same).
 inline int __syncthreads_or(int) { return 1; }
 inline unsigned long long atomicAdd(unsigned long long* a, unsigned long long v) {
   const unsigned long long old = *a;
   *a += v;
   return old;
 }
-inline void nt_flag_paths(unsigned long long* flags, unsigned long long p, bool flagged) {
-  if (flagged) flags[p >> 6] |= 1ull << (p & 63);
+inline void nt_flag_lanes(unsigned long long* flags, unsigned long long tid, bool flagged) {
+  if (flagged) flags[tid >> 6] |= 1ull << (tid & 63);
+}
+inline bool nt_take_lane_flag(unsigned long long* flags, unsigned long long tid) {
+  const unsigned long long bit = 1ull << (tid & 63);
+  const bool set = (flags[tid >> 6] & bit) != 0;
+  flags[tid >> 6] &= ~bit;
+  return set;
 }
 
 // Sequential stand-in for the block reduction: every emulated thread adds its

@@ -120,6 +120,36 @@ def test_noalloc_matches_replay(rocm, hip, tapes, name, prec, mode, roll, counts
             assert np.array_equal(got, want), (paths, got - want)
 
 
+MERTON = dict(spot=100.0, strike=100.0, vol=0.18, rate=0.03, maturity=1.0, jumpIntensity=0.75, jumpMean=-0.05,
+              jumpVol=0.15)
+
+
+@pytest.mark.parametrize("mode,counts", [(2, (50_001, 4_097)), (1, (20_001, 4_097))])
+def test_noalloc_with_exception_lanes(rocm, hip, nt, tapes, mode, counts):
+    """The Merton jump tape (32 steps): its smoothed indicator overflows exp on
+    most steps, so most lanes leave their paths to the exception kernel. Two
+    calls in a row (the second smaller) are each bit-equal to nt_exec_replay's
+    (which runs the exception kernel after a look at the count); then an
+    executable whose lanes flag nothing (C2), on the same static array, is
+    bit-equal too: the count and the lane bitmap were left at zero."""
+    from conftest import merton_call_tape
+    flat = merton_call_tape(nt, MERTON, steps=32).flat()
+    print(f"case noalloc merton32 fp64 mode={mode}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+        assert "nt_replay_slow" in x.source()
+        for paths in counts:
+            want, _ = x.replay(paths, OFFSET, 42)
+            got = noalloc(rocm, hip, x, flat["recorded_inputs"], paths, OFFSET, 42)
+            print(f"  paths={paths} sum={got[0]!r}", flush=True)
+            assert np.all(np.isfinite(got))
+            assert np.array_equal(got, want), (paths, got - want)
+    t = tapes["C2"]
+    with rocm.Executable(t, rocm.options("fp64")) as x:
+        want, _ = x.replay(65_536, OFFSET, 42)
+        got = noalloc(rocm, hip, x, t["recorded_inputs"], 65_536, OFFSET, 42)
+    assert np.array_equal(got, want), got - want
+
+
 def test_noalloc_refuses_oversized_scratch(rocm, hip, tapes):
     """A reverse-sweep executable that keeps its tape in device memory needs
     tape_slots x lanes of scratch; at the full grid that exceeds the static
