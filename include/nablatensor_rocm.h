@@ -212,8 +212,9 @@ int nt_exec_replay_paths(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_
  * kernels and returns; the caller synchronizes before reading d_sums. Sums are
  * bit-identical to nt_exec_replay's for the same inputs, paths, offset and
  * seed. The per-block partials (grid x channels doubles, twice that when the
- * tape has an exception kernel), the bitmap of paths left to the exception
- * kernel (paths / 8 bytes) and a reverse sweep's per-lane tape, if the
+ * tape has an exception kernel), the bitmap of lanes that left paths to the
+ * exception kernel (one bit per lane of the grid, in a fixed 128 KiB region of
+ * its own, for grids of up to 2^20 lanes) and a reverse sweep's per-lane tape, if the
  * executable keeps one in device memory, live in a static array of
  * NT_NOALLOC_SCRATCH_BYTES per device; a dispatch that needs more is refused
  * with NT_E_INVALID before anything is launched. Calls that overlap in time on
