@@ -39,11 +39,13 @@ MODES = {1: "reverse", 2: "tangent"}
 REFERENCE_ROCM_FP64 = 2.16e6
 
 
-def workload_tape(name: str):
+def workload_tape(name: str, coefficients: int = 16):
     from nablatensor_amd import workloads
 
     if name == "asian_weekdays":
         return workloads.schedule_tapes()[name].flat()
+    if name == "local_vol":
+        return workloads.local_vol_asian_tape(coefficients).flat()
     return workloads.workload_tapes()[name].flat()
 
 
@@ -75,6 +77,16 @@ def measured_counters(workload: str, precision: str, info: dict) -> dict:
     return out
 
 
+def cost_model(source: str) -> dict | None:
+    """The lowering's estimate of each derivative mode's work per path (VALU
+    instructions; the `// nt-cost:` line of the generated source), which
+    picks the mode when none is forced."""
+    for line in source.splitlines():
+        if line.startswith("// nt-cost:"):
+            return {k: int(v) for k, v in (kv.split("=") for kv in line.split()[2:])}
+    return None
+
+
 def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
             waves=0, max_blocks=0, basis=0, roll=1, block=0):
     from nablatensor_amd import flops
@@ -82,6 +94,7 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves,
                                                 max_blocks=max_blocks, basis=basis, roll=roll, block=block)) as x:
         info = x.info()
+        cost = cost_model(x.source())
         # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
         # (untimed) before the warmup steps, so a short --warmup does not time
         # a cold device.
@@ -128,7 +141,7 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
         "kernel": {**{k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
                                            "loop_iters", "seg_len", "n_segments", "checkpoint", "tape_slots",
                                            "grid_cap")},
-                   "mode": MODES[info["mode"]]},
+                   "mode": MODES[info["mode"]], "cost_model": cost},
     }
 
 
@@ -157,6 +170,68 @@ def measure_markets(rocm, flat, precision, paths, steps, warmup, seed, markets, 
     return {"value": paths * markets * steps / wall, "ms_per_step": wall / steps * 1e3, "replay_kernel_ms": avg,
             "single_market_kernel_ms": single, "markets": markets, "mode": MODES[info["mode"]],
             "speedup_vs_separate": markets * single / avg}
+
+
+def adjoint_vs_bump(rocm, flat, paths, seed, repeats=3, ramp=0.2) -> dict:
+    """The adjoint against bump-and-revalue on the headline tape (fp64): one
+    dispatch that returns the value and all 5 Greeks, against the 1 + 2 x 5
+    price-only dispatches of a central bump with common random numbers,
+    h_j = 5e-3 max(1, |x_j|) (BumpCrossCheck.java:33-49), and against the same
+    11 input sets priced in one multi-market dispatch that shares the draws.
+    Each is timed as the reference's Benchmarks.adjointVsBump does
+    (Benchmarks.java:69-90): a warm run, then the best of 3, wall clock on the
+    host per request, with the kernels' HIP-event time beside it."""
+    import numpy as np
+
+    from nablatensor_amd import bumps
+
+    sets, h = bumps.central_bump_sets(flat["recorded_inputs"])
+
+    def best(run):
+        run()
+        return min((run() for _ in range(repeats)), key=lambda r: r[0])
+
+    with rocm.Executable(flat, rocm.options("fp64")) as ad, \
+            rocm.Executable(flat, rocm.options("fp64", adjoints=False)) as po:
+        t_ramp = time.perf_counter()
+        while time.perf_counter() - t_ramp < ramp:
+            ad.replay(paths, 0, seed)
+
+        def adjoint():
+            t0 = time.perf_counter()
+            sums, tm = ad.replay(paths, 0, seed)
+            return time.perf_counter() - t0, tm["kernel_ms"], sums[2:] / paths
+
+        def separate():
+            t0, kernel, prices = time.perf_counter(), 0.0, []
+            for x in sets:
+                po.set_inputs(x)
+                sums, tm = po.replay(paths, 0, seed)
+                kernel += tm["kernel_ms"]
+                prices.append(sums[0] / paths)
+            return time.perf_counter() - t0, kernel, np.array(prices)
+
+        def shared():
+            t0 = time.perf_counter()
+            sums, tm = po.replay_many(sets, paths, 0, seed)
+            return time.perf_counter() - t0, tm["kernel_ms"], sums[:, 0] / paths
+
+        a, b, m = best(adjoint), best(separate), best(shared)
+        po.set_inputs(sets[0])
+        one = best(lambda: (lambda t0, r: (time.perf_counter() - t0, r[1]["kernel_ms"], None))(
+            time.perf_counter(), po.replay(paths, 0, seed)))
+    fd = bumps.bump_greeks(b[2], h)
+    return {"scenarios": paths, "relative_bump": 5e-3, "replays": len(sets),
+            "adjoint_ms": a[0] * 1e3, "adjoint_kernels_ms": a[1],
+            "bump_ms": b[0] * 1e3, "bump_kernels_ms": b[1],
+            "price_only_ms": one[0] * 1e3, "price_only_kernels_ms": one[1],
+            "bump_one_dispatch_ms": m[0] * 1e3, "bump_one_dispatch_kernels_ms": m[1],
+            "speedup": b[0] / a[0], "speedup_11x_one": len(sets) * one[0] / a[0],
+            "speedup_vs_one_dispatch_bump": m[0] / a[0],
+            "greeks_adjoint": [float(g) for g in a[2]], "greeks_bump": [float(g) for g in fd],
+            "max_abs_diff": float(np.max(np.abs(fd - a[2]))),
+            "one_dispatch_prices_equal": bool(np.array_equal(m[2], b[2])),
+            "reference": "cpu-jit, 2M scenarios: adjoint 1.11 s vs 11 bump replays 10.76 s (9.7x), README.md:70-71"}
 
 
 def host_cpu() -> dict:
@@ -214,7 +289,9 @@ def other_workload(rocm, args) -> int:
     desc, paths, seed, prec = workloads.DESCRIPTIONS[args.workload]
     prec = args.precision or prec
     paths = args.paths if args.paths != 2_000_000 else paths
-    flat = workload_tape(args.workload)
+    flat = workload_tape(args.workload, args.coefficients)
+    if args.workload == "local_vol":
+        desc = f"{desc}, k = {args.coefficients}"
     print(f"[bench] {args.workload} {desc}: {len(flat['op'])} nodes, {paths:,} scenarios/step, {prec}",
           file=sys.stderr, flush=True)
     if args.markets > 1:
@@ -415,10 +492,14 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=3_000_000,
                     help="scenarios in the CPU baseline's timed sample (about 25 CPU-seconds on 16 threads)")
     ap.add_argument("--no-fp32", action="store_true")
+    ap.add_argument("--no-bump", action="store_true",
+                    help="skip timing the adjoint against the 11 replays of a central bump-and-revalue")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",
                     help="skip the other benchmark configurations reported beside the headline")
-    ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "asian_weekdays"],
+    ap.add_argument("--coefficients", type=int, default=16,
+                    help="with --workload local_vol: coefficients of the local-volatility polynomial")
+    ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "asian_weekdays", "local_vol"],
                     help="C2 (default) prints the headline line; the others print the same fields for that workload")
     ap.add_argument("--precision", choices=["fp64", "fp32"], default=None,
                     help="run one workload at one precision and print its line (default: the workload's own; "
@@ -474,6 +555,11 @@ def main() -> int:
         f32 = measure(rocm, flat, "fp32", args.paths, args.steps, args.warmup, args.seed, args.policy, args.seg,
                       args.mode, args.ramp)
         print(f"[bench] fp32 {f32['kernel']['mode']} {f32['value']:.3e} scen/s", file=sys.stderr, flush=True)
+    bump = None
+    if not args.no_bump:
+        bump = adjoint_vs_bump(rocm, flat, args.paths, args.seed)
+        print(f"[bench] adjoint {bump['adjoint_ms']:.3f} ms vs 11 bump replays {bump['bump_ms']:.3f} ms "
+              f"({bump['speedup']:.1f}x)", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(flat, args.cpu_sample, args.seed)
     others = None if args.no_workloads else other_workloads(rocm)
     out = {
@@ -500,6 +586,7 @@ def main() -> int:
                                                                   "roofline", "kernel")},
         "fp32": None if f32 is None else {k: f32[k] for k in ("value", "ms_per_step", "replay_kernel_ms",
                                                                "roofline", "kernel")},
+        "adjoint_vs_bump": bump,
         "cpu_baseline": cpu,
         "workloads": others,
     }

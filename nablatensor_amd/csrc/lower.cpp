@@ -2870,6 +2870,11 @@ void Emitter::preamble() {
     o_ << "// nt-plan: tape_slots=" << p_.tape_slots << " seg=" << p_.seg << " ckpt=" << p_.ckpt << " mode=reverse\n";
     if (!f32_) o_ << "// nt-compile: -fmacf64-inst\n";
   }
+  if (p_.cost_reverse > 0 || p_.cost_tangent > 0) {
+    // the cost model's estimates per path (VALU instructions) behind the choice of mode
+    o_ << "// nt-cost: reverse=" << static_cast<long>(p_.cost_reverse + 0.5)
+       << " tangent=" << static_cast<long>(p_.cost_tangent + 0.5) << "\n";
+  }
   o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";
   if (p_.libm == 1) o_ << "#define NT_DEVICE_LIBM 1\n";
   if (p_.libm == 2) o_ << "#define NT_LIBM_SINCOS 1\n";

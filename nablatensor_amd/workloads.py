@@ -27,6 +27,8 @@ DESCRIPTIONS = {
            1_000_000, 42, "fp32"),
     "asian_weekdays": ("Asian call, GBM, 252 weekday fixings (TimeGrid.of, non-uniform), ATM 1y, value + 5 Greeks",
                        2_000_000, 42, "fp64"),
+    "local_vol": ("Asian call, 252 fixings, ATM 1y, parametric local volatility (polynomial in log-moneyness), "
+                  "value + 3 + k Greeks", 2_000_000, 42, "fp64"),
 }
 
 
@@ -73,3 +75,53 @@ def schedule_tapes() -> dict:
     grid = nt.TimeGrid.of(weekday_fixings())
     return {"asian_weekdays": nt.record(nt.Products.asianCall(), nt.EquityMarket.atmOneYear(), grid)}
 
+
+
+LOCAL_VOL_STEPS = 252
+
+
+def local_vol_coefficients(k: int) -> list[float]:
+    """theta_0 .. theta_{k-1} of the local-volatility polynomial: a 20% level,
+    a skew of -0.1, a smile of 0.1 per unit log-moneyness squared, then small
+    alternating higher terms 0.05 (-1)^j / j^2."""
+    base = [0.2, -0.1, 0.1]
+    return [base[j] if j < 3 else 0.05 * (-1) ** j / (j * j) for j in range(k)]
+
+
+def local_vol_asian_tape(k: int = 16, steps: int = LOCAL_VOL_STEPS):
+    """An arithmetic Asian call (252 fixings, ATM 1y) under a parametric local
+    volatility: per step sigma = max(theta_0 + theta_1 x + ... + theta_{k-1}
+    x^{k-1}, 0.01) in the log-moneyness x = ln(S / S0) (Horner's rule), then
+    the log-Euler GBM step with that sigma (GbmPath.step,
+    GbmPath.java:88-90, with the step's drift and diffusion formed from the
+    state-dependent sigma, as GbmPath's drift/diffusion hooks allow). Inputs:
+    spot, strike, rate, then the k coefficients. Every value of the step
+    depends on all k coefficients, so tangent mode carries k + 2 tangents
+    through a Horner chain of 2 (k - 1) nodes per step (work ~ k^2) where the
+    reverse sweep's rules stay linear in k: the tape on which the lowering's
+    cost model picks the reverse sweep once k is large enough."""
+    from . import _host as nt
+
+    dt = 1.0 / steps
+    theta0 = local_vol_coefficients(k)
+
+    def body(rec):
+        spot = rec.input("spot", 100.0)
+        strike = rec.input("strike", 100.0)
+        rate = rec.input("rate", 0.03)
+        theta = [rec.input(f"theta{j}", theta0[j]) for j in range(k)]
+        log_s0 = spot.log()
+        s = spot
+        acc = spot.mul(0.0)
+        for _ in range(steps):
+            x = s.log().sub(log_s0)
+            sigma = theta[k - 1]
+            for j in range(k - 2, -1, -1):
+                sigma = sigma.mul(x).add(theta[j])
+            sigma = sigma.max(0.01)
+            drift = rate.sub(sigma.mul(sigma).mul(0.5)).mul(dt)
+            s = s.mul(drift.add(sigma.mul(dt ** 0.5).mul(rec.randn())).exp())
+            acc = acc.add(s)
+        payoff = acc.mul(1.0 / steps).sub(strike).max(0.0)
+        rec.output(payoff.mul(rate.neg().exp()))
+    return nt.AadRecorder.record(body)

@@ -35,6 +35,9 @@ def patched(monkeypatch):
     monkeypatch.setattr(bench, "measure", fake_measure)
     monkeypatch.setattr(bench, "cpu_baseline", lambda flat, sample, seed: {
         "value": 1e6, "unit": "scenarios/s", "cores": 16, "kind": "port", "sample": "fake"})
+    monkeypatch.setattr(bench, "adjoint_vs_bump", lambda rocm, flat, paths, seed: {"speedup": 10.0,
+                                                                                   "adjoint_ms": 1.0,
+                                                                                   "bump_ms": 10.0})
 
 
 def run_main(monkeypatch, capsys, argv):
@@ -57,6 +60,7 @@ def test_headline_line_has_the_contract_fields(patched, monkeypatch, capsys):
     assert out["cpu_baseline"]["kind"] in ("port", "reference")
     assert out["reverse"]["kernel"]["mode"] == "reverse"
     assert out["fp32"]["value"] > 0
+    assert out["adjoint_vs_bump"]["speedup"] == 10.0
     w = out["workloads"]
     assert set(w) == {"C1_fp64", "C3_fp32", "C3_fp64", "C4_fp64", "C5_fp32", "C5_fp64", "asian_weekdays_fp64"}
     assert all(r["value"] > 0 and 0 < r["frac"] < 1 for r in w.values())
@@ -134,3 +138,51 @@ def test_committed_counters_cover_the_planned_kernels(workload, precision, mode,
     got = bench.measured_counters(workload, precision, info)
     assert set(got) == {"traffic", "executed"}, (workload, precision, info)
     assert got["traffic"]["bytes"] > 0 and got["executed"]["flops_per_scenario"] > 0
+
+
+def test_adjoint_vs_bump_prices_the_eleven_sets(monkeypatch):
+    """The bump leg replays the base market and +h, -h per input (price-only,
+    the same paths and seed), takes central differences, and divides the 11
+    replays' wall time by the adjoint dispatch's. A fake executable whose price
+    is linear in the inputs (slope j + 1 for input j) and whose adjoint
+    dispatch returns those slopes gives bump Greeks equal to them."""
+    import numpy as np
+
+    from nablatensor_amd import rocm
+
+    slopes = np.arange(1.0, 6.0)
+
+    class FakeExecutable:
+        def __init__(self, flat, opts):
+            self.adjoints = bool(opts.adjoints)
+            self.x = np.array(flat["recorded_inputs"], dtype=float)
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *exc):
+            return False
+
+        def set_inputs(self, x):
+            self.x = np.array(x, dtype=float)
+
+        def _sums(self, x, paths):
+            grads = slopes * paths if self.adjoints else np.zeros(5)
+            return np.concatenate([[float(slopes @ x) * paths, 0.0], grads])
+
+        def replay(self, paths, offset, seed):
+            return self._sums(self.x, paths), {"kernel_ms": 1.0, "wall_ms": 1.0, "replay_ms": 1.0}
+
+        def replay_many(self, sets, paths, offset, seed):
+            return np.stack([self._sums(x, paths) for x in sets]), {"kernel_ms": 2.0, "wall_ms": 2.0,
+                                                                    "replay_ms": 2.0}
+
+    monkeypatch.setattr(rocm, "Executable", FakeExecutable)
+    flat = {"recorded_inputs": [100.0, 100.0, 0.2, 0.03, 1.0]}
+    out = bench.adjoint_vs_bump(rocm, flat, 1000, 42, ramp=0.0)
+    assert out["replays"] == 11
+    assert np.allclose(out["greeks_bump"], slopes, rtol=1e-9)
+    assert np.allclose(out["greeks_adjoint"], slopes)
+    assert out["bump_kernels_ms"] == 11.0 and out["adjoint_kernels_ms"] == 1.0
+    assert out["speedup"] == pytest.approx(out["bump_ms"] / out["adjoint_ms"])
+    assert out["one_dispatch_prices_equal"] is True

@@ -843,3 +843,23 @@ def test_signed_affine_exponents_summed_after_the_loop(rocm, nt, precision):
     else:
         ov, og = oracle.replay_paths(flat, 200, OFFSET, 42, f32=True, threads=1)
         assert rel_err(v, ov) < 2e-4 and rel_err(g, og) < 2e-3
+
+
+@pytest.mark.parametrize("k", [2, 8, 16])
+def test_local_vol_tape_both_modes_emulated(rocm, k):
+    """The parametric local-volatility Asian (workloads.local_vol_asian_tape):
+    the cost model picks tangent mode for few coefficients and the reverse
+    sweep from 8 on; both modes match the oracle, the reverse sweep bit for bit
+    with libm Box-Muller, tangent mode within the per-path bar."""
+    from nablatensor_amd import workloads
+    flat = workloads.local_vol_asian_tape(k, steps=24).flat()
+    auto = rocm.lower(flat, rocm.options("fp64"))
+    assert ("mode=reverse" in auto) == (k >= 8)
+    paths = 96
+    ov, og = oracle.replay_paths(flat, paths, OFFSET, 42, threads=1)
+    _, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=1), paths, rocm=rocm)
+    assert np.array_equal(v, ov) and np.array_equal(g, og)
+    opts = rocm.options("fp64", libm=1, mode=2)
+    _, v, g = run_emulated(flat, opts, paths, rocm=rocm)
+    assert_values_match(v, ov, rocm.lower(flat, opts))
+    check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.9)
