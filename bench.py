@@ -39,7 +39,7 @@ MODES = {1: "reverse", 2: "tangent"}
 REFERENCE_ROCM_FP64 = 2.16e6
 
 
-def workload_tape(name: str, coefficients: int = 16):
+def workload_tape(name: str, coefficients: int = 24):
     from nablatensor_amd import workloads
 
     if name == "asian_weekdays":
@@ -51,7 +51,7 @@ def workload_tape(name: str, coefficients: int = 16):
 
 # The committed counter summary of each workload's replay kernel (profiles/).
 COUNTER_FILES = {"C1": "european1", "C2": "asian252", "C3": "barrier252", "C4": "heston_asian504",
-                 "C5": "worstof16", "asian_weekdays": "asian_weekdays252"}
+                 "C5": "worstof16", "asian_weekdays": "asian_weekdays252", "local_vol": "local_vol24"}
 
 
 def measured_counters(workload: str, precision: str, info: dict) -> dict:
@@ -391,6 +391,30 @@ def other_workloads(rocm, steps: int = 5, warmup: int = 1, ramp: float = 0.2) ->
     return out
 
 
+def local_vol_modes(rocm, k: int = 24, steps: int = 5, warmup: int = 1, ramp: float = 0.2) -> dict:
+    """Both derivative modes on the parametric local-volatility Asian (k
+    coefficients, k + 3 inputs), the tape on which the cost model picks the
+    reverse sweep: each mode's kernel time, roofline fraction and executed
+    fraction, and the mode the engine picks by itself."""
+    from nablatensor_amd import workloads
+
+    desc, paths, seed, prec = workloads.DESCRIPTIONS["local_vol"]
+    flat = workload_tape("local_vol", k)
+    out = {"workload": f"{desc}, k = {k}", "inputs": len(flat["input_node"]), "scenarios_per_step": paths}
+    for mode in (1, 2):
+        m = measure(rocm, flat, prec, paths, steps, warmup, seed, 0, 0, mode, ramp, "local_vol")
+        out[MODES[mode]] = {"value": m["value"], "replay_kernel_ms": m["replay_kernel_ms"],
+                            "frac": m["roofline"]["frac"], "executed_frac": m["roofline"]["executed_frac"],
+                            "vgprs": m["kernel"]["vgprs"], "scratch_bytes": m["kernel"]["scratch_bytes"]}
+        out["cost_model"] = m["kernel"]["cost_model"]
+    with rocm.Executable(flat, rocm.options(prec)) as x:
+        out["picked"] = MODES[x.info()["mode"]]
+    out["reverse_speedup"] = out["tangent"]["replay_kernel_ms"] / out["reverse"]["replay_kernel_ms"]
+    print(f"[bench] local_vol k={k}: reverse {out['reverse']['replay_kernel_ms']:.3f} ms, tangent "
+          f"{out['tangent']['replay_kernel_ms']:.3f} ms, engine picks {out['picked']}", file=sys.stderr, flush=True)
+    return out
+
+
 def host_overheads(rocm, args) -> int:
     """Host-path costs around the replay kernel on the Asian 252 tape, fp64:
     building an executable (lowering + hipRTC compile, or a code-object cache
@@ -497,7 +521,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-workloads", action="store_true",
                     help="skip the other benchmark configurations reported beside the headline")
-    ap.add_argument("--coefficients", type=int, default=16,
+    ap.add_argument("--coefficients", type=int, default=24,
                     help="with --workload local_vol: coefficients of the local-volatility polynomial")
     ap.add_argument("--workload", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "asian_weekdays", "local_vol"],
                     help="C2 (default) prints the headline line; the others print the same fields for that workload")
@@ -562,6 +586,7 @@ def main() -> int:
               f"({bump['speedup']:.1f}x)", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu_baseline else cpu_baseline(flat, args.cpu_sample, args.seed)
     others = None if args.no_workloads else other_workloads(rocm)
+    modes = None if args.no_workloads else local_vol_modes(rocm)
     out = {
         "metric": "scenarios/sec for value+all Greeks (fp64), % of VALU FP64 peak",
         "value": f64["value"],
@@ -589,6 +614,7 @@ def main() -> int:
         "adjoint_vs_bump": bump,
         "cpu_baseline": cpu,
         "workloads": others,
+        "local_vol_modes": modes,
     }
     print(json.dumps(out), flush=True)
     return 0

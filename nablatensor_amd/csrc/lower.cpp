@@ -896,6 +896,7 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   double fwd = 0;
   for (int i = 0; i < t.n; ++i) fwd += fwd_cost(t.op[i], p.precision == NT_FP32);
   p.path_cost = fwd;
+  p.cost_forward = fwd;
   if (!p.adjoints && p.markets == 1 && !multi) return;
   compute_deps(t, p);
   const LoopPlan& L = p.loop;
@@ -926,8 +927,15 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   // the tangent frame without tangents).
   // Several outputs get their Jacobian rows from one tangent sweep (the
   // reverse sweep here follows one output).
+  // Per estimated instruction, a reverse-sweep kernel takes about twice a
+  // tangent kernel's time on MI355X: it holds a segment's values, its
+  // adjoints and the accumulators at once (more VGPRs, fewer resident waves)
+  // and stores and reloads checkpoints. Measured time over (forward +
+  // estimate), reverse against tangent: 1.9-2.2 near the modes' crossover on
+  // the local-volatility Asian (8 to 16 coefficients), 1.3-1.7 on C2-C4.
+  constexpr double kReverseTime = 2.0;
   const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || multi ||
-                       (p.adjoints && o.mode == NT_MODE_AUTO && tan < rev);
+                       (p.adjoints && o.mode == NT_MODE_AUTO && fwd + tan < kReverseTime * (fwd + rev));
   p.path_cost = fwd + (tangent ? tan : rev);
   if (!tangent) return;
   p.mode = NT_MODE_TANGENT;
@@ -2872,7 +2880,8 @@ void Emitter::preamble() {
   }
   if (p_.cost_reverse > 0 || p_.cost_tangent > 0) {
     // the cost model's estimates per path (VALU instructions) behind the choice of mode
-    o_ << "// nt-cost: reverse=" << static_cast<long>(p_.cost_reverse + 0.5)
+    o_ << "// nt-cost: forward=" << static_cast<long>(p_.cost_forward + 0.5)
+       << " reverse=" << static_cast<long>(p_.cost_reverse + 0.5)
        << " tangent=" << static_cast<long>(p_.cost_tangent + 0.5) << "\n";
   }
   o_ << "#pragma clang fp contract(" << (p_.contract ? "fast" : "off") << ")\n";

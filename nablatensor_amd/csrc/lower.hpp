@@ -78,6 +78,7 @@ struct Plan {
   std::vector<uint64_t> deps;             // node -> inputs it depends on (bitset), tangent mode
   std::vector<uint64_t> posdeps;          // loop position -> union over the iterations
   double cost_reverse = 0, cost_tangent = 0;  // estimated extra VALU work per path of each mode
+  double cost_forward = 0;                    // estimated VALU work per path of the forward sweep alone
   double path_cost = 0;                   // estimated VALU instructions per path: the forward plus the chosen
                                           // mode's extra work
   int adjoints = 1;

@@ -88,10 +88,11 @@ def local_vol_coefficients(k: int) -> list[float]:
     return [base[j] if j < 3 else 0.05 * (-1) ** j / (j * j) for j in range(k)]
 
 
-def local_vol_asian_tape(k: int = 16, steps: int = LOCAL_VOL_STEPS):
+def local_vol_asian_tape(k: int = 24, steps: int = LOCAL_VOL_STEPS):
     """An arithmetic Asian call (252 fixings, ATM 1y) under a parametric local
     volatility: per step sigma = max(theta_0 + theta_1 x + ... + theta_{k-1}
-    x^{k-1}, 0.01) in the log-moneyness x = ln(S / S0) (Horner's rule), then
+    x^{k-1}, 0.01) in the log-moneyness x = ln(S / S0), held to [-1, 1] so the
+    polynomial stays bounded (Horner's rule), then
     the log-Euler GBM step with that sigma (GbmPath.step,
     GbmPath.java:88-90, with the step's drift and diffusion formed from the
     state-dependent sigma, as GbmPath's drift/diffusion hooks allow). Inputs:
@@ -114,7 +115,7 @@ def local_vol_asian_tape(k: int = 16, steps: int = LOCAL_VOL_STEPS):
         s = spot
         acc = spot.mul(0.0)
         for _ in range(steps):
-            x = s.log().sub(log_s0)
+            x = s.log().sub(log_s0).max(-1.0).min(1.0)
             sigma = theta[k - 1]
             for j in range(k - 2, -1, -1):
                 sigma = sigma.mul(x).add(theta[j])

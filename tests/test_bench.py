@@ -12,6 +12,8 @@ import conftest
 sys.path.insert(0, str(conftest.ROOT))
 import bench  # noqa: E402
 
+LOCAL_VOL_MODES = bench.local_vol_modes  # the real one: the fixture below replaces it for the headline tests
+
 
 def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode=0, ramp=0.5, workload="C2",
                  waves=0, max_blocks=0, basis=0, roll=1, block=0):
@@ -24,7 +26,8 @@ def fake_measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg,
                          "executed_flops_per_scenario": 15000, "executed_achieved": 8.0, "executed_frac": 8.0 / 78.6,
                          "valu_issue": 0.85, "executed_source": "fake",
                          "flops_per_scenario": 18723, "convention": "NT-FLOP v1"},
-            "kernel": {"vgprs": 100, "scratch_bytes": 0, "mode": resolved}}
+            "kernel": {"vgprs": 100, "scratch_bytes": 0, "mode": resolved,
+                       "cost_model": {"forward": 1, "reverse": 2, "tangent": 3}}}
 
 
 @pytest.fixture
@@ -35,6 +38,7 @@ def patched(monkeypatch):
     monkeypatch.setattr(bench, "measure", fake_measure)
     monkeypatch.setattr(bench, "cpu_baseline", lambda flat, sample, seed: {
         "value": 1e6, "unit": "scenarios/s", "cores": 16, "kind": "port", "sample": "fake"})
+    monkeypatch.setattr(bench, "local_vol_modes", lambda rocm: {"picked": "reverse", "reverse_speedup": 1.5})
     monkeypatch.setattr(bench, "adjoint_vs_bump", lambda rocm, flat, paths, seed: {"speedup": 10.0,
                                                                                    "adjoint_ms": 1.0,
                                                                                    "bump_ms": 10.0})
@@ -61,6 +65,7 @@ def test_headline_line_has_the_contract_fields(patched, monkeypatch, capsys):
     assert out["reverse"]["kernel"]["mode"] == "reverse"
     assert out["fp32"]["value"] > 0
     assert out["adjoint_vs_bump"]["speedup"] == 10.0
+    assert out["local_vol_modes"]["picked"] == "reverse"
     w = out["workloads"]
     assert set(w) == {"C1_fp64", "C3_fp32", "C3_fp64", "C4_fp64", "C5_fp32", "C5_fp64", "asian_weekdays_fp64"}
     assert all(r["value"] > 0 and 0 < r["frac"] < 1 for r in w.values())
@@ -186,3 +191,28 @@ def test_adjoint_vs_bump_prices_the_eleven_sets(monkeypatch):
     assert out["bump_kernels_ms"] == 11.0 and out["adjoint_kernels_ms"] == 1.0
     assert out["speedup"] == pytest.approx(out["bump_ms"] / out["adjoint_ms"])
     assert out["one_dispatch_prices_equal"] is True
+
+
+def test_local_vol_modes_reports_both_sweeps(patched, monkeypatch):
+    """The local-volatility row times the reverse sweep and tangent mode of
+    the same tape and names the mode the engine picks on its own."""
+    from nablatensor_amd import rocm
+
+    class FakeExecutable:
+        def __init__(self, flat, opts):
+            pass
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *exc):
+            return False
+
+        def info(self):
+            return {"mode": 1}
+
+    monkeypatch.setattr(rocm, "Executable", FakeExecutable)
+    out = LOCAL_VOL_MODES(rocm, k=4)
+    assert out["inputs"] == 7 and out["picked"] == "reverse"
+    assert out["reverse"]["replay_kernel_ms"] == 2.0 and out["tangent"]["replay_kernel_ms"] == 2.0
+    assert out["reverse_speedup"] == 1.0 and out["cost_model"]["reverse"] == 2

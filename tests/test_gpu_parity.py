@@ -503,16 +503,17 @@ def test_checkpointed_straight_line_fp32_reconciles(rocm, tapes):
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
 def test_local_vol_tape_per_path(rocm, mode):
-    """The Asian under a parametric local volatility with 16 coefficients (19
-    inputs; workloads.local_vol_asian_tape): the cost model picks the reverse
-    sweep (mode 0), and both sweeps match the oracle per path within the bar,
-    with no scratch."""
+    """The Asian under a parametric local volatility with 24 coefficients (27
+    inputs; workloads.local_vol_asian_tape), where the reverse sweep runs 1.5x
+    faster than tangent mode: the cost model picks the reverse sweep (mode
+    0), and both sweeps match the oracle per path within the bar, with no
+    scratch."""
     from nablatensor_amd import workloads
-    flat = workloads.local_vol_asian_tape(16).flat()
-    print(f"case local_vol k=16 mode={mode} paths=512", flush=True)
+    flat = workloads.local_vol_asian_tape(24).flat()
+    print(f"case local_vol k=24 mode={mode} paths=512", flush=True)
     with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
         info = x.info()
         assert info["scratch_bytes"] == 0
         assert info["mode"] == (1 if mode == 0 else mode)
         v, g = x.replay_paths(512, OFFSET, 42)
-    print(check_per_path(v, g, flat, 512, OFFSET, 42, min_strict=0.88))  # measured 0.885
+    print(check_per_path(v, g, flat, 512, OFFSET, 42, min_strict=0.88))  # measured 0.891
