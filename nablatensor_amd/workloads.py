@@ -94,7 +94,7 @@ def local_vol_asian_tape(k: int = 24, steps: int = LOCAL_VOL_STEPS):
     x^{k-1}, 0.01) in the log-moneyness x = ln(S / S0), held to [-1, 1] so the
     polynomial stays bounded (Horner's rule), then
     the log-Euler GBM step with that sigma (GbmPath.step,
-    GbmPath.java:88-90, with the step's drift and diffusion formed from the
+    GbmPath.java:89-91, with the step's drift and diffusion formed from the
     state-dependent sigma, as GbmPath's drift/diffusion hooks allow). Inputs:
     spot, strike, rate, then the k coefficients. Every value of the step
     depends on all k coefficients, so tangent mode carries k + 2 tangents
