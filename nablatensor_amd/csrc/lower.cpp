@@ -1038,7 +1038,7 @@ class Emitter {
   bool needs_tables() const {
     if (f32_) return false;
     for (int i = 0; i < t_.n; ++i) {
-      if (t_.op[i] == NT_OP_RANDN || t_.op[i] == NT_OP_EXP) return true;
+      if (t_.op[i] == NT_OP_RANDN || t_.op[i] == NT_OP_EXP || t_.op[i] == NT_OP_LOG) return true;
     }
     return false;
   }
@@ -1056,7 +1056,10 @@ class Emitter {
         if (f32_) return "nt_expf(" + x + ")";
         if (p_.libm == 1 || slow_) return "exp(" + x + ")";
         return "nt_exp_fast(" + x + ", nt_slow" + ms(exp_active_) + ")";
-      case NT_OP_LOG: return f32_ ? "(nt_hw_log2f(" + x + ") * 0.693147180559945309f)" : "log(" + x + ")";
+      case NT_OP_LOG:
+        if (f32_) return "(nt_hw_log2f(" + x + ") * 0.693147180559945309f)";
+        if (p_.libm == 1 || slow_) return "log(" + x + ")";
+        return "nt_log_fast(" + x + ", nt_slow" + ms(exp_active_) + ")";
       case NT_OP_SQRT: return f32_ ? "nt_hw_sqrtf(" + x + ")" : "sqrt(" + x + ")";
       case NT_OP_ABS: return f("fabs") + "(" + x + ")";
       case NT_OP_MAX: return f("fmax") + "(" + x + ", " + y + ")";
@@ -1401,7 +1404,10 @@ class Emitter {
   bool exp_fallback() const {
     if (f32_ || p_.libm == 1) return false;
     for (int i = 0; i < t_.n; ++i) {
-      if (t_.op[i] == NT_OP_EXP || ((t_.op[i] == NT_OP_SQRT || t_.op[i] == NT_OP_DIV) && fast_sqrt())) return true;
+      if (t_.op[i] == NT_OP_EXP || t_.op[i] == NT_OP_LOG ||
+          ((t_.op[i] == NT_OP_SQRT || t_.op[i] == NT_OP_DIV) && fast_sqrt())) {
+        return true;
+      }
     }
     return false;
   }

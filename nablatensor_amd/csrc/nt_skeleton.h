@@ -54,6 +54,8 @@ __device__ __forceinline__ double nt_rsq(double x) { return __builtin_amdgcn_rsq
 __device__ __forceinline__ double nt_rcp(double x) { return __builtin_amdgcn_rcp(x); }
 // x is -0, +0 or a positive normal number: one v_cmp_class_f64
 __device__ __forceinline__ bool nt_zero_or_pos_normal(double x) { return __builtin_amdgcn_class(x, 0x160); }
+// x is a positive normal number (finite, not subnormal): one v_cmp_class_f64
+__device__ __forceinline__ bool nt_pos_normal(double x) { return __builtin_amdgcn_class(x, 0x100); }
 // fp32 hardware transcendentals (quarter-rate VALU): exp2, log2, sqrt, and
 // sin/cos of 2 pi x (the instructions take their argument in revolutions).
 __device__ __forceinline__ float nt_hw_exp2f(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -185,14 +187,16 @@ __device__ __forceinline__ double nt_exp(double x) {
   return bad ? exp(x) : y;
 }
 
-// -2 ln(u) for u = (c + 0.5) * 2^-32, by Tang's table-driven method: u = 2^e x
+// -2 ln(u) for a positive normal u, by Tang's table-driven method: u = 2^e x
 // with x in [sqrt(1/2), sqrt(2)), F = x rounded to 8 fractional bits of its
 // binade (rounding the high word at bit 12 moves F = 2 - 2^-8 up to the next
 // binade exactly), ln u = e ln2 + ln F + ln(1 + r), r = (x - F) / F,
 // |r| <= 2^-9. x - F is exact and F = 1 near u = 1, so ln u keeps full
 // relative accuracy there. Tables and constants carry the factor -2 (exact).
-__device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
-  const double u = fma(static_cast<double>(c), 0x1p-32, 0x1p-33);
+// The exponent comes from u's high word alone, so any biased exponent works
+// (the high word may carry into bit 31 for u near the largest double; the
+// arithmetic is unsigned).
+__device__ __forceinline__ double nt_neg2log(double u) {
   nt_u32 hx = nt_hi(u) + (0x3FF00000u - 0x3FE6A09Eu);
   // e = (hx >> 20) - 1023 as a double: the biased exponent in the low word of
   // 2^52 + (hx >> 20), less 2^52 + 1023 (exact), instead of a conversion
@@ -210,6 +214,19 @@ __device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
   const double hi = fma(ed, NT_M2LN2_HI, nt_tables.lg.hi[idx]);  // exact by the table's layout
   const double lo = fma(ed, NT_M2LN2_LO, nt_tables.lg.lo[idx]) + p;
   return hi + lo;
+}
+
+// Box-Muller's -2 ln(u) for u = (c + 0.5) * 2^-32.
+__device__ __forceinline__ double nt_neg2log_u32(nt_u32 c) {
+  return nt_neg2log(fma(static_cast<double>(c), 0x1p-32, 0x1p-33));
+}
+
+// ln(a) of a LOG node: -1/2 times nt_neg2log (an exact scaling). An argument
+// that is not a positive normal number (zero, subnormal, negative, infinite,
+// NaN) sets `bad`, and the path is evaluated again with device libm.
+__device__ __forceinline__ double nt_log_fast(double a, bool& bad) {
+  bad |= !nt_pos_normal(a);
+  return -0.5 * nt_neg2log(a);
 }
 
 // sqrt(a) for a positive normal finite a: reciprocal square root seed and one

@@ -35,6 +35,16 @@ __global__ void k_exp(const double* __restrict__ x, double* __restrict__ out, in
   }
 }
 
+__global__ void k_log(const double* __restrict__ x, double* __restrict__ out, int* __restrict__ bad, long n) {
+  nt_tables_load();
+  const long T = static_cast<long>(gridDim.x) * blockDim.x;
+  for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += T) {
+    bool b = false;
+    out[i] = nt_log_fast(x[i], b);
+    bad[i] = b ? 1 : 0;
+  }
+}
+
 __global__ void k_sqrt_q(const double* __restrict__ a, double* __restrict__ out, double* __restrict__ q,
                          int* __restrict__ bad, long n) {
   const long T = static_cast<long>(gridDim.x) * blockDim.x;
@@ -128,6 +138,18 @@ int dm_exp(const double* x, double* out, int* bad, long n) {
   auto* dout = static_cast<double*>(b.add(nullptr, sizeof(double) * n));
   auto* dbad = static_cast<int*>(b.add(nullptr, sizeof(int) * n));
   if (b.err == hipSuccess) hipLaunchKernelGGL(k_exp, grid_for(n), dim3(256), 0, 0, dx, dout, dbad, n);
+  int rc = finish(b);
+  b.back(1, out);
+  b.back(2, bad);
+  return rc ? rc : static_cast<int>(b.err);
+}
+
+int dm_log(const double* x, double* out, int* bad, long n) {
+  Buffers b;
+  auto* dx = static_cast<double*>(b.add(x, sizeof(double) * n));
+  auto* dout = static_cast<double*>(b.add(nullptr, sizeof(double) * n));
+  auto* dbad = static_cast<int*>(b.add(nullptr, sizeof(int) * n));
+  if (b.err == hipSuccess) hipLaunchKernelGGL(k_log, grid_for(n), dim3(256), 0, 0, dx, dout, dbad, n);
   int rc = finish(b);
   b.back(1, out);
   b.back(2, bad);

@@ -13,6 +13,14 @@ void emu_neg2log(const nt_u32* c, double* out, long n) {
   load_tables();
   for (long i = 0; i < n; ++i) out[i] = nt_neg2log_u32(c[i]);
 }
+void emu_log(const double* a, double* out, int* bad, long n) {
+  load_tables();
+  for (long i = 0; i < n; ++i) {
+    bool b = false;
+    out[i] = nt_log_fast(a[i], b);
+    bad[i] = b ? 1 : 0;
+  }
+}
 void emu_sincos(const nt_u32* c, double* s, double* co, long n) {
   load_tables();
   for (long i = 0; i < n; ++i) nt_sincos_2pi_u32(c[i], s[i], co[i]);

@@ -31,6 +31,7 @@ template <typename T>
 inline T nt_opaque(T x) { return x; }
 template <typename T>
 inline T nt_opaque_u(T x) { return x; }
+inline bool nt_pos_normal(double x) { return std::fpclassify(x) == FP_NORMAL && !std::signbit(x); }
 inline bool nt_zero_or_pos_normal(double x) {
   const int c = std::fpclassify(x);
   return c == FP_ZERO || (c == FP_NORMAL && !std::signbit(x));

@@ -6,7 +6,7 @@ hardware seeds (v_rsq_f64, v_rcp_f64) that carry a pseudo-random relative
 error of up to 2^-22; these run the real instructions. References: numpy long double (pinned to mpmath at 40 digits in
 test_math.py) for the random arguments, mpmath values from
 tests/golden/math_mpmath.json for the fixture's. Bounds: -2 ln u within
-2 ulp, sin and cos of the reference's rounded angle within 2 * 2^-53
+2 ulp, ln a of a LOG node within 2 ulp (the flag set off the positive normals), sin and cos of the reference's rounded angle within 2 * 2^-53
 absolute, exp within 1 ulp for |x| <= 708 (the range flag set outside it),
 sqrt within 1 ulp and 1 / (2 sqrt) within 2 ulp for positive normals, 1/b
 within 1 ulp for 2^-1022 <= |b| <= 2^1022 (the flag set outside); the
@@ -42,6 +42,7 @@ def dm():
     L.dm_neg2log.argtypes = [P(C.c_uint32), P(C.c_double), C.c_long]
     L.dm_sincos.argtypes = [P(C.c_uint32), P(C.c_double), P(C.c_double), C.c_long]
     L.dm_exp.argtypes = [P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
+    L.dm_log.argtypes = [P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
     L.dm_sqrt_q.argtypes = [P(C.c_double), P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
     L.dm_recip.argtypes = [P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
     L.dm_normal_pair.argtypes = [P(C.c_uint32)] * 3 + [P(C.c_double)] * 2 + [C.c_long]
@@ -122,6 +123,35 @@ def test_exp_within_one_ulp_and_its_range_flag(dm, fx):
     exact = mp_ulps(out[:len(fixture)], fx["exp"]["value"])
     print(f"exp worst {err.max():.3f} ulp (fixture vs mpmath {exact:.3f})")
     assert err.max() <= 1.0 and exact <= 1.0
+
+
+def test_log_within_two_ulp_and_its_range_flag(dm):
+    """ln(a) of a LOG node (nt_log_fast) on the device: within 2 ulp over the
+    positive normal range (10^6 arguments against long double, 300 of them
+    against mpmath); zero, subnormal, negative, infinite and NaN arguments
+    raise the flag."""
+    rng = np.random.default_rng(17)
+    x = np.ascontiguousarray(np.concatenate([
+        np.exp(rng.uniform(-700.0, 700.0, N // 2)), 1.0 + rng.uniform(-2.0 ** -8, 2.0 ** -8, N // 4),
+        rng.uniform(0.5, 2.0, N // 4), [2.2250738585072014e-308, 1.7976931348623157e308, 1.0],
+        [0.0, -0.0, 5e-324, -1.0, np.inf, -np.inf, np.nan]]))
+    special = 7
+    out = np.zeros(len(x))
+    bad = np.zeros(len(x), dtype=np.int32)
+    print(f"case log n={len(x)}", flush=True)
+    assert dm.dm_log(_p(x, C.c_double), _p(out, C.c_double), _p(bad, C.c_int), len(x)) == 0
+    assert (bad[:-special] == 0).all() and (bad[-special:] == 1).all()
+    xs, os_ = x[:-special], out[:-special]
+    keep = xs != 1.0
+    err = ulps(os_[keep], np.log(xs[keep].astype(LD)))
+    assert os_[~keep].max() == 0.0
+    pick = rng.choice(np.nonzero(keep)[0], 300, replace=False)
+    exact = 0.0
+    for i in pick:
+        want = mp.log(mp.mpf(float(xs[i])))
+        exact = max(exact, float(abs(mp.mpf(float(os_[i])) - want) / mp.mpf(float(np.spacing(abs(float(want)))))))
+    print(f"log worst {err.max():.3f} ulp (sample vs mpmath {exact:.3f})")
+    assert err.max() <= 2.0 and exact <= 2.0
 
 
 def test_sqrt_and_its_tangent_factor(dm, fx):

@@ -330,6 +330,34 @@ def test_merton_jump_tape_per_path(rocm, nt, mode):
     print(check_per_path(v, g, flat, 2048, OFFSET, 42, min_strict=0.94))  # measured 0.947
 
 
+def test_merton_jump_tape_several_markets(rocm, nt):
+    """The Merton tape priced for three input sets in one dispatch: its lanes
+    leave paths to the exception kernel in every market, each market with its
+    own lane bitmap, and each market's sums equal a separate replay's bit for
+    bit; a second, smaller dispatch of the three sets (on a smaller grid)
+    again equals a separate replay, so the first left its bitmaps clear, and
+    the oracle's sums within 1e-10."""
+    from conftest import merton_call_tape
+    flat = merton_call_tape(nt, MERTON, steps=32).flat()
+    x0 = np.array(flat["recorded_inputs"])
+    sets = np.stack([x0, x0 * 1.03, x0 * 0.97])
+    paths = 100_000
+    print(f"case merton32 markets=3 paths={paths}", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64")) as x:
+        assert "nt_replay_slow" in x.source()
+        many, _ = x.replay_many(sets, paths, OFFSET, 42)
+        for m in range(len(sets)):
+            x.set_inputs(sets[m])
+            one, _ = x.replay(paths, OFFSET, 42)
+            assert np.all(np.isfinite(one)) and np.array_equal(many[m], one), m
+        many2, _ = x.replay_many(sets, 20_000, OFFSET, 42)
+        x.set_inputs(sets[2])
+        one, _ = x.replay(20_000, OFFSET, 42)
+        assert np.array_equal(many2[2], one)
+    ref = oracle.replay_sums(flat, 20_000, OFFSET, 42, inputs=sets[2])
+    assert rel_err(one, ref, floor=1e-300) <= 1e-10
+
+
 def test_merton_jump_tape_converges_to_the_poisson_series(rocm, nt):
     """JumpModelsTest.mertonMonteCarloConvergesToThePoissonSeries at its own
     size (1,500,000 scenarios, seed 42, 128 steps): the device sums agree with

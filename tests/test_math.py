@@ -30,6 +30,7 @@ def lib():
     L = C.CDLL(str(out))
     P = C.POINTER
     L.emu_neg2log.argtypes = [P(C.c_uint32), P(C.c_double), C.c_long]
+    L.emu_log.argtypes = [P(C.c_double), P(C.c_double), P(C.c_int), C.c_long]
     L.emu_sincos.argtypes = [P(C.c_uint32), P(C.c_double), P(C.c_double), C.c_long]
     L.emu_sqrt.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
     L.emu_exp.argtypes = [P(C.c_double), P(C.c_double), C.c_long]
@@ -75,6 +76,40 @@ def test_neg2log_within_two_ulp(lib):
         u = (mp.mpf(int(ci)) + mp.mpf(0.5)) / mp.mpf(2) ** 32
         worst = max(worst, ulp_err(oi, -2 * mp.log(u)))
     assert worst <= 2.0, worst
+
+
+def log_arguments(n: int, seed: int) -> np.ndarray:
+    """Positive normal doubles over the whole exponent range, around 1 (where
+    ln a is small and F = 1), at the table's sector edges and the largest and
+    smallest normal numbers."""
+    rng = np.random.default_rng(seed)
+    a = np.concatenate([
+        np.exp(rng.uniform(-700.0, 700.0, n)),
+        1.0 + rng.uniform(-2.0 ** -8, 2.0 ** -8, n // 4),
+        rng.uniform(0.5, 2.0, n // 4),
+        np.ldexp(1.0 + np.arange(0, 257) / 256.0, rng.integers(-1000, 1000, 257)),
+        [1.0, np.nextafter(1.0, 2.0), np.nextafter(1.0, 0.0), 2.0, 0.5, np.sqrt(0.5), np.sqrt(2.0),
+         2.2250738585072014e-308, 1.7976931348623157e308, 1e-300, 1e300]])
+    return np.ascontiguousarray(a)
+
+
+def test_log_within_two_ulp_and_its_range_flag(lib):
+    """ln(a) of a LOG node (nt_log_fast: -1/2 of the Box-Muller routine's
+    -2 ln on a's own exponent and mantissa) within 2 ulp of mpmath over the
+    positive normal range; every other argument raises the flag."""
+    a = log_arguments(4000, 11)
+    out = np.zeros(len(a))
+    bad = np.zeros(len(a), dtype=np.int32)
+    lib.emu_log(_ptr(a, C.c_double), _ptr(out, C.c_double), _ptr(bad, C.c_int), len(a))
+    assert not bad.any()
+    worst = max(ulp_err(o, mp.log(mp.mpf(float(x)))) for x, o in zip(a, out) if x != 1.0)
+    assert worst <= 2.0, worst
+    assert out[np.nonzero(a == 1.0)[0][0]] == 0.0
+    sp = np.ascontiguousarray([0.0, -0.0, 5e-324, 2.2250738585072009e-308, -1.0, np.inf, -np.inf, np.nan])
+    out = np.zeros(len(sp))
+    bad = np.zeros(len(sp), dtype=np.int32)
+    lib.emu_log(_ptr(sp, C.c_double), _ptr(out, C.c_double), _ptr(bad, C.c_int), len(sp))
+    assert bad.all()
 
 
 def test_sincos_within_two_ulp(lib):
