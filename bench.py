@@ -145,14 +145,15 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
     }
 
 
-def measure_markets(rocm, flat, precision, paths, steps, warmup, seed, markets, ramp=0.5):
+def measure_markets(rocm, flat, precision, paths, steps, warmup, seed, markets, ramp=0.5, adjoints=True):
     """A revaluation ladder: `markets` input sets (the recorded inputs scaled by
-    1 + 1% * (m - markets/2)) priced per dispatch from shared draws."""
+    1 + 1% * (m - markets/2)) priced per dispatch from shared draws (with the
+    Greeks, or prices only)."""
     import numpy as np
 
     x0 = np.array(flat["recorded_inputs"])
     sets = np.stack([x0 * (1.0 + 0.01 * (m - markets // 2)) for m in range(markets)])
-    with rocm.Executable(flat, rocm.options(precision)) as x:
+    with rocm.Executable(flat, rocm.options(precision, adjoints=adjoints)) as x:
         info = x.info()
         t_ramp = time.perf_counter()
         while time.perf_counter() - t_ramp < ramp:
@@ -292,11 +293,15 @@ def other_workload(rocm, args) -> int:
     flat = workload_tape(args.workload, args.coefficients)
     if args.workload == "local_vol":
         desc = f"{desc}, k = {args.coefficients}"
+    if args.price_only:
+        desc = f"{desc.split(', value')[0]}, value only"
     print(f"[bench] {args.workload} {desc}: {len(flat['op'])} nodes, {paths:,} scenarios/step, {prec}",
           file=sys.stderr, flush=True)
-    if args.markets > 1:
-        m = measure_markets(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.markets, args.ramp)
-        out = {"metric": f"market-scenarios/sec for value+all Greeks ({prec}, {args.markets} input sets per dispatch)",
+    if args.markets > 1 or args.price_only:
+        m = measure_markets(rocm, flat, prec, paths, args.steps, args.warmup, seed, args.markets, args.ramp,
+                            adjoints=not args.price_only)
+        what = "value" if args.price_only else "value+all Greeks"
+        out = {"metric": f"market-scenarios/sec for {what} ({prec}, {args.markets} input sets per dispatch)",
                "value": m["value"], "unit": "market-scenarios/s", "n_gpus": 1, "steps": args.steps,
                "warmup": args.warmup, "ms_per_step": m["ms_per_step"], "higher_is_better": True, "scaling": "weak",
                "vs_baseline": None, "dtype": "f64" if prec == "fp64" else "f32",
@@ -513,6 +518,8 @@ def main() -> int:
     ap.add_argument("--no-reverse", action="store_true", help="skip the reverse-sweep comparison run")
     ap.add_argument("--markets", type=int, default=1,
                     help="with --workload/--precision: price this many input sets per dispatch from shared draws")
+    ap.add_argument("--price-only", action="store_true",
+                    help="with --markets: price the input sets without Greeks")
     ap.add_argument("--cpu-sample", type=int, default=3_000_000,
                     help="scenarios in the CPU baseline's timed sample (about 25 CPU-seconds on 16 threads)")
     ap.add_argument("--no-fp32", action="store_true")

@@ -83,7 +83,8 @@ enum {
  * knobs that the reference passes as engineOptions). Zero means default. */
 typedef struct nt_options {
   int32_t precision;        /* NT_FP64 or NT_FP32 */
-  int32_t adjoints;         /* 1: value + every first-order Greek; 0: price only */
+  int32_t adjoints;         /* 1: value + every first-order Greek; 0: price only (lowered in the tangent frame with
+                               no tangents unless mode is NT_MODE_REVERSE, so nt_exec_replay_many shares draws) */
   int32_t block;            /* threads per block; 0 = 256 */
   int32_t max_blocks;       /* grid cap; 0 = sized from occupancy */
   int32_t checkpoint;       /* NT_CKPT_* */
@@ -183,7 +184,8 @@ int nt_exec_replay(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_t seed
 /* Prices `markets` input sets (row-major [markets][n_inputs]) over the same paths and seed in one
  * dispatch; sums[m * n_sums_one + c] as nt_exec_replay's sums (n_sums_one of them) for set m. In tangent mode each path's
  * draws are generated once and shared by the sets in registers (a kernel is compiled per set count on
- * first use); a reverse-sweep executable replays the sets one after another. Either way the sums are
+ * first use; a price-only executable is in tangent mode unless built with NT_MODE_REVERSE); a
+ * reverse-sweep executable replays the sets one after another. Either way the sums are
  * bit-identical to `markets` separate nt_exec_replay calls with those inputs. The executable's bound
  * inputs are left unchanged. Replaces VulkanAadKernel.replayMany (nablatensor-engine-vulkan/.../
  * VulkanAadKernel.java:162-238), the draw-sharing form of ScenarioRunner ladders

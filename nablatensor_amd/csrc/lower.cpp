@@ -897,7 +897,12 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   for (int i = 0; i < t.n; ++i) fwd += fwd_cost(t.op[i], p.precision == NT_FP32);
   p.path_cost = fwd;
   p.cost_forward = fwd;
-  if (!p.adjoints && p.markets == 1 && !multi) return;
+  // Price only: the tangent frame with no tangents, the frame several input
+  // sets per dispatch take, so one set and several give the same bits and a
+  // price-only executable shares each path's draws across input sets. Forcing
+  // the reverse sweep keeps the step-by-step forward of the reverse frame.
+  const bool price_only = !p.adjoints;
+  if (price_only && o.mode == NT_MODE_REVERSE && p.markets == 1 && !multi) return;
   compute_deps(t, p);
   const LoopPlan& L = p.loop;
   const int le = L.found ? L.end() : 0;
@@ -934,9 +939,9 @@ void choose_mode(const TapeIR& t, const nt_options& o, Plan& p) {
   // estimate), reverse against tangent: 1.9-2.2 near the modes' crossover on
   // the local-volatility Asian (8 to 16 coefficients), 1.3-1.7 on C2-C4.
   constexpr double kReverseTime = 2.0;
-  const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || multi ||
+  const bool tangent = o.mode == NT_MODE_TANGENT || p.markets > 1 || multi || price_only ||
                        (p.adjoints && o.mode == NT_MODE_AUTO && fwd + tan < kReverseTime * (fwd + rev));
-  p.path_cost = fwd + (tangent ? tan : rev);
+  p.path_cost = fwd + (price_only ? 0.0 : tangent ? tan : rev);
   if (!tangent) return;
   p.mode = NT_MODE_TANGENT;
   p.ckpt = 0;

@@ -201,6 +201,28 @@ def test_replay_many_equals_separate_replays(rocm, tapes, name, mode, paths):
     assert np.max(np.abs(many[1][2:] - ref[2:])) <= 1e-10 * np.max(np.abs(ref[2:]))
 
 
+@pytest.mark.parametrize("name,paths", [("C3", 100_000), ("C4", 20_000)])
+def test_price_only_replay_many_shares_draws(rocm, tapes, name, paths):
+    """A price-only executable runs in the tangent frame with no tangents, so
+    several input sets share each path's draws in one dispatch, each set's
+    sums equal to a separate price-only replay bit for bit and the price to
+    the oracle's to 1e-10."""
+    t = tapes[name]
+    x0 = np.array(t["recorded_inputs"])
+    sets = np.stack([x0 * 0.97, x0, x0 * 1.03])
+    print(f"case {name} price only markets=3 paths={paths}", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", adjoints=False)) as x:
+        assert x.info()["mode"] == 2
+        many, _ = x.replay_many(sets, paths, OFFSET, 42)
+        for m in range(len(sets)):
+            x.set_inputs(sets[m])
+            one, _ = x.replay(paths, OFFSET, 42)
+            assert np.array_equal(many[m], one), m
+            assert np.all(one[2:] == 0.0)
+    ref = oracle.replay_sums(t, paths, OFFSET, 42, inputs=sets[2], adjoints=False)
+    assert rel_err(many[2][:2], ref[:2], floor=1e-300) <= 1e-10
+
+
 def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
     t = tapes["C2"]
     with rocm.Executable(t, rocm.options("fp64")) as x:

@@ -223,10 +223,19 @@ def test_checkpointed_straight_line_exception_kernel(nt, rocm, precision):
 
 
 def test_price_only_and_moved_inputs(rocm, tapes):
+    """Price only, at inputs other than the recorded ones: by default in the
+    tangent frame with no tangents (the frame several input sets per dispatch
+    use), and with the reverse frame forced the step-by-step forward pass,
+    bit-equal to the oracle."""
     flat = tapes["C3"]
     x = [95.0, 101.0, 0.3, 0.01, 0.75]
-    sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False, libm=1), 200, inputs=x, rocm=rocm)
     ov, _ = oracle.replay_paths(flat, 200, OFFSET, 42, inputs=x, threads=1)
+    assert _mode(rocm, flat, adjoints=False) == "tangent"
+    opts = rocm.options("fp64", adjoints=False, libm=1)
+    sums, v, _ = run_emulated(flat, opts, 200, inputs=x, rocm=rocm)
+    assert_values_match(v, ov, rocm.lower(flat, opts))
+    assert np.all(sums[2:] == 0.0)
+    sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False, libm=1, mode=1), 200, inputs=x, rocm=rocm)
     assert np.array_equal(v, ov)
     assert np.all(sums[2:] == 0.0)
 
@@ -319,7 +328,9 @@ def test_cost_model_picks_the_cheaper_mode(rocm, tapes):
     chain = _product_chain(40)
     assert _mode(rocm, chain) == "reverse"
     assert _mode(rocm, chain, mode=2) == "tangent"
-    assert _mode(rocm, tapes["C2"], adjoints=False) == "reverse"  # price only: no derivative code at all
+    # price only: the tangent frame with no tangents, unless the reverse frame is forced
+    assert _mode(rocm, tapes["C2"], adjoints=False) == "tangent"
+    assert _mode(rocm, tapes["C2"], adjoints=False, mode=1) == "reverse"
 
 
 def test_product_chain_both_modes_match_oracle(rocm):
