@@ -54,24 +54,27 @@ COUNTER_FILES = {"C1": "european1", "C2": "asian252", "C3": "barrier252", "C4": 
                  "C5": "worstof16", "asian_weekdays": "asian_weekdays252", "local_vol": "local_vol24"}
 
 
-def measured_counters(workload: str, precision: str, info: dict) -> dict:
+def measured_counters(workload: str, precision: str, info: dict, grid: int | None = None) -> dict:
     """From the committed rocprofv3 summary of this workload and precision, the
     lines that match this kernel (derivative mode, checkpoint policy, segment
-    length, straight-line segments and VGPRs): `traffic` (HBM bytes per
-    dispatch, FETCH_SIZE and WRITE_SIZE copy-calibrated) and `executed`
-    (executed FLOPs per scenario from the VALU counters)."""
+    length, straight-line segments and VGPRs, and, when `grid` is given, the
+    blocks the dispatch launches): `traffic` (HBM bytes per dispatch,
+    FETCH_SIZE and WRITE_SIZE copy-calibrated) and `executed` (executed FLOPs
+    per scenario from the VALU counters)."""
     out = {}
     path = ROOT / "profiles" / f"nt_replay_{COUNTER_FILES.get(workload, workload)}_{precision}_counters.md"
     if not path.exists():
         return out
     want = {"mode": info["mode"], "checkpoint": info["checkpoint"], "seg_len": info["seg_len"],
             "segments": info["n_segments"], "vgprs": info["vgprs"]}
+    if grid is not None:
+        want["grid"] = grid
     for line in path.read_text().splitlines():
         kind = line.split(":", 1)[0]
         if kind not in ("traffic", "executed"):
             continue
         kv = dict(item.split("=") for item in line.split()[1:])
-        if all(int(kv[k]) == v for k, v in want.items() if k in kv):
+        if all(k in kv and int(kv[k]) == v for k, v in want.items()):
             out[kind] = {k: float(v) for k, v in kv.items() if k not in want}
             out[kind]["source"] = str(path.relative_to(ROOT))
     return out
@@ -94,6 +97,7 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
     with rocm.Executable(flat, rocm.options(precision, checkpoint=policy, seg_len=seg, mode=mode, waves=waves,
                                                 max_blocks=max_blocks, basis=basis, roll=roll, block=block)) as x:
         info = x.info()
+        grid = x.grid(paths)[0]
         cost = cost_model(x.source())
         # The GPU's clocks ramp under sustained load: replay for `ramp` seconds
         # (untimed) before the warmup steps, so a short --warmup does not time
@@ -115,7 +119,7 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
     # The committed counter summaries are per workload at the scenarios per dispatch it names.
     from nablatensor_amd import workloads
 
-    counted = measured_counters(workload, precision, info) if paths == workloads.DESCRIPTIONS[workload][1] else {}
+    counted = measured_counters(workload, precision, info, grid) if paths == workloads.DESCRIPTIONS[workload][1] else {}
     traffic = counted.get("traffic")
     executed = counted.get("executed")
     achieved = fl * paths / avg_replay_s / 1e12
@@ -136,12 +140,12 @@ def measure(rocm, flat, precision, paths, steps, warmup, seed, policy, seg, mode
                      "executed_frac": None if ex_achieved is None else ex_achieved / peak,
                      "valu_issue": None if executed is None else executed.get("valu_issue"),
                      "executed_source": None if executed is None else executed["source"],
-                     "algorithmic_bytes": 8 * (len(flat["input_node"]) + info["grid_cap"] * (2 + len(flat["input_node"]))),
+                     "algorithmic_bytes": 8 * (len(flat["input_node"]) + grid * (2 + len(flat["input_node"]))),
                      "flops_per_scenario": fl, "convention": "NT-FLOP v1"},
         "kernel": {**{k: info[k] for k in ("vgprs", "sgprs", "scratch_bytes", "lds_bytes", "loop_period",
                                            "loop_iters", "seg_len", "n_segments", "checkpoint", "tape_slots",
                                            "grid_cap")},
-                   "mode": MODES[info["mode"]], "cost_model": cost},
+                   "grid": grid, "mode": MODES[info["mode"]], "cost_model": cost},
     }
 
 

@@ -215,8 +215,8 @@ int nt_exec_replay_paths(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_
  * bit-identical to nt_exec_replay's for the same inputs, paths, offset and
  * seed. The per-block partials (grid x channels doubles, twice that when the
  * tape has an exception kernel), the bitmap of lanes that left paths to the
- * exception kernel (one bit per lane of the grid, in a fixed 128 KiB region of
- * its own, for grids of up to 2^20 lanes) and a reverse sweep's per-lane tape, if the
+ * exception kernel (one bit per lane of the grid, in a fixed 512 KiB region of
+ * its own, for grids of up to 2^22 lanes) and a reverse sweep's per-lane tape, if the
  * executable keeps one in device memory, live in a static array of
  * NT_NOALLOC_SCRATCH_BYTES per device; a dispatch that needs more is refused
  * with NT_E_INVALID before anything is launched. Calls that overlap in time on
@@ -225,6 +225,14 @@ int nt_exec_replay_noalloc(nt_exec *exec, const double *d_inputs, uint64_t paths
                            double *d_sums, int32_t n_sums, void *stream);
 
 int nt_exec_info_get(const nt_exec *exec, nt_exec_info *info);
+
+/* Blocks (*grid) of *block threads that a single-set dispatch of `paths`
+ * launches (nt_exec_replay, nt_exec_replay_noalloc, and each set count of
+ * nt_exec_replay_many). At most info.grid_cap; a long path launches more
+ * blocks than the device holds at once. A measurement aid with no counterpart
+ * in the reference, whose launch geometry is fixed per dispatch
+ * (DeviceAadExecutable.java:196-200). */
+int nt_exec_grid(const nt_exec *exec, uint64_t paths, int32_t *grid, int32_t *block);
 
 /* Copy of the generated source (same *len protocol as nt_lower). */
 int nt_exec_source(const nt_exec *exec, char *source, int64_t *len);

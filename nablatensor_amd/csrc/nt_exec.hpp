@@ -68,7 +68,8 @@ struct nt_exec {
                                 //   (grown with the dispatch; the count is zero between dispatches)
   size_t flags_bytes = 0;
   int dev = 0;
-  int grid_cap = 1;
+  int grid_cap = 1;     // most blocks a dispatch launches (partials, flags and tape are sized for it)
+  int resident = 1;     // blocks the device holds at once (occupancy x compute units)
   int cus = 0;          // compute units of the device
   bool fixed_grid = false;  // the caller capped the grid (nt_options.max_blocks)
   std::vector<double> inputs;

@@ -47,9 +47,10 @@ void* g_scratch[kMaxDevices] = {};  // device address of each device's copy of `
 constexpr size_t round_up_256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
 // The flag region: the count and one bitmap word per 64 lanes (the layout of
-// ntr::flags_bytes_for for one input set), for up to kFlagLanes lanes (2^20;
-// a resident grid on MI355X holds 256 CUs x 2,048).
-constexpr uint64_t kFlagLanes = 1ull << 20;
+// ntr::flags_bytes_for for one input set), for up to kFlagLanes lanes (2^22:
+// a resident grid on MI355X holds at most 256 CUs x 2,048 lanes, and a
+// dispatch launches at most 8 resident grids).
+constexpr uint64_t kFlagLanes = 1ull << 22;
 constexpr size_t kFlagBytes = round_up_256((1 + kFlagLanes / 64) * sizeof(uint64_t));
 
 // The device address of `scratch` on device `dev`, looked up once per device
@@ -94,7 +95,7 @@ extern "C" int nt_exec_replay_noalloc(nt_exec* x, const double* d_inputs, uint64
   const uint64_t lanes = static_cast<uint64_t>(grid) * static_cast<uint64_t>(x->low.plan.block);
   if (lanes > kFlagLanes) {
     return ntr::fail(NT_E_INVALID, "the dispatch's grid has more lanes than the allocation-free entry point's "
-                                   "flags cover (2^20)");
+                                   "flags cover (2^22)");
   }
   const int rows = ntr::partial_rows(grid, x->fn_slow != nullptr);
   const size_t partial_bytes = round_up_256(sizeof(double) * static_cast<size_t>(rows) * static_cast<size_t>(nch));

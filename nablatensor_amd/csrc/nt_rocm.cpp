@@ -401,20 +401,44 @@ namespace ntr {
 // dispatch gets about kLanePaths paths per lane instead, in a whole number of
 // blocks per compute unit (a CU holding one block more than the others sets
 // the kernel's time). Measured on the European call, 10^6 paths: 2048 blocks
-// 17.4 us, 768 blocks 13.1 us (fp64); 13.4 and 10.4 us (fp32). A long path
-// (the 252-step Asian) is fastest on the full resident grid.
+// 17.4 us, 768 blocks 13.1 us (fp64); 13.4 and 10.4 us (fp32).
+//
+// A long path is VALU-bound, and a resident grid that strides over all the
+// paths ends in a tail: the lanes whose last round has a path run it while
+// the rest of the chip idles, and a SIMD left with one wave issues far below
+// its rate. More blocks than the device holds let the dispatcher hand each
+// freed slot the next block, so a long path gets the fewest whole blocks per
+// compute unit that leave at most kLongLanePaths paths per lane, up to
+// kOversubscribe times the resident grid (a reverse sweep that keeps its tape
+// in device memory stays on the resident grid: its tape is sized per lane).
+// Whole blocks per CU matter as much as the count: a grid of q CUs' worth
+// plus r blocks leaves r CUs one block longer than the rest. Measured on one
+// MI355X (three interleaved runs per grid, spread below 0.5 %), kernel time
+// at the resident grid, at 16 blocks per CU (4,096) and at 4,112 blocks:
+// Asian fp64 2M 0.894 / 0.838 / 0.869 ms, Asian fp32 2M 0.298 / 0.291 /
+// 0.300 ms; weekday Asian fp64 2M 1.087 ms resident, 1.011 ms at 4,096
+// blocks, 1.041 ms at 4,224; worst-of fp32 10^6 2.701 ms resident, 2.544 ms at 8 blocks per CU,
+// 3.343 ms at 576 blocks. Barrier fp64 20M 14.25 / 12.80 ms at 40 blocks per
+// CU; Heston-Asian 10M 25.08 / 23.88 ms at 24.
 constexpr double kShortPath = 1000;
 constexpr uint64_t kLanePaths = 4;
+constexpr uint64_t kLongLanePaths = 2;
+constexpr int kOversubscribe = 8;
 
 int grid_for(const nt_exec* x, uint64_t paths) {
-  const int block = x->low.plan.block;
-  const uint64_t need = (paths + static_cast<uint64_t>(block) - 1) / static_cast<uint64_t>(block);
-  int grid = std::max(1, static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap))));
-  if (!x->fixed_grid && x->cus > 0 && x->low.plan.path_cost < kShortPath) {
-    const uint64_t per_cu = paths / (static_cast<uint64_t>(block) * kLanePaths) / static_cast<uint64_t>(x->cus);
-    if (per_cu >= 1 && per_cu * static_cast<uint64_t>(x->cus) < static_cast<uint64_t>(grid)) {
-      grid = static_cast<int>(per_cu) * x->cus;
-    }
+  const uint64_t block = static_cast<uint64_t>(x->low.plan.block);
+  const uint64_t need = (paths + block - 1) / block;
+  if (x->fixed_grid) return std::max(1, static_cast<int>(std::min<uint64_t>(need, static_cast<uint64_t>(x->grid_cap))));
+  const uint64_t resident = static_cast<uint64_t>(x->resident);
+  int grid = std::max(1, static_cast<int>(std::min(need, resident)));
+  if (x->cus <= 0) return grid;
+  const uint64_t cus = static_cast<uint64_t>(x->cus);
+  if (x->low.plan.path_cost < kShortPath) {
+    const uint64_t per_cu = paths / (block * kLanePaths) / cus;
+    if (per_cu >= 1 && per_cu * cus < static_cast<uint64_t>(grid)) grid = static_cast<int>(per_cu * cus);
+  } else if (need > resident) {
+    const uint64_t per_cu = (need + kLongLanePaths * cus - 1) / (kLongLanePaths * cus);
+    grid = static_cast<int>(std::min(std::max(per_cu * cus, resident), static_cast<uint64_t>(x->grid_cap)));
   }
   return grid;
 }
@@ -550,8 +574,10 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
          "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
   NT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, x->dev), "hipDeviceGetAttribute");
   const nt_options o = options ? *options : nt_options{};
-  x->grid_cap = std::max(1, per_cu * cus);
+  x->resident = std::max(1, per_cu * cus);
   x->cus = cus;
+  const bool long_path = x->low.plan.path_cost >= ntr::kShortPath && x->low.plan.tape_slots == 0;
+  x->grid_cap = long_path ? ntr::kOversubscribe * x->resident : x->resident;
   if (o.max_blocks > 0) {
     x->grid_cap = o.max_blocks;
     x->fixed_grid = true;
@@ -904,6 +930,15 @@ int nt_exec_info_get(const nt_exec* x, nt_exec_info* info) {
   if (!x) return fail(NT_E_CLOSED, "executable is closed");
   if (!info) return fail(NT_E_INVALID, "info is null");
   *info = x->info;
+  return NT_OK;
+}
+
+int nt_exec_grid(const nt_exec* x, uint64_t paths, int32_t* grid, int32_t* block) {
+  if (!x) return fail(NT_E_CLOSED, "executable is closed");
+  if (!grid || !block) return fail(NT_E_INVALID, "grid or block is null");
+  if (paths == 0) return fail(NT_E_INVALID, "paths must be positive");
+  *grid = grid_for(x, paths);
+  *block = x->low.plan.block;
   return NT_OK;
 }
 

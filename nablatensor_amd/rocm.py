@@ -23,7 +23,7 @@ ABI_VERSION = 3
 
 EXPORTS = ("nt_probe", "nt_device_name", "nt_lower", "nt_compile_check", "nt_exec_create", "nt_exec_set_inputs",
            "nt_exec_replay", "nt_exec_replay_many", "nt_exec_replay_paths", "nt_exec_replay_noalloc",
-           "nt_exec_info_get", "nt_exec_source",
+           "nt_exec_info_get", "nt_exec_grid", "nt_exec_source",
            "nt_exec_destroy", "nt_last_error", "nt_abi_version")
 
 
@@ -85,6 +85,7 @@ def lib() -> C.CDLL:
         L.nt_exec_replay_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64,
                                              C.c_void_p, C.c_int32, C.c_void_p]
         L.nt_exec_info_get.argtypes = [C.c_void_p, C.POINTER(NtExecInfo)]
+        L.nt_exec_grid.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]
         L.nt_exec_source.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_int64)]
         L.nt_exec_destroy.argtypes = [C.c_void_p]
         if L.nt_abi_version() != ABI_VERSION:
@@ -243,6 +244,12 @@ class Executable:
         i = NtExecInfo()
         _check(lib().nt_exec_info_get(self._h, C.byref(i)))
         return i.as_dict()
+
+    def grid(self, paths: int) -> tuple[int, int]:
+        """(blocks, threads per block) of a single-set dispatch of `paths`."""
+        g, b = C.c_int32(0), C.c_int32(0)
+        _check(lib().nt_exec_grid(self._h, paths, C.byref(g), C.byref(b)))
+        return g.value, b.value
 
     def source(self) -> str:
         n = C.c_int64(0)

@@ -145,6 +145,26 @@ def test_committed_counters_cover_the_planned_kernels(workload, precision, mode,
     assert got["traffic"]["bytes"] > 0 and got["executed"]["flops_per_scenario"] > 0
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("workload,precision,mode,roll", COUNTED)
+def test_committed_counters_match_the_launch_grid(workload, precision, mode, roll):
+    """On the device, the committed counter lines of each reported kernel were
+    taken at the grid the engine launches today for the workload's scenarios
+    per dispatch (the grid sets the partial rows, the HBM bytes and the
+    tail), so a change of launch geometry that leaves the reported traffic
+    stale fails here."""
+    from nablatensor_amd import rocm, workloads
+
+    paths = workloads.DESCRIPTIONS[workload][1]
+    print(f"case {workload} {precision} mode={mode} roll={roll} paths={paths}", flush=True)
+    with rocm.Executable(bench.workload_tape(workload), rocm.options(precision, mode=mode, roll=roll)) as x:
+        info = x.info()
+        grid, block = x.grid(paths)
+    assert block == info["block"] and 1 <= grid <= info["grid_cap"]
+    got = bench.measured_counters(workload, precision, info, grid)
+    assert set(got) == {"traffic", "executed"}, (workload, precision, grid, info)
+
+
 def test_adjoint_vs_bump_prices_the_eleven_sets(monkeypatch):
     """The bump leg replays the base market and +h, -h per input (price-only,
     the same paths and seed), takes central differences, and divides the 11

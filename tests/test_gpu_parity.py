@@ -223,6 +223,43 @@ def test_price_only_replay_many_shares_draws(rocm, tapes, name, paths):
     assert rel_err(many[2][:2], ref[:2], floor=1e-300) <= 1e-10
 
 
+def test_launch_grid(rocm, tapes):
+    """The launch geometry: a long path on the fewest whole blocks per compute
+    unit that leave at most two paths per lane, up to 8 resident grids; a
+    short path (the European) on at most one resident grid; a reverse sweep
+    with its tape in device memory on the resident grid; a caller's
+    max_blocks as a hard cap."""
+    import ctypes
+
+    hip = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so.7")  # the runtime libnt_rocm.so links
+    n = ctypes.c_int(0)
+    assert hip.hipDeviceGetAttribute(ctypes.byref(n), 63, 0) == 0  # hipDeviceAttributeMultiprocessorCount
+    cus = n.value
+    print(f"case launch grid C1 C2, {cus} CUs", flush=True)
+    with rocm.Executable(tapes["C2"], rocm.options("fp64")) as x:
+        info = x.info()
+        assert info["mode"] == 2 and info["tape_slots"] == 0
+        resident = info["grid_cap"] // 8
+        assert resident % cus == 0
+        need = -(-2_000_000 // 256)
+        assert x.grid(2_000_000) == (-(-need // (2 * cus)) * cus, 256)
+        assert x.grid(2_000_000)[0] * 256 * 2 >= 2_000_000
+        assert x.grid(100) == (1, 256)
+        assert x.grid(resident * 256)[0] == resident
+        assert x.grid(resident * 256 + 1)[0] == resident
+        assert x.grid(10**12)[0] == info["grid_cap"]
+        with pytest.raises(rocm.NtError):
+            x.grid(0)
+    with rocm.Executable(tapes["C2"], rocm.options("fp64", max_blocks=100)) as x:
+        assert x.info()["grid_cap"] == 100 and x.grid(2_000_000)[0] == 100 and x.grid(1000)[0] == 4
+    with rocm.Executable(tapes["C2"], rocm.options("fp64", mode=1, checkpoint=2)) as x:
+        info = x.info()
+        assert info["tape_slots"] > 0 and x.grid(2_000_000)[0] == info["grid_cap"]
+    with rocm.Executable(tapes["C1"], rocm.options("fp64")) as x:
+        info = x.info()
+        assert x.grid(1_000_000)[0] <= info["grid_cap"] and x.grid(10**9)[0] == info["grid_cap"]
+
+
 def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
     t = tapes["C2"]
     with rocm.Executable(t, rocm.options("fp64")) as x:
