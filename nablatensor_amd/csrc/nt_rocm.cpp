@@ -409,8 +409,12 @@ namespace ntr {
 // its rate. More blocks than the device holds let the dispatcher hand each
 // freed slot the next block, so a long path gets the fewest whole blocks per
 // compute unit that leave at most kLongLanePaths paths per lane, up to
-// kOversubscribe times the resident grid (a reverse sweep that keeps its tape
-// in device memory stays on the resident grid: its tape is sized per lane).
+// kOversubscribe times the resident grid. A reverse sweep that keeps its tape
+// in device memory sizes that tape per lane of the largest grid, so it gets
+// the larger grid only while the tape stays within kTapeBudget, and only with
+// two or more waves per SIMD resident: at one wave per SIMD its tape traffic,
+// not the tail, sets the time (local-volatility tape, 388 VGPRs: 8.89 ms
+// resident, 9.33 ms on 8 resident grids).
 // Whole blocks per CU matter as much as the count: a grid of q CUs' worth
 // plus r blocks leaves r CUs one block longer than the rest. Measured on one
 // MI355X (three interleaved runs per grid, spread below 0.5 %), kernel time
@@ -424,6 +428,20 @@ constexpr double kShortPath = 1000;
 constexpr uint64_t kLanePaths = 4;
 constexpr uint64_t kLongLanePaths = 2;
 constexpr int kOversubscribe = 8;
+constexpr uint64_t kTapeBudget = 1ull << 30;
+
+// The largest grid a dispatch of this executable launches (partials, lane
+// flags and tape are sized for it).
+int grid_cap_for(const nt_exec* x, int per_cu, int cus) {
+  const int resident = std::max(1, per_cu * cus);
+  if (x->low.plan.path_cost < kShortPath || cus <= 0) return resident;
+  const uint64_t tape_block = tape_bytes_per_lane(x) * static_cast<uint64_t>(x->low.plan.block);
+  if (tape_block == 0) return kOversubscribe * resident;
+  if (per_cu * x->low.plan.block < 2 * 256) return resident;  // fewer than two waves per SIMD
+  const uint64_t by_tape = kTapeBudget / tape_block / static_cast<uint64_t>(cus) * static_cast<uint64_t>(cus);
+  return static_cast<int>(std::min<uint64_t>(static_cast<uint64_t>(kOversubscribe) * resident,
+                                             std::max<uint64_t>(resident, by_tape)));
+}
 
 int grid_for(const nt_exec* x, uint64_t paths) {
   const uint64_t block = static_cast<uint64_t>(x->low.plan.block);
@@ -576,8 +594,7 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   const nt_options o = options ? *options : nt_options{};
   x->resident = std::max(1, per_cu * cus);
   x->cus = cus;
-  const bool long_path = x->low.plan.path_cost >= ntr::kShortPath && x->low.plan.tape_slots == 0;
-  x->grid_cap = long_path ? ntr::kOversubscribe * x->resident : x->resident;
+  x->grid_cap = ntr::grid_cap_for(x.get(), per_cu, cus);
   if (o.max_blocks > 0) {
     x->grid_cap = o.max_blocks;
     x->fixed_grid = true;

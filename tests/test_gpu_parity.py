@@ -227,8 +227,8 @@ def test_launch_grid(rocm, tapes):
     """The launch geometry: a long path on the fewest whole blocks per compute
     unit that leave at most two paths per lane, up to 8 resident grids; a
     short path (the European) on at most one resident grid; a reverse sweep
-    with its tape in device memory on the resident grid; a caller's
-    max_blocks as a hard cap."""
+    with its tape in device memory on as many blocks as 1 GiB of tape holds;
+    a caller's max_blocks as a hard cap."""
     import ctypes
 
     hip = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so.7")  # the runtime libnt_rocm.so links
@@ -255,6 +255,7 @@ def test_launch_grid(rocm, tapes):
     with rocm.Executable(tapes["C2"], rocm.options("fp64", mode=1, checkpoint=2)) as x:
         info = x.info()
         assert info["tape_slots"] > 0 and x.grid(2_000_000)[0] == info["grid_cap"]
+        assert info["grid_cap"] * 256 * info["tape_slots"] * 8 <= 1 << 30 and info["grid_cap"] % cus == 0
     with rocm.Executable(tapes["C1"], rocm.options("fp64")) as x:
         info = x.info()
         assert x.grid(1_000_000)[0] <= info["grid_cap"] and x.grid(10**9)[0] == info["grid_cap"]
