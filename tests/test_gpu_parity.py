@@ -261,6 +261,28 @@ def test_launch_grid(rocm, tapes):
         assert x.grid(1_000_000)[0] <= info["grid_cap"] and x.grid(10**9)[0] == info["grid_cap"]
 
 
+@pytest.mark.parametrize("mode", [2, 1])
+def test_sums_do_not_depend_on_the_grid(rocm, tapes, mode):
+    """The launch grid decides only which lane takes which path and the order
+    of the partial sums: the default grid (more blocks than the device holds)
+    and a grid capped at 256 blocks give the same sums to rounding, and the
+    same per-path values bit for bit."""
+    t = tapes["C2"]
+    paths = 1_000_000
+    print(f"case C2 mode={mode} grid independence, {paths} paths", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
+        g = x.grid(paths)[0]
+        assert g * 256 < paths  # more than one path per lane, more blocks than 256
+        a, _ = x.replay(paths, OFFSET, 42)
+        va, ga = x.replay_paths(2_000, OFFSET, 42)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode, max_blocks=256)) as x:
+        assert x.grid(paths)[0] == 256 != g
+        b, _ = x.replay(paths, OFFSET, 42)
+        vb, gb = x.replay_paths(2_000, OFFSET, 42)
+    assert rel_err(a, b, floor=1e-300) <= 1e-12
+    assert np.array_equal(va, vb) and np.array_equal(ga, gb)
+
+
 def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
     t = tapes["C2"]
     with rocm.Executable(t, rocm.options("fp64")) as x:
