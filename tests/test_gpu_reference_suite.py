@@ -1,0 +1,233 @@
+"""The reference's engine-agnostic hot-path tests, run against the rocm engine
+through the host layer, with the reference's workloads, seeds and
+tolerances, and beside each the tighter bar this engine holds against the
+oracle:
+
+* AadOpConformanceTest (AadOpConformanceTest.java:50-120): a tape touching
+  every AadOpEnum, RANDU included, 200,000 scenarios, seed 0x5EED5;
+* BitReproTest (BitReproTest.java:33-62): the Asian at 64 steps within 1e-6
+  of the oracle, and the European's adjoint delta against a central bump;
+* Fp32BackendComparisonTest (Fp32BackendComparisonTest.java:57-72,319-413):
+  the 50-fixing price-space Asian in fp32 against the fp64 oracle, 60 settled
+  repeats and a burst of 25 shifted offsets;
+* OpenClAsianParityTest (OpenClAsianParityTest.java:75-181): the same tape
+  swept in reverse through a checkpointed straight line (segments of 48 and 96
+  nodes) against the plain kernel at offset 0x100000003, spot 100 and 101,
+  and 40 repeats bit-identical.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+
+from nablatensor_amd import bumps
+
+OFFSET = 0x100000003
+ALL_OPS = set(range(15))  # AadOpEnum ordinals CONST .. ABS
+
+
+def every_op(rec):
+    """AadOpConformanceTest.everyOp (AadOpConformanceTest.java:57-68)."""
+    x = rec.input("x", 1.3)
+    y = rec.input("y", 0.7)
+    z = rec.randn()
+    u = rec.randu()
+    a = x.add(y).sub(0.1)
+    b = x.mul(y).div(x.add(0.5))
+    c = a.neg().exp().add(b.abs())
+    d = c.add(1.0).log().sqrt()
+    e = d.max(z.mul(0.01)).min(x.mul(2.0))
+    rec.output(e.add(u.mul(y)))
+
+
+def price_space_asian(rec, fixings=50, s0=100.0, strike=100.0, vol=0.20, rate=0.03, maturity=1.0):
+    """The price-space GBM Asian of Fp32BackendComparisonTest.java:57-72 and
+    OpenClAsianParityTest.java:55-71."""
+    spot = rec.input("spot", s0)
+    v = rec.input("vol", vol)
+    dt = maturity / fixings
+    drift = v.mul(v).mul(-0.5 * dt).add(rate * dt)
+    diffusion = v.mul(math.sqrt(dt))
+    price = spot
+    total = rec.constant(0.0)
+    for _ in range(fixings):
+        price = price.mul(drift.add(diffusion.mul(rec.randn())).exp())
+        total = total.add(price)
+    rec.output(total.mul(1.0 / fixings).sub(strike).max(0.0).mul(math.exp(-rate * maturity)))
+
+
+@pytest.fixture(scope="module")
+def rocm():
+    from nablatensor_amd import rocm as r
+    assert r.probe() > 0, "no gfx950 device visible to libnt_rocm.so"
+    return r
+
+
+def _fp64(nt):
+    return nt.AadOptions.defaults().withPrecision(nt.AadOptions.PrecisionEnum.FLOAT64)
+
+
+def _fp32(nt):
+    return nt.AadOptions.defaults().withPrecision(nt.AadOptions.PrecisionEnum.FLOAT32)
+
+
+def _op_ordinal(op) -> int:
+    return int(op.value) if hasattr(op, "value") else int(op)
+
+
+def test_every_aad_op_is_exercised_by_the_conformance_tape(nt):
+    tape = nt.AadRecorder.record(every_op)
+    assert {_op_ordinal(tape.op(i)) for i in range(tape.size())} == ALL_OPS
+
+
+@pytest.mark.gpu
+def test_every_available_backend_matches_the_oracle_or_declines(nt):
+    n, seed = 200_000, 0x5EED5
+    tape = nt.AadRecorder.record(every_op)
+    flat = tape.flat()
+    want = oracle.to_result(oracle.replay_sums(flat, n, 0, seed), n)
+    fp64 = _fp64(nt)
+    engines = [e for e in nt.AadEngines.available(fp64)]
+    assert [e.name() for e in engines] == ["rocm"]
+    for engine in engines:
+        print(f"case every-op tape on {engine.name()}, {n} scenarios, seed {seed:#x}", flush=True)
+        exe = engine.compile(tape, fp64)
+        got = exe.replaySafe(n, seed)
+        exe.close()
+        assert got.paths() == n
+        price, grads = got.value(), np.asarray(got.gradients())
+        # the reference's bar
+        assert abs(price - want["price"]) <= 5e-4 + 5e-4 * abs(want["price"])
+        assert np.all(np.abs(grads - want["gradient"]) <= 5e-3 + 5e-3 * np.abs(want["gradient"]))
+        # this engine's: the sums to 1e-10
+        assert abs(price - want["price"]) <= 1e-10 * abs(want["price"])
+        assert rel_err(grads, want["gradient"], floor=1e-300) <= 1e-10
+
+
+@pytest.mark.gpu
+def test_every_available_backend_reproduces_the_oracle(nt):
+    """BitReproTest.everyAvailableBackendReproducesTheOracle: the Asian at 64
+    steps, 200,000 scenarios, seed 20260830, within 1e-6 / (1 + |x|) on the
+    price and each Greek (EngineComparison.java:38-55)."""
+    n, seed = 200_000, 20260830
+    mc = (nt.MonteCarlo.of(nt.Products.asianCall()).market(nt.EquityMarket.atmOneYear())
+          .steps(64).greeks().fp64().on("rocm").build())
+    print(f"case Asian 64 steps on rocm, {n} scenarios, seed {seed}", flush=True)
+    v = mc.run(n, seed)
+    flat = mc.tape().flat()
+    mc.close()
+    want = oracle.to_result(oracle.replay_sums(flat, n, 0, seed), n)
+    got = np.array([v.price(), *v.gradients()])
+    ref = np.array([want["price"], *want["gradient"]])
+    assert np.all(np.abs(got - ref) / (1.0 + np.abs(ref)) <= 1e-6)
+    assert rel_err(got, ref, floor=1e-300) <= 1e-10
+
+
+@pytest.mark.gpu
+def test_adjoint_delta_agrees_with_central_bump(nt, rocm):
+    """BitReproTest.adjointDeltaAgreesWithCentralBump: the European at one
+    step, 200,000 scenarios, seed 20260830, central bump of 5e-3 max(1, |x|)
+    with common random numbers (BumpCrossCheck.java:33-49): |adjoint delta -
+    bump delta| < 5e-3."""
+    n, seed = 200_000, 20260830
+    tape = nt.record(nt.Products.europeanCall(), nt.EquityMarket.atmOneYear(), nt.TimeGrid.uniform(1))
+    flat = tape.flat()
+    print(f"case European adjoint delta vs central bump, {n} scenarios", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64")) as x:
+        sums, _ = x.replay(n, 0, seed)
+    adjoint = sums[2:] / n
+    sets, h = bumps.central_bump_sets(flat["recorded_inputs"], 5e-3)
+    with rocm.Executable(flat, rocm.options("fp64", adjoints=False)) as x:
+        many, _ = x.replay_many(sets, n, 0, seed)
+    fd = bumps.bump_greeks(many[:, 0] / n, h)
+    assert abs(adjoint[0] - fd[0]) < 5e-3, (adjoint[0], fd[0])
+    # and the oracle's bumps of the same sets
+    ofd = bumps.bump_greeks(np.array([oracle.replay_sums(flat, n, 0, seed, inputs=s, adjoints=False)[0] / n
+                                      for s in sets]), h)
+    assert np.allclose(fd, ofd, rtol=0.0, atol=1e-9)
+
+
+@pytest.mark.gpu
+def test_fp32_engine_against_the_fp64_oracle_and_stable(nt):
+    """Fp32BackendComparisonTest.compareFp32EnginesAndReportStability: one
+    dispatch of 10^6 scenarios in fp32, seed 0xA51A17, against the fp64
+    oracle at 4x10^6: price within 3e-3 + 3e-3 |x|, delta and vega within
+    1e-2 + 1e-2 |x|; 60 settled repeats drift less than 1e-4 (here: not at
+    all, the reductions are deterministic); 25 dispatches over shifted offsets
+    all finite."""
+    paths, oracle_paths, seed = 1_000_000, 4_000_000, 0xA51A17
+    tape = nt.AadRecorder.record(price_space_asian)
+    flat = tape.flat()
+    want = oracle.to_result(oracle.replay_sums(flat, oracle_paths, 0, seed), oracle_paths)
+    fp32 = _fp32(nt)
+    print(f"case 50-fixing Asian fp32 on rocm, {paths} scenarios per dispatch, seed {seed:#x}", flush=True)
+    exe = nt.AadEngines.require("rocm", fp32).compile(tape, fp32)
+    baseline = exe.replay(paths, 0, seed)
+    for i in range(60):
+        r = exe.replay(paths, 0, seed)
+        assert r.rawSums() == baseline.rawSums(), i
+    for i in range(25):
+        r = exe.replay(paths, i * paths, seed)
+        assert np.all(np.isfinite(r.rawSums())), i
+    exe.close()
+    price, (delta, vega) = baseline.value(), baseline.gradients()
+    assert abs(price - want["price"]) <= 3e-3 + 3e-3 * abs(want["price"])
+    assert abs(delta - want["gradient"][0]) <= 1e-2 + 1e-2 * abs(want["gradient"][0])
+    assert abs(vega - want["gradient"][1]) <= 1e-2 + 1e-2 * abs(want["gradient"][1])
+    # this engine's fp32 bar: the fp64 oracle over the same scenarios, to 1e-5
+    same = oracle.to_result(oracle.replay_sums(flat, paths, 0, seed), paths)
+    assert abs(price - same["price"]) <= 1e-5 * abs(same["price"])
+    assert rel_err(np.asarray(baseline.gradients()), same["gradient"], floor=1e-300) <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("precision,bar", [("fp32", 2e-6), ("fp64", 2e-12)])
+def test_checkpointed_straight_line_matches_plain(nt, rocm, precision, bar):
+    """OpenClAsianParityTest.checkpointedFp32MatchesPlain (and
+    CudaCheckpointParityTest's fp64 bar of 2e-12): the 50-fixing Asian swept
+    in reverse through a checkpointed straight line of 48- and 96-node
+    segments against the plain kernel, 20,000 scenarios at offset
+    0x100000003, spot 100 and then 101, within bar x max(1, |x|)."""
+    flat = nt.AadRecorder.record(price_space_asian).flat()
+    x0 = list(flat["recorded_inputs"])
+    print(f"case 50-fixing Asian {precision} checkpointed vs plain", flush=True)
+    with rocm.Executable(flat, rocm.options(precision)) as plain:
+        for seg in (48, 96):
+            with rocm.Executable(flat, rocm.options(precision, mode=1, roll=-1, seg_len=seg)) as ck:
+                info = ck.info()
+                assert info["mode"] == 1 and info["loop_period"] == 0 and info["n_segments"] > 1
+                for spot in (100.0, 101.0):
+                    plain.set_inputs([spot, *x0[1:]])
+                    ck.set_inputs([spot, *x0[1:]])
+                    a, _ = plain.replay(20_000, OFFSET, 0xA51A17)
+                    b, _ = ck.replay(20_000, OFFSET, 0xA51A17)
+                    for i in [0, *range(2, len(a))]:
+                        assert np.isfinite(a[i]) and np.isfinite(b[i])
+                        assert abs(a[i] / 20_000 - b[i] / 20_000) <= bar * max(1.0, abs(a[i] / 20_000)), (seg, spot, i)
+
+
+@pytest.mark.gpu
+def test_fp64_matches_the_oracle_and_repeats_bit_identically(nt):
+    """OpenClAsianParityTest.openClMatchesCpuJitAndIsStable: 200,000
+    scenarios of the 50-fixing Asian in fp64, 40 repeats bit-identical to the
+    first, and the price and Greeks against the oracle (the reference's
+    5e-4 / 5e-3; here 1e-10)."""
+    n, seed = 200_000, 0xA51A17
+    tape = nt.AadRecorder.record(price_space_asian)
+    fp64 = _fp64(nt)
+    print(f"case 50-fixing Asian fp64 on rocm, {n} scenarios, 40 repeats", flush=True)
+    exe = nt.AadEngines.require("rocm", fp64).compile(tape, fp64)
+    first = exe.replay(n, 0, seed)
+    for i in range(40):
+        assert exe.replay(n, 0, seed).rawSums() == first.rawSums(), i
+    exe.close()
+    want = oracle.to_result(oracle.replay_sums(tape.flat(), n, 0, seed), n)
+    assert abs(first.value() - want["price"]) <= 5e-4 + 5e-4 * abs(want["price"])
+    assert abs(first.value() - want["price"]) <= 1e-10 * abs(want["price"])
+    assert rel_err(np.asarray(first.gradients()), want["gradient"], floor=1e-300) <= 1e-10
+    assert 0.0 < first.value() < 100.0
