@@ -13,7 +13,10 @@ oracle:
 * OpenClAsianParityTest (OpenClAsianParityTest.java:75-181): the same tape
   swept in reverse through a checkpointed straight line (segments of 48 and 96
   nodes) against the plain kernel at offset 0x100000003, spot 100 and 101,
-  and 40 repeats bit-identical.
+  and 40 repeats bit-identical;
+* RandomStreamsTest (RandomStreamsTest.java:42-137): uniforms' mean and range,
+  the jump-clock tape on a named stream, independent streams and a plain
+  single-stream tape, price only, 400,000 scenarios, seed 0xC0FFEE.
 """
 from __future__ import annotations
 
@@ -231,3 +234,96 @@ def test_fp64_matches_the_oracle_and_repeats_bit_identically(nt):
     assert abs(first.value() - want["price"]) <= 1e-10 * abs(want["price"])
     assert rel_err(np.asarray(first.gradients()), want["gradient"], floor=1e-300) <= 1e-10
     assert 0.0 < first.value() < 100.0
+
+
+STREAM_N, STREAM_SEED = 400_000, 0xC0FFEE
+
+
+def _mean_on_rocm(nt, body):
+    """RandomStreamsTest.meanOnEngine (RandomStreamsTest.java:44-49) on the
+    rocm engine: the price-only mean over 400,000 scenarios, seed 0xC0FFEE;
+    and the oracle's mean over the same scenarios."""
+    tape = nt.AadRecorder.record(body)
+    opts = _fp64(nt).withAdjoints(False)
+    exe = nt.AadEngines.require("rocm", opts).compile(tape, opts)
+    got = exe.replay(STREAM_N, 0, STREAM_SEED).value()
+    exe.close()
+    want = oracle.replay_sums(tape.flat(), STREAM_N, 0, STREAM_SEED, adjoints=False)[0] / STREAM_N
+    return got, want
+
+
+@pytest.mark.gpu
+def test_uniform_draw_has_the_right_mean_and_range(nt):
+    def mean(rec):
+        rec.input("x", 0.0)
+        rec.output(rec.randu())
+
+    def fourth(rec):
+        rec.input("x", 0.0)
+        u = rec.randu()
+        rec.output(u.mul(u).mul(u).mul(u))
+
+    print("case uniform moments on rocm", flush=True)
+    got, want = _mean_on_rocm(nt, mean)
+    assert abs(got - 0.5) <= 5e-3 and abs(got - want) <= 1e-12 * abs(want)
+    got, want = _mean_on_rocm(nt, fourth)
+    assert abs(got - 0.2) <= 5e-3 and abs(got - want) <= 1e-12 * abs(want)
+
+
+@pytest.mark.gpu
+def test_uniforms_and_named_streams_match_the_oracle(nt):
+    """cpuAndJitAgreeBitForBitOnUniformsAndNamedStreams: the jump-clock tape
+    (a normal on the default stream and a uniform on a named stream per step),
+    here against the oracle's mean to 1e-12 (the device's transcendentals
+    differ from glibc's in the last place, so not bit for bit)."""
+    from conftest import jump_clock_tape
+
+    body_tape = jump_clock_tape(nt, 16)
+    flat = body_tape.flat()
+    opts = _fp64(nt).withAdjoints(False)
+    print("case jump-clock tape, price only, on rocm", flush=True)
+    exe = nt.AadEngines.require("rocm", opts).compile(body_tape, opts)
+    got = exe.replay(STREAM_N, 0, STREAM_SEED).value()
+    exe.close()
+    want = oracle.replay_sums(flat, STREAM_N, 0, STREAM_SEED, adjoints=False)[0] / STREAM_N
+    assert abs(got - want) <= 1e-12 * abs(want)
+
+
+@pytest.mark.gpu
+def test_named_streams_are_independent(nt):
+    def cross(rec):
+        rec.input("x", 0.0)
+        rec.output(rec.stream("a").randn().mul(rec.stream("b").randn()))
+
+    print("case named-stream independence on rocm", flush=True)
+    got, want = _mean_on_rocm(nt, cross)
+    assert abs(got) <= 5e-3 and abs(got - want) <= 1e-12
+
+
+@pytest.mark.gpu
+def test_a_uniform_and_named_stream_tape_runs_on_rocm(nt):
+    """aBackendWithoutNativeSupportDeclinesSoSelectionFallsBack: the rocm
+    engine has native uniforms and named streams, so it takes the tape (the
+    reference's device engines decline it) and prices it finitely."""
+    def body(rec):
+        rec.input("x", 0.0)
+        rec.output(rec.randu().add(rec.stream("k").randn()))
+
+    print("case randu + named stream tape on rocm", flush=True)
+    got, want = _mean_on_rocm(nt, body)
+    assert math.isfinite(got) and abs(got - want) <= 1e-12 * max(1.0, abs(want))
+
+
+@pytest.mark.gpu
+def test_single_stream_normal_tape_is_unaffected(nt):
+    def body(rec):
+        s0 = rec.input("S0", 100.0)
+        vol = rec.input("sigma", 0.2)
+        s = s0
+        for _ in range(32):
+            s = s.mul(vol.mul(rec.randn()).mul(0.03).add(1.0))
+        rec.output(s)
+
+    print("case single-stream normal tape on rocm", flush=True)
+    got, want = _mean_on_rocm(nt, body)
+    assert got != 0.0 and abs(got - want) <= 1e-12 * abs(want)
