@@ -16,7 +16,18 @@ oracle:
   and 40 repeats bit-identical;
 * RandomStreamsTest (RandomStreamsTest.java:42-137): uniforms' mean and range,
   the jump-clock tape on a named stream, independent streams and a plain
-  single-stream tape, price only, 400,000 scenarios, seed 0xC0FFEE.
+  single-stream tape, price only, 400,000 scenarios, seed 0xC0FFEE;
+* MvpPricingTest (MvpPricingTest.java:33-100): the European against
+  Black-Scholes, the Asian's adjoint delta against a bump of 1.0, four
+  products against the oracle;
+* ModelsTest.heston (ModelsTest.java:60-86): adjoint price = price-only price,
+  delta against a bump, the v0 sensitivity's sign;
+* TimeGridTest (TimeGridTest.java:66-92): a uniform grid bit-identical to
+  steps(64), an explicit equal-gap grid, a front-loaded grid's European
+  against Black-Scholes;
+* ExoticsTest (ExoticsTest.java:57-107): knock-out + knock-in = vanilla,
+  width refinement, the barrier's adjoint delta against a bump, the cash
+  digital against e^{-rT} N(d2).
 """
 from __future__ import annotations
 
@@ -327,3 +338,215 @@ def test_single_stream_normal_tape_is_unaffected(nt):
     print("case single-stream normal tape on rocm", flush=True)
     got, want = _mean_on_rocm(nt, body)
     assert got != 0.0 and abs(got - want) <= 1e-12 * abs(want)
+
+
+# MvpPricingTest (MvpPricingTest.java:33-115), ModelsTest.heston
+# (ModelsTest.java:60-86, Phase1Support.java) and TimeGridTest
+# (TimeGridTest.java:34-92) on the rocm engine.
+MVP_N, MVP_SEED, MVP_STEPS = 400_000, 20260830, 64
+
+
+def _black_scholes_call(s, k, vol, r, t):
+    """Black-Scholes call price, delta, vega, rho and dV/dK."""
+    n = lambda x: 0.5 * math.erfc(-x / math.sqrt(2.0))  # noqa: E731
+    pdf = lambda x: math.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)  # noqa: E731
+    d1 = (math.log(s / k) + (r + 0.5 * vol * vol) * t) / (vol * math.sqrt(t))
+    d2 = d1 - vol * math.sqrt(t)
+    disc = math.exp(-r * t)
+    return {"price": s * n(d1) - k * disc * n(d2), "delta": n(d1), "vega": s * pdf(d1) * math.sqrt(t),
+            "rho": k * t * disc * n(d2), "strike": -disc * n(d2)}
+
+
+def _mc(nt, product, steps=None, grid=None, greeks=True):
+    b = nt.MonteCarlo.of(product).market(nt.EquityMarket.atmOneYear())
+    b = b.timeGrid(grid) if grid is not None else b.steps(steps)
+    b = b.greeks() if greeks else b.priceOnly()
+    return b.fp64().on("rocm").build()
+
+
+@pytest.mark.gpu
+def test_european_call_adjoint_greeks_match_black_scholes(nt):
+    print("case European vs Black-Scholes on rocm", flush=True)
+    mc = _mc(nt, nt.Products.europeanCall(), steps=1)
+    v = mc.run(MVP_N, MVP_SEED)
+    flat = mc.tape().flat()
+    mc.close()
+    m = nt.EquityMarket.atmOneYear()
+    ref = _black_scholes_call(m.spot(), m.strike(), m.vol(), m.rate(), m.maturity())
+    assert abs(v.price() - ref["price"]) <= 0.15
+    assert abs(v.greek("spot") - ref["delta"]) <= 0.02
+    assert abs(v.greek("vol") - ref["vega"]) <= 0.60
+    assert abs(v.greek("rate") - ref["rho"]) <= 0.60
+    assert abs(v.greek("strike") - ref["strike"]) <= 0.02
+    want = oracle.to_result(oracle.replay_sums(flat, MVP_N, 0, MVP_SEED), MVP_N)
+    assert abs(v.price() - want["price"]) <= 1e-10 * abs(want["price"])
+
+
+@pytest.mark.gpu
+def test_adjoint_greeks_match_central_bump_for_asian(nt):
+    print("case Asian 64 adjoint delta vs central bump h = 1 on rocm", flush=True)
+    greeks = _mc(nt, nt.Products.asianCall(), steps=MVP_STEPS)
+    price = _mc(nt, nt.Products.asianCall(), steps=MVP_STEPS, greeks=False)
+    m = nt.EquityMarket.atmOneYear()
+    adjoint = greeks.run(MVP_N, MVP_SEED)
+    h = 0.01 * m.spot()
+    up = price.run(m.withSpot(m.spot() + h), MVP_N, MVP_SEED).price()
+    dn = price.run(m.withSpot(m.spot() - h), MVP_N, MVP_SEED).price()
+    greeks.close()
+    price.close()
+    assert abs((up - dn) / (2 * h) - adjoint.greek("spot")) <= 5e-3
+    assert adjoint.price() > 0.0
+
+
+@pytest.mark.gpu
+def test_kernel_reproduces_scalar_oracle(nt):
+    """bytecodeKernelReproducesScalarOracle: the European, Asian and both
+    lookbacks at 64 steps within 1e-6 (1 + |x|) of the oracle on price, delta
+    and vega (here 1e-10 on the price and every Greek)."""
+    for product in (nt.Products.europeanCall(), nt.Products.asianCall(), nt.Products.lookbackCall(),
+                    nt.Products.lookbackPut()):
+        print(f"case {product} at 64 steps on rocm vs oracle", flush=True)
+        mc = _mc(nt, product, steps=MVP_STEPS)
+        v = mc.run(MVP_N, MVP_SEED)
+        flat = mc.tape().flat()
+        mc.close()
+        want = oracle.to_result(oracle.replay_sums(flat, MVP_N, 0, MVP_SEED), MVP_N)
+        names = list(flat["input_names"])
+        for got, ref in ((v.price(), want["price"]), (v.greek("spot"), want["gradient"][names.index("spot")]),
+                         (v.greek("vol"), want["gradient"][names.index("vol")])):
+            assert abs(got - ref) <= 1e-6 * (1 + abs(ref))
+        assert abs(v.price() - want["price"]) <= 1e-10 * abs(want["price"])
+        assert rel_err(np.asarray(v.gradients()), want["gradient"], floor=1e-300) <= 1e-10
+
+
+@pytest.mark.gpu
+def test_heston_adjoint_against_price_only_and_bump(nt):
+    """ModelsTest.heston: a European call under Heston, 48 steps, 200,000
+    scenarios, seed 20260830 (Phase1Support.java): the adjoint run's price
+    equals a price-only run's to 1e-9 (1 + price), the spot delta is within
+    2e-2 (1 + fd) of a central bump of 1.0 with common random numbers, every
+    sensitivity is finite, dPrice/dv0 > 0 and a higher v0 prices higher."""
+    n, seed = 200_000, 20260830
+    params = dict(spot=100, strike=100, rate=0.02, v0=0.04, kappa=1.5, theta=0.04, xi=0.5, rho=-0.7)
+    val = nt.HestonModel.european(nt.OptionTypeEnum.CALL, 1.0, 48)
+
+    def price_at(**kw):
+        market = nt.HestonMarket.create(**{**params, **kw})
+        pricer = nt.modelHeston(market, val).fp64().priceOnly().on("rocm").build()
+        p = pricer.run(market, n, seed).price()
+        pricer.close()
+        return p
+
+    print("case Heston European 48 steps on rocm", flush=True)
+    market = nt.HestonMarket.create(**params)
+    pricer = nt.modelHeston(market, val).fp64().greeks().on("rocm").build()
+    v = pricer.run(market, n, seed)
+    pricer.close()
+    assert abs(price_at() - v.price()) <= 1e-9 * (1 + v.price())
+    assert v.price() > 0.0
+    fd = (price_at(spot=101.0) - price_at(spot=99.0)) / 2.0
+    assert abs(fd - v.greek("spot")) <= 2e-2 * (1 + fd)
+    assert np.all(np.isfinite(v.gradients()))
+    assert v.greek("v0") > 0.0
+    assert price_at(v0=0.06) > price_at(v0=0.03)
+
+
+@pytest.mark.gpu
+def test_uniform_time_grid_equals_steps_bit_for_bit(nt):
+    """TimeGridTest.uniformTimeGridEqualsStepsIntArithmeticBitForBit (400,000
+    scenarios, seed 77): the same kernel, so the same sums to the bit."""
+    print("case uniform TimeGrid vs steps(64) on rocm", flush=True)
+    a = _mc(nt, nt.Products.asianCall(), steps=64)
+    b = _mc(nt, nt.Products.asianCall(), grid=nt.TimeGrid.uniform(64))
+    ra, rb = a.run(400_000, 77), b.run(400_000, 77)
+    a.close()
+    b.close()
+    assert ra.rawSums() == rb.rawSums()
+
+
+@pytest.mark.gpu
+def test_equal_gap_explicit_grid_matches_uniform(nt):
+    print("case explicit equal-gap grid vs steps(8) on rocm", flush=True)
+    a = _mc(nt, nt.Products.asianCall(), steps=8, greeks=False)
+    b = _mc(nt, nt.Products.asianCall(), grid=nt.TimeGrid.of([(i + 1) / 8 for i in range(8)]), greeks=False)
+    pa, pb = a.run(400_000, 77).price(), b.run(400_000, 77).price()
+    a.close()
+    b.close()
+    assert abs(pa - pb) <= 1e-9
+
+
+@pytest.mark.gpu
+def test_non_uniform_grid_prices_a_european_against_black_scholes(nt):
+    print("case front-loaded grid European vs Black-Scholes on rocm", flush=True)
+    grid = nt.TimeGrid.of([0.1, 0.15, 0.25, 0.45, 0.7, 1.0])
+    assert not grid.isUniform()
+    mc = _mc(nt, nt.Products.europeanCall(), grid=grid)
+    v = mc.run(1_000_000, 77)
+    flat = mc.tape().flat()
+    mc.close()
+    m = nt.EquityMarket.atmOneYear()
+    ref = _black_scholes_call(m.spot(), m.strike(), m.vol(), m.rate(), m.maturity())
+    assert abs(v.price() - ref["price"]) <= 0.15 and abs(v.greek("spot") - ref["delta"]) <= 0.02
+    want = oracle.to_result(oracle.replay_sums(flat, 1_000_000, 0, 77), 1_000_000)
+    assert abs(v.price() - want["price"]) <= 1e-10 * abs(want["price"])
+
+
+# ExoticsTest (ExoticsTest.java:30-107) on the rocm engine, fp64: 64 steps,
+# 200,000 scenarios, seed 12345.
+EX_N, EX_SEED, EX_STEPS = 200_000, 12345, 64
+
+
+def _ex_price(nt, product, steps=EX_STEPS, n=EX_N):
+    mc = _mc(nt, product, steps=steps, greeks=False)
+    p = mc.run(n, EX_SEED).price()
+    mc.close()
+    return p
+
+
+def _barrier(nt, kind, level, width):
+    return nt.ExoticProducts.barrier(nt.OptionTypeEnum.CALL, getattr(nt.ExoticProducts.BarrierEnum, kind), level, width)
+
+
+@pytest.mark.gpu
+def test_knock_out_plus_knock_in_equals_vanilla(nt):
+    print("case up-and-out + up-and-in = vanilla on rocm", flush=True)
+    out = _ex_price(nt, _barrier(nt, "UP_OUT", 130.0, 1.0))
+    inn = _ex_price(nt, _barrier(nt, "UP_IN", 130.0, 1.0))
+    vanilla = _ex_price(nt, nt.Products.europeanCall())
+    assert abs(vanilla - (out + inn)) <= 1e-9 * (1 + vanilla)
+    assert 0.0 < out < vanilla
+
+
+@pytest.mark.gpu
+def test_barrier_converges_as_smoothing_width_shrinks(nt):
+    print("case up-and-out width refinement on rocm", flush=True)
+    vanilla = _ex_price(nt, nt.Products.europeanCall())
+    p = [_ex_price(nt, _barrier(nt, "UP_OUT", 120.0, w)) for w in (4.0, 2.0, 1.0, 0.5, 0.25)]
+    assert all(-1e-9 <= x <= vanilla + 1e-9 for x in p), p
+    assert abs(p[-1] - p[-2]) < abs(p[1] - p[0]), p
+
+
+@pytest.mark.gpu
+def test_barrier_adjoint_delta_matches_a_bump_of_the_smoothed_payoff(nt):
+    print("case up-and-out 125 adjoint delta vs central bump h = 0.5 on rocm", flush=True)
+    product = _barrier(nt, "UP_OUT", 125.0, 1.5)
+    greeks = _mc(nt, product, steps=EX_STEPS)
+    adj = greeks.run(EX_N, EX_SEED).greek("spot")
+    greeks.close()
+    price = _mc(nt, product, steps=EX_STEPS, greeks=False)
+    m = nt.EquityMarket.atmOneYear()
+    up = price.run(m.withSpot(m.spot() + 0.5), EX_N, EX_SEED).price()
+    dn = price.run(m.withSpot(m.spot() - 0.5), EX_N, EX_SEED).price()
+    price.close()
+    fd = (up - dn) / 1.0
+    assert abs(fd - adj) <= 5e-3 + 5e-3 * abs(fd), (adj, fd)
+
+
+@pytest.mark.gpu
+def test_cash_digital_matches_black_scholes(nt):
+    print("case cash digital vs e^-rT N(d2) on rocm", flush=True)
+    got = _ex_price(nt, nt.ExoticProducts.digitalCash(nt.OptionTypeEnum.CALL, 1.0, 0.5), steps=1, n=1_000_000)
+    m = nt.EquityMarket.atmOneYear()
+    d2 = (math.log(m.spot() / m.strike()) + (m.rate() - 0.5 * m.vol() ** 2) * m.maturity()) / (m.vol() * math.sqrt(m.maturity()))
+    ref = math.exp(-m.rate() * m.maturity()) * 0.5 * math.erfc(-d2 / math.sqrt(2.0))
+    assert abs(got - ref) <= 0.03, (got, ref)
