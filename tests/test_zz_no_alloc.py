@@ -87,8 +87,10 @@ def noalloc(rocm, hip, x, inputs, paths, offset, seed, stream=None):
 # (workload, precision, derivative mode, loop rolling, path counts of three consecutive
 # calls). The reverse sweep (mode 1) keeps its tape per lane in device memory (288 bytes
 # rolled, 272 bytes as a checkpointed straight line with roll -1), so its dispatches stay
-# within the lanes whose tape fits the static array.
+# within the lanes whose tape fits the static array. 2,000,000 and 1,000,000 paths launch
+# more blocks than the device holds (16 and 8 per CU).
 CASES = [("C2", "fp64", 0, 1, (200_001, 4_097, 65_536)), ("C3", "fp32", 0, 1, (200_001, 4_097, 65_536)),
+         ("C2", "fp64", 0, 1, (2_000_000, 4_097, 1_000_000)),
          ("C2", "fp64", 1, 1, (20_001, 4_097, 16_384)), ("C2", "fp64", 1, -1, (20_001, 4_097, 16_384))]
 
 
