@@ -417,13 +417,13 @@ namespace ntr {
 // resident, 9.33 ms on 8 resident grids).
 // Whole blocks per CU matter as much as the count: a grid of q CUs' worth
 // plus r blocks leaves r CUs one block longer than the rest. Measured on one
-// MI355X (three interleaved runs per grid, spread below 0.5 %), kernel time
+// MI355X (bench.py --max-blocks, two runs per grid, kernel HIP-event means),
 // at the resident grid, at 16 blocks per CU (4,096) and at 4,112 blocks:
-// Asian fp64 2M 0.894 / 0.838 / 0.869 ms, Asian fp32 2M 0.298 / 0.291 /
-// 0.300 ms; weekday Asian fp64 2M 1.087 ms resident, 1.011 ms at 4,096
-// blocks, 1.041 ms at 4,224; worst-of fp32 10^6 2.701 ms resident, 2.544 ms at 8 blocks per CU,
-// 3.343 ms at 576 blocks. Barrier fp64 20M 14.25 / 12.80 ms at 40 blocks per
-// CU; Heston-Asian 10M 25.08 / 23.88 ms at 24.
+// Asian fp64 2M 0.894 / 0.839 / 0.866 ms; Asian fp32 2M 0.299 ms resident,
+// 0.292 ms at 4,096, 0.314 ms at 2,176; weekday Asian fp64 2M 1.093 /
+// 1.012 ms, 1.043 ms at 4,224; worst-of fp32 10^6 2.694 ms resident, 2.525 ms
+// at 8 blocks per CU, 3.339 ms at 576 blocks; barrier fp64 20M 14.40 / 13.10
+// ms at 40 blocks per CU; Heston-Asian 10M 25.56 / 24.48 ms at 24.
 constexpr double kShortPath = 1000;
 constexpr uint64_t kLanePaths = 4;
 constexpr uint64_t kLongLanePaths = 2;
