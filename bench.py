@@ -513,7 +513,7 @@ def main() -> int:
     ap.add_argument("--seg", type=int, default=0, help="loop iterations per checkpoint segment (0 auto)")
     ap.add_argument("--mode", type=int, default=0, help="derivative mode (0 cost model, 1 reverse sweep, 2 tangent)")
     ap.add_argument("--max-blocks", type=int, default=0,
-                    help="cap on the replay grid in blocks (0: one resident wave of blocks)")
+                    help="cap on the replay grid in blocks (0: the engine's own, whole blocks per CU, up to 8 resident grids)")
     ap.add_argument("--basis", type=int, default=0, choices=(0, 1, 2),
                     help="with --workload/--precision: tangent loops over 1 the inputs, 2 the loop's parameters "
                          "(0: the engine's choice)")

@@ -86,7 +86,8 @@ typedef struct nt_options {
   int32_t adjoints;         /* 1: value + every first-order Greek; 0: price only (lowered in the tangent frame with
                                no tangents unless mode is NT_MODE_REVERSE, so nt_exec_replay_many shares draws) */
   int32_t block;            /* threads per block; 0 = 256 */
-  int32_t max_blocks;       /* grid cap; 0 = sized from occupancy */
+  int32_t max_blocks;       /* grid cap; 0 = the engine's launch geometry (whole blocks per CU from occupancy,
+                               up to 8 resident grids for a long path; nt_exec_grid reports it) */
   int32_t checkpoint;       /* NT_CKPT_* */
   int32_t seg_len;          /* loop iterations per checkpoint segment; 0 = cost model. For a tape with no rolled
                                loop swept in reverse: nodes per checkpointed segment (0: about sqrt(nodes), at
