@@ -32,6 +32,13 @@ class Hip:
         self.L.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
         self.L.hipStreamSynchronize.argtypes = [C.c_void_p]
         self.L.hipStreamDestroy.argtypes = [C.c_void_p]
+        self.L.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+        self.L.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.L.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.L.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        self.L.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.L.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.L.hipGraphDestroy.argtypes = [C.c_void_p]
 
     def ok(self, rc):
         assert rc == 0, f"HIP error {rc}"
@@ -150,6 +157,55 @@ def test_noalloc_with_exception_lanes(rocm, hip, nt, tapes, mode, counts):
         want, _ = x.replay(65_536, OFFSET, 42)
         got = noalloc(rocm, hip, x, t["recorded_inputs"], 65_536, OFFSET, 42)
     assert np.array_equal(got, want), got - want
+
+
+@pytest.mark.parametrize("name,mode,paths", [("C2", 2, 200_001), ("C2", 2, 2_000_000), ("C3", 2, 100_000),
+                                             ("C2", 1, 20_001), ("merton32", 2, 50_001)])
+def test_noalloc_replays_from_a_captured_graph(rocm, hip, nt, tapes, name, mode, paths):
+    """The entry point enqueues its kernels and nothing else (no allocation,
+    copy, memset or wait), so a caller can capture it into a HIP graph: four
+    launches of the instantiated graph, with eager replays and
+    synchronisations between them, each give nt_exec_replay's sums for the
+    same paths, offset and seed, bit for bit; also with a reverse sweep's
+    device-memory tape and with lanes left to the exception kernel (the Merton
+    tape), whose count and bitmap each launch leaves at zero."""
+    L = hip.L
+    if name == "merton32":
+        from conftest import merton_call_tape
+        t = merton_call_tape(nt, MERTON, steps=32).flat()
+    else:
+        t = tapes[name]
+    print(f"case {name} mode={mode} paths={paths} noalloc captured into a graph", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
+        want, _ = x.replay(paths, OFFSET, 42)
+        n_sums = x.n_outputs * (2 + x.n_inputs)
+        d_in = hip.to_device(t["recorded_inputs"])
+        d_sums = hip.malloc(8 * n_sums)
+        stream, graph, gexec = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        hip.ok(L.hipStreamCreate(C.byref(stream)))
+        try:
+            hip.ok(L.hipStreamBeginCapture(stream, 2))  # hipStreamCaptureModeRelaxed
+            rc = rocm.lib().nt_exec_replay_noalloc(x._h, d_in, paths, OFFSET, 42, d_sums, n_sums, stream)
+            end = L.hipStreamEndCapture(stream, C.byref(graph))
+            assert rc == 0, rocm.lib().nt_last_error().decode()
+            assert end == 0, f"hipStreamEndCapture returned {end}"
+            hip.ok(L.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0))
+            for i in range(4):
+                hip.ok(L.hipMemset(d_sums, 0, 8 * n_sums))  # eager, outside the graph
+                hip.ok(L.hipGraphLaunch(gexec, stream))
+                hip.ok(L.hipStreamSynchronize(stream))
+                got = hip.to_host(d_sums, n_sums)
+                print(f"  launch {i}: sum={got[0]!r}", flush=True)
+                assert np.array_equal(got, want), (i, got - want)
+                x.replay(4_097, 0, 7)  # eager work on the executable's own stream
+        finally:
+            if gexec:
+                L.hipGraphExecDestroy(gexec)
+            if graph:
+                L.hipGraphDestroy(graph)
+            L.hipStreamDestroy(stream)
+            L.hipFree(d_in)
+            L.hipFree(d_sums)
 
 
 def test_noalloc_refuses_oversized_scratch(rocm, hip, tapes):
