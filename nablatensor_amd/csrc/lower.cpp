@@ -1067,8 +1067,12 @@ class Emitter {
         return "nt_log_fast(" + x + ", nt_slow" + ms(exp_active_) + ")";
       case NT_OP_SQRT: return f32_ ? "nt_hw_sqrtf(" + x + ")" : "sqrt(" + x + ")";
       case NT_OP_ABS: return f("fabs") + "(" + x + ")";
-      case NT_OP_MAX: return f("fmax") + "(" + x + ", " + y + ")";
-      case NT_OP_MIN: return f("fmin") + "(" + x + ", " + y + ")";
+      case NT_OP_MAX:
+      case NT_OP_MIN: {
+        const char* name = op == NT_OP_MAX ? "nt_max" : "nt_min";
+        if (!max_fast(op) || slow_) return f(name) + "(" + x + ", " + y + ")";
+        return std::string(name) + "_fast(" + x + ", " + y + ")";
+      }
       default: return "0";
     }
   }
@@ -1407,12 +1411,24 @@ class Emitter {
   // ---- kernel frame ----
   bool slow_ = false;  // emitting the device-libm re-evaluation of a flagged path
   bool exp_fallback() const {
-    if (f32_ || p_.libm == 1) return false;
+    if (f32_) return false;
     for (int i = 0; i < t_.n; ++i) {
+      if (max_fast(t_.op[i])) return true;
+      if (p_.libm == 1) continue;
       if (t_.op[i] == NT_OP_EXP || t_.op[i] == NT_OP_LOG ||
           ((t_.op[i] == NT_OP_SQRT || t_.op[i] == NT_OP_DIV) && fast_sqrt())) {
         return true;
       }
+    }
+    return false;
+  }
+  // fp64 MAX and MIN: v_max_f64 / v_min_f64 in the fast pass, a non-finite
+  // operand making the value NaN (nt_max_fast), so the path's sums are not
+  // finite and the exception kernel evaluates it again with nt_max / nt_min.
+  bool max_fast(int op) const { return !f32_ && (op == NT_OP_MAX || op == NT_OP_MIN); }
+  bool minmax_fallback() const {
+    for (int i = 0; i < t_.n; ++i) {
+      if (max_fast(t_.op[i])) return true;
     }
     return false;
   }
@@ -3312,7 +3328,7 @@ void Emitter::kernel(bool slow) {
     for (int m = 0; m < M; ++m) {
       const std::string bad = "nt_lane_bad" + std::to_string(m);
       const int c0 = m * p_.n_channels, c1 = c0 + p_.n_channels;
-      if (nonfinite_fallback()) {
+      if (nonfinite_fallback() || minmax_fallback()) {
         o_ << "  for (int c = " << c0 << "; c < " << c1 << "; ++c) " << bad << " |= !__builtin_isfinite(acc[c]);\n";
       }
       o_ << "  if (" << bad << ") {\n    for (int c = " << c0 << "; c < " << c1 << "; ++c) acc[c] = 0.0;\n  }\n";

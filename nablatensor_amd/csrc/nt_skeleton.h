@@ -56,6 +56,24 @@ __device__ __forceinline__ double nt_rcp(double x) { return __builtin_amdgcn_rcp
 __device__ __forceinline__ bool nt_zero_or_pos_normal(double x) { return __builtin_amdgcn_class(x, 0x160); }
 // x is a positive normal number (finite, not subnormal): one v_cmp_class_f64
 __device__ __forceinline__ bool nt_pos_normal(double x) { return __builtin_amdgcn_class(x, 0x100); }
+// MAX and MIN nodes as java.lang.Math.max/min evaluate them in the reference's
+// scalar engine: NaN when either operand is NaN, and -0 below +0 (IEEE
+// 754-2019 maximum/minimum). C's fmax/fmin would return the other operand for
+// a NaN and hide a path that the reference prices as NaN. fp64: v_max_f64 and
+// a NaN select; fp32: one v_maximum3_f32 / v_minimum3_f32.
+__device__ __forceinline__ double nt_max(double a, double b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ double nt_min(double a, double b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float nt_maxf(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float nt_minf(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+// The fp64 fast pass: v_max_f64 / v_min_f64 (which order -0 below +0), times
+// a factor that is exactly 1 for finite operands and NaN when either is NaN
+// or infinite. A NaN there makes the path's sums non-finite, and the path is
+// evaluated again by the exception kernel with nt_max / nt_min, which give
+// Math.max/min's value for an infinite operand too. Costs two VALU
+// instructions and no register beyond its operands, where the NaN select of
+// nt_max costs the 16-asset worst-of its second wave.
+__device__ __forceinline__ double nt_max_fast(double a, double b) { return fmax(a, b) * fma(a + b, 0.0, 1.0); }
+__device__ __forceinline__ double nt_min_fast(double a, double b) { return fmin(a, b) * fma(a + b, 0.0, 1.0); }
 // fp32 hardware transcendentals (quarter-rate VALU): exp2, log2, sqrt, and
 // sin/cos of 2 pi x (the instructions take their argument in revolutions).
 __device__ __forceinline__ float nt_hw_exp2f(float x) { return __builtin_amdgcn_exp2f(x); }

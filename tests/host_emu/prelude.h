@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <limits>
 
 #define NT_HOST_EMU 1
 #define __global__
@@ -32,6 +33,27 @@ inline T nt_opaque(T x) { return x; }
 template <typename T>
 inline T nt_opaque_u(T x) { return x; }
 inline bool nt_pos_normal(double x) { return std::fpclassify(x) == FP_NORMAL && !std::signbit(x); }
+// java.lang.Math.max/min: NaN if either operand is NaN, -0 below +0
+template <typename T>
+inline T nt_jmax(T a, T b) {
+  if (std::isnan(a) || std::isnan(b)) return std::numeric_limits<T>::quiet_NaN();
+  if (a == b) return std::signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+template <typename T>
+inline T nt_jmin(T a, T b) {
+  if (std::isnan(a) || std::isnan(b)) return std::numeric_limits<T>::quiet_NaN();
+  if (a == b) return std::signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+inline double nt_max(double a, double b) { return nt_jmax(a, b); }
+inline double nt_min(double a, double b) { return nt_jmin(a, b); }
+inline float nt_maxf(float a, float b) { return nt_jmax(a, b); }
+inline float nt_minf(float a, float b) { return nt_jmin(a, b); }
+// the device's fast pass: v_max_f64 / v_min_f64 (-0 below +0) times a factor
+// that is 1 for finite operands and NaN for a NaN or infinite one
+inline double nt_max_fast(double a, double b) { return nt_jmax(a, b) * std::fma(a + b, 0.0, 1.0); }
+inline double nt_min_fast(double a, double b) { return nt_jmin(a, b) * std::fma(a + b, 0.0, 1.0); }
 inline bool nt_zero_or_pos_normal(double x) {
   const int c = std::fpclassify(x);
   return c == FP_ZERO || (c == FP_NORMAL && !std::signbit(x));

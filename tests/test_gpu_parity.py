@@ -366,6 +366,30 @@ def test_sqrt_routine_and_fallback_on_device(rocm, nt, s_val, floor):
     assert np.array_equal(np.isnan(v), np.isnan(ov))
 
 
+@pytest.mark.parametrize("mode", [2, 1])
+def test_non_finite_inputs_give_non_finite_sums_and_leave_the_executable_usable(rocm, tapes, mode):
+    """A NaN spot or an infinite volatility sends every lane to the exception
+    kernel, whose device-libm replay returns the non-finite sums the oracle
+    returns (NaN where it has NaN); the executable then replays finite inputs
+    exactly as before."""
+    t = tapes["C2"]
+    x0 = list(t["recorded_inputs"])
+    paths = 20_000
+    print(f"case C2 mode={mode} non-finite inputs", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
+        before, _ = x.replay(paths, OFFSET, 42)
+        for bad in ([float("nan"), *x0[1:]], [*x0[:2], float("inf"), *x0[3:]]):
+            x.set_inputs(bad)
+            got, _ = x.replay(paths, OFFSET, 42)
+            want = oracle.replay_sums(t, paths, OFFSET, 42, inputs=bad)
+            assert not np.all(np.isfinite(got)), got
+            assert np.array_equal(np.isnan(got), np.isnan(want)), (got, want)
+            assert np.array_equal(np.isposinf(got), np.isposinf(want)) and np.array_equal(np.isneginf(got), np.isneginf(want))
+        x.set_inputs(x0)
+        after, _ = x.replay(paths, OFFSET, 42)
+    assert np.array_equal(before, after)
+
+
 @pytest.mark.parametrize("basis", [1, 2])
 @pytest.mark.parametrize("name,paths", [("C2", 2048), ("C3", 1024), ("C4", 512), ("C5", 256)])
 def test_loop_tangents_over_inputs_and_parameters_on_device(rocm, tapes, name, paths, basis):
