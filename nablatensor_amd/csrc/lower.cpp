@@ -1048,7 +1048,9 @@ class Emitter {
     return false;
   }
 
-  std::string expr(int op, const std::string& x, const std::string& y, double c, int a) const {
+  // `node`: the tape node (its first iteration, in a step loop), which tells
+  // whether an operand of MAX or MIN is a literal.
+  std::string expr(int op, const std::string& x, const std::string& y, double c, int a, int node = -1) const {
     switch (op) {
       case NT_OP_CONST: return lit(c);
       case NT_OP_INPUT: return "in" + std::to_string(a) + ms(true) + in_sfx_;
@@ -1071,6 +1073,10 @@ class Emitter {
       case NT_OP_MIN: {
         const char* name = op == NT_OP_MAX ? "nt_max" : "nt_min";
         if (!max_fast(op) || slow_) return f(name) + "(" + x + ", " + y + ")";
+        const bool a_lit = node >= 0 && t_.op[t_.a[node]] == NT_OP_CONST;
+        const bool b_lit = node >= 0 && t_.op[t_.b[node]] == NT_OP_CONST;
+        if (b_lit && !a_lit) return std::string(name) + "_lit(" + x + ", " + y + ")";
+        if (a_lit && !b_lit) return std::string(name) + "_lit(" + y + ", " + x + ")";
         return std::string(name) + "_fast(" + x + ", " + y + ")";
       }
       default: return "0";
@@ -1423,8 +1429,9 @@ class Emitter {
     return false;
   }
   // fp64 MAX and MIN: v_max_f64 / v_min_f64 in the fast pass, a non-finite
-  // operand making the value NaN (nt_max_fast), so the path's sums are not
-  // finite and the exception kernel evaluates it again with nt_max / nt_min.
+  // operand making the value NaN (nt_max_fast, nt_max_lit when one operand is
+  // a literal), so the path's sums are not finite and the exception kernel
+  // evaluates it again with nt_max / nt_min.
   bool max_fast(int op) const { return !f32_ && (op == NT_OP_MAX || op == NT_OP_MIN); }
   bool minmax_fallback() const {
     for (int i = 0; i < t_.n; ++i) {
@@ -1477,7 +1484,7 @@ class Emitter {
   std::string body_expr(int j, int u, int op, const std::string& x, const std::string& y) const {
     const int i = L_.start + j;
     if (op == NT_OP_CONST && L_.table_lit(j)) return "nt_lit" + std::to_string(j) + "[it0 + " + std::to_string(u) + "u]";
-    return expr(op, x, y, t_.c[i], t_.a[i]);
+    return expr(op, x, y, t_.c[i], t_.a[i], i);
   }
   bool recip_ = false;  // the DIV just emitted is a nt_recip
   void preamble();
@@ -2064,7 +2071,7 @@ void Emitter::tline(int lo, int hi) {
       exp_active_ = act;
       const std::string x = ar >= 1 ? vname(t_.a[i]) : "";
       const std::string y = ar >= 2 ? vname(t_.b[i]) : "";
-      std::string val = expr(op, x, y, t_.c[i], t_.a[i]);
+      std::string val = expr(op, x, y, t_.c[i], t_.a[i], i);
       sqrt_q_.clear();
       if (op == NT_OP_SQRT && fast_sqrt() && !slow_) {
         const std::string q = "t" + std::to_string(i) + "_q" + ms(true);

@@ -65,15 +65,20 @@ __device__ __forceinline__ double nt_max(double a, double b) { return __builtin_
 __device__ __forceinline__ double nt_min(double a, double b) { return __builtin_elementwise_minimum(a, b); }
 __device__ __forceinline__ float nt_maxf(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float nt_minf(float a, float b) { return __builtin_elementwise_minimum(a, b); }
-// The fp64 fast pass: v_max_f64 / v_min_f64 (which order -0 below +0), times
-// a factor that is exactly 1 for finite operands and NaN when either is NaN
-// or infinite. A NaN there makes the path's sums non-finite, and the path is
-// evaluated again by the exception kernel with nt_max / nt_min, which give
-// Math.max/min's value for an infinite operand too. Costs two VALU
-// instructions and no register beyond its operands, where the NaN select of
-// nt_max costs the 16-asset worst-of its second wave.
+// The fp64 fast pass: v_max_f64 / v_min_f64 (which order -0 below +0), made
+// NaN when an operand is NaN or infinite; such a NaN makes the path's sums
+// non-finite and the exception kernel evaluates the path again with nt_max /
+// nt_min, which also give Math.max/min's value for an infinite operand. Two
+// variable operands: times fma(a + b, 0, 1), exactly 1 for finite ones. One
+// literal operand c: plus a * 0, an exact +-0 for a finite a that leaves the
+// maximum as it is (-0 + -0 stays -0, +0 + -0 is +0 only where the maximum
+// is +0); MIN as -MAX(-a, -c), the negations free source modifiers. No
+// register beyond the operands, where nt_max's NaN select costs the reverse
+// sweep of the Asian its third wave.
 __device__ __forceinline__ double nt_max_fast(double a, double b) { return fmax(a, b) * fma(a + b, 0.0, 1.0); }
 __device__ __forceinline__ double nt_min_fast(double a, double b) { return fmin(a, b) * fma(a + b, 0.0, 1.0); }
+__device__ __forceinline__ double nt_max_lit(double a, double c) { return fma(a, 0.0, fmax(a, c)); }
+__device__ __forceinline__ double nt_min_lit(double a, double c) { return -nt_max_lit(-a, -c); }
 // fp32 hardware transcendentals (quarter-rate VALU): exp2, log2, sqrt, and
 // sin/cos of 2 pi x (the instructions take their argument in revolutions).
 __device__ __forceinline__ float nt_hw_exp2f(float x) { return __builtin_amdgcn_exp2f(x); }

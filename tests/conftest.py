@@ -465,3 +465,37 @@ def signed_basket_tape(nt, steps=40):
             c = c.mul(rc.mul(z2).exp())
         rec.output(a.add(b).add(c).sub(300.0).max(rec.constant(0.0)))
     return nt.AadRecorder.record(body).flat()
+
+
+MAX_MIN_OUTPUTS = 6
+
+
+def max_min_tape(nt, only=None):
+    """MAX and MIN of two inputs and of an input and a literal, each its own
+    output (or output `only` alone, for the reverse sweep, which follows one
+    output), for the edge cases of java.lang.Math.max/min (signed zeros, NaN,
+    infinities)."""
+    def body(rec):
+        x = rec.input("x", 1.0)
+        y = rec.input("y", 2.0)
+        outs = [("max", lambda: x.max(y)), ("min", lambda: x.min(y)), ("max0", lambda: x.max(0.0)),
+                ("min0", lambda: x.min(0.0)), ("maxm1", lambda: y.max(-1.0)),
+                ("minmax", lambda: x.max(y).min(y.mul(2.0)))]
+        for k, (name, f) in enumerate(outs):
+            if only is None or only == k:
+                rec.output(name, f())
+    return nt.AadRecorder.record(body)
+
+
+MAX_MIN_CASES = [(-0.0, 0.0), (0.0, -0.0), (-0.0, -0.0), (float("nan"), 1.0), (1.0, float("nan")),
+                 (float("inf"), 1.0), (float("-inf"), 1.0), (float("-inf"), float("-inf")),
+                 (float("inf"), float("-inf")), (2.0, 3.0), (-0.0, 5.0), (5.0, -0.0), (-3.0, -0.0)]
+
+
+def same_special(a, b):
+    """Equal as Math.max/min results: NaN where the other is NaN, otherwise
+    equal values with equal signs of zero."""
+    a, b = np.asarray(a), np.asarray(b)
+    return bool(np.array_equal(np.isnan(a), np.isnan(b)) and
+                np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)]) and
+                np.array_equal(np.signbit(a[~np.isnan(a)]), np.signbit(b[~np.isnan(b)])))

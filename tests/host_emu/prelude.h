@@ -50,10 +50,12 @@ inline double nt_max(double a, double b) { return nt_jmax(a, b); }
 inline double nt_min(double a, double b) { return nt_jmin(a, b); }
 inline float nt_maxf(float a, float b) { return nt_jmax(a, b); }
 inline float nt_minf(float a, float b) { return nt_jmin(a, b); }
-// the device's fast pass: v_max_f64 / v_min_f64 (-0 below +0) times a factor
-// that is 1 for finite operands and NaN for a NaN or infinite one
+// the device's fast pass: v_max_f64 / v_min_f64 (-0 below +0), NaN for a NaN
+// or infinite operand; with a literal operand, MIN as -MAX(-a, -c)
 inline double nt_max_fast(double a, double b) { return nt_jmax(a, b) * std::fma(a + b, 0.0, 1.0); }
 inline double nt_min_fast(double a, double b) { return nt_jmin(a, b) * std::fma(a + b, 0.0, 1.0); }
+inline double nt_max_lit(double a, double c) { return std::fma(a, 0.0, nt_jmax(a, c)); }
+inline double nt_min_lit(double a, double c) { return -nt_max_lit(-a, -c); }
 inline bool nt_zero_or_pos_normal(double x) {
   const int c = std::fpclassify(x);
   return c == FP_ZERO || (c == FP_NORMAL && !std::signbit(x));

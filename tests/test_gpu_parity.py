@@ -366,6 +366,23 @@ def test_sqrt_routine_and_fallback_on_device(rocm, nt, s_val, floor):
     assert np.array_equal(np.isnan(v), np.isnan(ov))
 
 
+@pytest.mark.parametrize("precision,mode", [("fp64", 2), ("fp64", 1), ("fp32", 2)])
+def test_max_min_follow_java_math_on_device(rocm, nt, precision, mode):
+    """MAX and MIN per path against the oracle's java.lang.Math.max/min on
+    signed zeros, NaN and infinities (two inputs, and an input and a literal):
+    the value with its sign of zero, NaN where the oracle has NaN."""
+    from conftest import MAX_MIN_CASES, MAX_MIN_OUTPUTS, max_min_tape, same_special
+    tapes_ = [max_min_tape(nt).flat()] if mode == 2 else [max_min_tape(nt, o).flat() for o in range(MAX_MIN_OUTPUTS)]
+    print(f"case MAX/MIN edge cases {precision} mode={mode}", flush=True)
+    for flat in tapes_:
+        with rocm.Executable(flat, rocm.options(precision, mode=mode)) as x:
+            for case in MAX_MIN_CASES:
+                x.set_inputs(list(case))
+                v, _ = x.replay_paths(64, 0, 42)
+                ov, _ = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), f32=precision == "fp32", output=None)
+                assert same_special(np.reshape(v, ov.shape), ov), (case, v[:1], ov[:1])
+
+
 @pytest.mark.parametrize("mode", [2, 1])
 def test_non_finite_inputs_give_non_finite_sums_and_leave_the_executable_usable(rocm, tapes, mode):
     """A NaN spot or an infinite volatility sends every lane to the exception

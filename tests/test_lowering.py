@@ -875,3 +875,24 @@ def test_local_vol_tape_both_modes_emulated(rocm, k):
     _, v, g = run_emulated(flat, opts, paths, rocm=rocm)
     assert_values_match(v, ov, rocm.lower(flat, opts))
     check_per_path(v, g, flat, paths, OFFSET, 42, min_strict=0.9)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_max_min_follow_java_math_emulated(nt, rocm, mode):
+    """The fp64 fast pass's MAX and MIN (v_max_f64 with a NaN-making term, the
+    exception kernel's exact rule behind it) per path against the oracle on
+    signed zeros, NaN and infinities: tangent mode on the six-output tape, the
+    reverse sweep on each output alone."""
+    from conftest import MAX_MIN_CASES, MAX_MIN_OUTPUTS, max_min_tape, same_special
+    tapes_ = [max_min_tape(nt).flat()] if mode == 2 else [max_min_tape(nt, o).flat() for o in range(MAX_MIN_OUTPUTS)]
+    for flat in tapes_:
+        opts = rocm.options("fp64", mode=mode)
+        src = rocm.lower(flat, opts)
+        assert ("nt_max_lit(" in src or "nt_min_lit(" in src or "nt_max_fast(" in src or "nt_min_fast(" in src)
+        assert "nt_replay_slow" in src
+        outputs = len(flat["output_node"])
+        k = emu.EmulatedKernel(src, len(flat["input_node"]), tape_slots(src))
+        for case in MAX_MIN_CASES:
+            _, v, _ = k.run(list(case), 64, 0, 42, grid=3, block=64, outputs=outputs)
+            ov, _ = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), threads=1, output=None)
+            assert same_special(np.reshape(v, ov.shape), ov), (case, v[:1], ov[:1])
