@@ -1651,7 +1651,6 @@ void Emitter::line_case_head() {
 }
 
 void Emitter::body_reverse_segmented() {
-  const int n = t_.n;
   const auto& B = p_.lbound;
   const auto& seg = p_.lseg;
   const int S = static_cast<int>(B.size()) - 1;
