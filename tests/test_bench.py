@@ -126,7 +126,7 @@ def test_markets_line(patched, monkeypatch, capsys):
 
 
 COUNTED = [("C2", "fp64", 0, 1), ("C2", "fp64", 1, 1), ("C2", "fp32", 0, 1), ("C2", "fp64", 1, -1),
-           *[(w, p, 0, 1) for w, p in bench.OTHER_WORKLOADS]]
+           *[(w, p, 0, 1) for w, p in bench.OTHER_WORKLOADS], ("local_vol", "fp64", 0, 1), ("local_vol", "fp64", 2, 1)]
 
 
 @pytest.mark.parametrize("workload,precision,mode,roll", COUNTED)
