@@ -499,3 +499,44 @@ def same_special(a, b):
     return bool(np.array_equal(np.isnan(a), np.isnan(b)) and
                 np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)]) and
                 np.array_equal(np.signbit(a[~np.isnan(a)]), np.signbit(b[~np.isnan(b)])))
+
+
+SPECIAL_OUTPUTS = 8
+
+
+def special_ops_tape(nt, only=None):
+    """EXP, LOG, SQRT, DIV (and 1 / x, the literal-numerator reciprocal), ABS,
+    NEG and MUL of inputs set to special values, each its own output (or
+    output `only` alone, for the reverse sweep)."""
+    def body(rec):
+        x = rec.input("x", 1.0)
+        y = rec.input("y", 2.0)
+        outs = [("exp", lambda: x.exp()), ("log", lambda: x.log()), ("sqrt", lambda: x.sqrt()),
+                ("div", lambda: x.div(y)), ("recip", lambda: rec.constant(1.0).div(x)), ("abs", lambda: x.abs()),
+                ("neg", lambda: x.neg()), ("mul", lambda: x.mul(y))]
+        for k, (name, f) in enumerate(outs):
+            if only is None or only == k:
+                rec.output(name, f())
+    return nt.AadRecorder.record(body)
+
+
+SPECIAL_CASES = [(-0.0, 1.0), (0.0, 1.0), (float("inf"), 1.0), (float("-inf"), 1.0), (float("nan"), 1.0),
+                 (5e-324, 1.0), (-2.0, 1.0), (710.0, 2.0), (-746.0, 0.5), (1e308, 1e-308), (0.0, 0.0),
+                 (1e-310, 3.0), (-1e-310, -3.0), (0.75, -0.0)]
+
+
+def close_special(a, b, rel):
+    """NaN where the other is NaN, the same infinities and signed zeros, and
+    finite non-zero values within `rel` relative."""
+    a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+    if not np.array_equal(np.isnan(a), np.isnan(b)):
+        return False
+    m = ~np.isnan(a)
+    a, b = a[m], b[m]
+    if not (np.array_equal(np.isinf(a), np.isinf(b)) and np.array_equal(a[np.isinf(a)], b[np.isinf(b)])):
+        return False
+    z = (a == 0) | (b == 0)
+    if not (np.array_equal(a[z], b[z]) and np.array_equal(np.signbit(a[z]), np.signbit(b[z]))):
+        return False
+    f = np.isfinite(a) & ~z
+    return bool(np.all(np.abs(a[f] - b[f]) <= rel * np.abs(b[f])))

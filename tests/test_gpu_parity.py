@@ -383,6 +383,24 @@ def test_max_min_follow_java_math_on_device(rocm, nt, precision, mode):
                 assert same_special(np.reshape(v, ov.shape), ov), (case, v[:1], ov[:1])
 
 
+@pytest.mark.parametrize("precision,mode,rel", [("fp64", 2, 5e-16), ("fp64", 1, 5e-16), ("fp32", 2, 4e-7)])
+def test_special_values_follow_the_oracle_on_device(rocm, nt, precision, mode, rel):
+    """EXP, LOG, SQRT, DIV, 1 / x, ABS, NEG and MUL at signed zeros,
+    subnormals, infinities, NaN and the exponential's overflow and underflow,
+    per path against the oracle (fp32: the fp32 oracle): the same NaNs,
+    infinities and signed zeros, finite values within `rel`."""
+    from conftest import SPECIAL_CASES, SPECIAL_OUTPUTS, close_special, special_ops_tape
+    tapes_ = [special_ops_tape(nt).flat()] if mode == 2 else [special_ops_tape(nt, o).flat() for o in range(SPECIAL_OUTPUTS)]
+    print(f"case special values {precision} mode={mode}", flush=True)
+    for flat in tapes_:
+        with rocm.Executable(flat, rocm.options(precision, mode=mode)) as x:
+            for case in SPECIAL_CASES:
+                x.set_inputs(list(case))
+                v, _ = x.replay_paths(64, 0, 42)
+                ov, _ = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), f32=precision == "fp32", output=None)
+                assert close_special(np.reshape(v, ov.shape), ov, rel), (case, flat["output_node"], v[:1], ov[:1])
+
+
 @pytest.mark.parametrize("mode", [2, 1])
 def test_non_finite_inputs_give_non_finite_sums_and_leave_the_executable_usable(rocm, tapes, mode):
     """A NaN spot or an infinite volatility sends every lane to the exception

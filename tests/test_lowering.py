@@ -896,3 +896,20 @@ def test_max_min_follow_java_math_emulated(nt, rocm, mode):
             _, v, _ = k.run(list(case), 64, 0, 42, grid=3, block=64, outputs=outputs)
             ov, _ = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), threads=1, output=None)
             assert same_special(np.reshape(v, ov.shape), ov), (case, v[:1], ov[:1])
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_special_values_follow_the_oracle_emulated(nt, rocm, mode):
+    """EXP, LOG, SQRT, DIV, 1 / x, ABS, NEG and MUL at signed zeros,
+    subnormals, infinities, NaN and the exponential's overflow and underflow,
+    per path against the oracle: the fast pass's own math flags what it does
+    not cover and the exception kernel evaluates it with libm."""
+    from conftest import SPECIAL_CASES, SPECIAL_OUTPUTS, close_special, special_ops_tape
+    tapes_ = [special_ops_tape(nt).flat()] if mode == 2 else [special_ops_tape(nt, o).flat() for o in range(SPECIAL_OUTPUTS)]
+    for flat in tapes_:
+        src = rocm.lower(flat, rocm.options("fp64", mode=mode))
+        k = emu.EmulatedKernel(src, len(flat["input_node"]), tape_slots(src))
+        for case in SPECIAL_CASES:
+            _, v, _ = k.run(list(case), 64, 0, 42, grid=3, block=64, outputs=len(flat["output_node"]))
+            ov, _ = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), threads=1, output=None)
+            assert close_special(np.reshape(v, ov.shape), ov, 4e-16), (case, flat["output_node"], v[:1], ov[:1])
