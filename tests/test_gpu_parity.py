@@ -396,9 +396,11 @@ def test_special_values_follow_the_oracle_on_device(rocm, nt, precision, mode, r
         with rocm.Executable(flat, rocm.options(precision, mode=mode)) as x:
             for case in SPECIAL_CASES:
                 x.set_inputs(list(case))
-                v, _ = x.replay_paths(64, 0, 42)
-                ov, _ = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), f32=precision == "fp32", output=None)
+                v, g = x.replay_paths(64, 0, 42)
+                ov, og = oracle.replay_paths(flat, 64, 0, 42, inputs=list(case), f32=precision == "fp32", output=None)
                 assert close_special(np.reshape(v, ov.shape), ov, rel), (case, flat["output_node"], v[:1], ov[:1])
+                if mode == 1:  # the reverse sweep's adjoints too
+                    assert close_special(np.reshape(g, og.shape), og, rel), (case, flat["output_node"], g[:1], og[:1])
 
 
 @pytest.mark.parametrize("mode", [2, 1])
