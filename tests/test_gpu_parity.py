@@ -283,6 +283,28 @@ def test_sums_do_not_depend_on_the_grid(rocm, tapes, mode):
     assert np.array_equal(va, vb) and np.array_equal(ga, gb)
 
 
+@pytest.mark.parametrize("name", ["C2", "C4"])
+def test_replay_many_with_a_non_finite_set(rocm, tapes, name):
+    """One input set of several with a NaN first input: its lanes go to the
+    exception kernel for that set alone, its sums have the oracle's NaN
+    pattern, and the other sets' sums equal separate replays bit for bit."""
+    t = tapes[name]
+    x0 = np.array(t["recorded_inputs"])
+    bad = x0.copy()
+    bad[0] = np.nan
+    sets = np.stack([x0, bad, x0 * 1.01])
+    paths = 20_000
+    print(f"case {name} replay_many with a NaN set", flush=True)
+    with rocm.Executable(t, rocm.options("fp64")) as x:
+        many, _ = x.replay_many(sets, paths, OFFSET, 42)
+        for m in (0, 2):
+            x.set_inputs(sets[m])
+            one, _ = x.replay(paths, OFFSET, 42)
+            assert np.array_equal(many[m], one), m
+    want = oracle.replay_sums(t, paths, OFFSET, 42, inputs=bad)
+    assert np.array_equal(np.isnan(many[1]), np.isnan(want)), (many[1], want)
+
+
 def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
     t = tapes["C2"]
     with rocm.Executable(t, rocm.options("fp64")) as x:
