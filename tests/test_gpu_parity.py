@@ -305,6 +305,23 @@ def test_replay_many_with_a_non_finite_set(rocm, tapes, name):
     assert np.array_equal(np.isnan(many[1]), np.isnan(want)), (many[1], want)
 
 
+@pytest.mark.parametrize("mode", [2, 1])
+def test_tiny_counts_and_an_offset_that_wraps(rocm, tapes, mode):
+    """Dispatches of 1 to 257 paths (one partly filled block, a partial wave)
+    and a range of paths whose 64-bit index wraps past 2^64 - 1: sums against
+    the oracle's over the same paths to 1e-10, per path within the bar."""
+    t = tapes["C2"]
+    print(f"case C2 mode={mode} tiny counts and a wrapping offset", flush=True)
+    with rocm.Executable(t, rocm.options("fp64", mode=mode)) as x:
+        for paths, offset in [(1, 0), (2, OFFSET), (63, 5), (64, 0), (65, OFFSET), (255, 1), (257, 77),
+                              (16, 2**64 - 7)]:
+            got, _ = x.replay(paths, offset, 42)
+            want = oracle.replay_sums(t, paths, offset, 42)
+            assert rel_err(got, want, floor=1e-300) <= 1e-10, (paths, offset)
+        v, g = x.replay_paths(16, 2**64 - 7, 42)
+    check_per_path(v, g, t, 16, 2**64 - 7, 42, min_strict=0.8, max_above=0.25)
+
+
 def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
     t = tapes["C2"]
     with rocm.Executable(t, rocm.options("fp64")) as x:
