@@ -322,6 +322,24 @@ def test_tiny_counts_and_an_offset_that_wraps(rocm, tapes, mode):
     check_per_path(v, g, t, 16, 2**64 - 7, 42, min_strict=0.8, max_above=0.25)
 
 
+@pytest.mark.parametrize("name,precision", [("C2", "fp64"), ("C3", "fp32")])
+def test_replay_many_beyond_one_kernel(rocm, tapes, name, precision):
+    """Thirteen input sets: more than one multi-market kernel holds at two
+    waves per SIMD, so the dispatch is split into kernels of a few sets each;
+    every set's sums still equal a separate replay bit for bit."""
+    t = tapes[name]
+    x0 = np.array(t["recorded_inputs"])
+    sets = np.stack([x0 * (1.0 + 0.004 * (m - 6)) for m in range(13)])
+    paths = 50_000
+    print(f"case {name} {precision} replay_many of 13 sets", flush=True)
+    with rocm.Executable(t, rocm.options(precision)) as x:
+        many, _ = x.replay_many(sets, paths, OFFSET, 42)
+        for m in range(len(sets)):
+            x.set_inputs(sets[m])
+            one, _ = x.replay(paths, OFFSET, 42)
+            assert np.array_equal(many[m], one), m
+
+
 def test_replay_many_of_one_set_and_bad_arguments(rocm, tapes):
     t = tapes["C2"]
     with rocm.Executable(t, rocm.options("fp64")) as x:
