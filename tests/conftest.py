@@ -278,6 +278,19 @@ def sqrt_classes_tape(nt, s_val, floor=True, steps=16):
     return nt.AadRecorder.record(body)
 
 
+def no_input_tape(nt, steps=16):
+    """A price with no inputs, so no Greeks: an Asian call on a GBM spot whose
+    start, volatility and strike are literals (the sums are Σy and Σy² alone)."""
+    def body(rec):
+        s = rec.randn().mul(0.05).exp().mul(100.0)
+        acc = s
+        for _ in range(steps - 1):
+            s = s.mul(rec.randn().mul(0.05).exp())
+            acc = acc.add(s)
+        rec.output(acc.mul(1.0 / steps).sub(100.0).max(0.0))
+    return nt.AadRecorder.record(body)
+
+
 def branching_tape(nt, steps=24):
     """The reference's random branching tape for its checkpoint parity test
     (CudaCheckpointParityTest.java:75-85): a level driven by two normals per

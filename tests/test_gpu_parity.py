@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import ABOVE, STRICT, check_per_path, reconcile, rel_err
+from conftest import ABOVE, STRICT, check_per_path, no_input_tape, reconcile, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -303,6 +303,25 @@ def test_replay_many_with_a_non_finite_set(rocm, tapes, name):
             assert np.array_equal(many[m], one), m
     want = oracle.replay_sums(t, paths, OFFSET, 42, inputs=bad)
     assert np.array_equal(np.isnan(many[1]), np.isnan(want)), (many[1], want)
+
+
+@pytest.mark.parametrize("precision,mode", [("fp64", 2), ("fp64", 1), ("fp32", 2)])
+def test_tape_with_no_inputs(rocm, nt, precision, mode):
+    """A price with no inputs: two sums (Σy, Σy²) and no derivative columns,
+    against the oracle (fp32 against the fp64 oracle at 1e-5)."""
+    flat = no_input_tape(nt).flat()
+    print(f"case no-input tape {precision} mode {mode}", flush=True)
+    with rocm.Executable(flat, rocm.options(precision, mode=mode)) as x:
+        x.set_inputs([])
+        sums, _ = x.replay(200_000, OFFSET, 42)
+        want = oracle.replay_sums(flat, 200_000, OFFSET, 42)
+        assert len(sums) == 2
+        assert rel_err(sums, want, floor=1e-300) <= (1e-10 if precision == "fp64" else 1e-5)
+        if precision == "fp64":
+            v, g = x.replay_paths(4096, OFFSET, 42)
+            ov, _ = oracle.replay_paths(flat, 4096, OFFSET, 42)
+            assert g.shape == (4096, 0)
+            assert rel_err(v, ov) <= 1e-12
 
 
 @pytest.mark.parametrize("mode", [2, 1])

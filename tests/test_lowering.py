@@ -20,7 +20,8 @@ import pytest
 
 import emu
 import oracle
-from conftest import ABOVE, STRICT, check_per_path, equity_tape, rel_err, scaled_exp_tape, sqrt_classes_tape, tape_slots
+from conftest import (ABOVE, STRICT, check_per_path, equity_tape, no_input_tape, rel_err, scaled_exp_tape,
+                      sqrt_classes_tape, tape_slots)
 
 OFFSET = 0x100000003
 
@@ -238,6 +239,25 @@ def test_price_only_and_moved_inputs(rocm, tapes):
     sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False, libm=1, mode=1), 200, inputs=x, rocm=rocm)
     assert np.array_equal(v, ov)
     assert np.all(sums[2:] == 0.0)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+def test_tape_with_no_inputs(rocm, nt, mode):
+    """A tape with no inputs lowers to a kernel with two channels (Σy, Σy²)
+    and no derivative columns: the oracle's values bit for bit with libm
+    draws, within 1e-12 with the skeleton's own math."""
+    flat = no_input_tape(nt).flat()
+    assert len(flat["input_node"]) == 0
+    ov, og = oracle.replay_paths(flat, 500, OFFSET, 42, threads=1)
+    ref = oracle.replay_sums(flat, 500, OFFSET, 42, threads=1)
+    assert og.shape == (500, 0) and len(ref) == 2
+    sums, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=mode), 500, rocm=rocm)
+    assert g.shape == (500, 0) and len(sums) == 2
+    assert np.array_equal(v, ov)
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-13
+    sums, v, _ = run_emulated(flat, rocm.options("fp64", mode=mode), 500, rocm=rocm)
+    assert rel_err(v, ov) <= 1e-12
+    assert rel_err(sums, ref, floor=1e-300) <= 1e-12
 
 
 @pytest.mark.parametrize("mode", [1, 2])
