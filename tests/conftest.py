@@ -291,6 +291,30 @@ def no_input_tape(nt, steps=16):
     return nt.AadRecorder.record(body)
 
 
+def degenerate_tapes(nt):
+    """Tapes at the edges of the format: no draws at all, an output that is an
+    input node, an output with a zero derivative, and an output that is a
+    draw (no active path to the inputs)."""
+    def no_draws(rec):
+        x, y = rec.input("x", 1.5), rec.input("y", 2.0)
+        rec.output(x.mul(y).add(x.exp()))
+
+    def input_out(rec):
+        x, _ = rec.input("x", 1.5), rec.input("y", 2.0)
+        rec.output(x)
+
+    def const_out(rec):
+        x = rec.input("x", 1.5)
+        rec.output(x.mul(0.0).add(3.0))
+
+    def draw_out(rec):
+        rec.input("x", 1.5)
+        rec.output(rec.randn())
+    return {name: nt.AadRecorder.record(body).flat()
+            for name, body in [("no_draws", no_draws), ("input_out", input_out), ("const_out", const_out),
+                               ("draw_out", draw_out)]}
+
+
 def branching_tape(nt, steps=24):
     """The reference's random branching tape for its checkpoint parity test
     (CudaCheckpointParityTest.java:75-85): a level driven by two normals per

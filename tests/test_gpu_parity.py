@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import ABOVE, STRICT, check_per_path, no_input_tape, reconcile, rel_err
+from conftest import ABOVE, STRICT, check_per_path, degenerate_tapes, no_input_tape, reconcile, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -303,6 +303,20 @@ def test_replay_many_with_a_non_finite_set(rocm, tapes, name):
             assert np.array_equal(many[m], one), m
     want = oracle.replay_sums(t, paths, OFFSET, 42, inputs=bad)
     assert np.array_equal(np.isnan(many[1]), np.isnan(want)), (many[1], want)
+
+
+@pytest.mark.parametrize("mode", [2, 1])
+def test_degenerate_tapes(rocm, nt, mode):
+    """No draws, an output that is an input, a zero derivative, an output that
+    is a draw: per path and summed against the oracle."""
+    for name, flat in degenerate_tapes(nt).items():
+        print(f"case degenerate tape {name} mode {mode}", flush=True)
+        with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+            sums, _ = x.replay(100_000, OFFSET, 42)
+            assert rel_err(sums, oracle.replay_sums(flat, 100_000, OFFSET, 42), floor=1e-300) <= 1e-10, name
+            v, g = x.replay_paths(1000, OFFSET, 42)
+            ov, og = oracle.replay_paths(flat, 1000, OFFSET, 42)
+            assert rel_err(v, ov) <= 1e-12 and rel_err(g, og) <= 1e-12, name
 
 
 @pytest.mark.parametrize("precision,mode", [("fp64", 2), ("fp64", 1), ("fp32", 2)])

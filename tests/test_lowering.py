@@ -20,7 +20,7 @@ import pytest
 
 import emu
 import oracle
-from conftest import (ABOVE, STRICT, check_per_path, equity_tape, no_input_tape, rel_err, scaled_exp_tape,
+from conftest import (ABOVE, STRICT, check_per_path, degenerate_tapes, equity_tape, no_input_tape, rel_err, scaled_exp_tape,
                       sqrt_classes_tape, tape_slots)
 
 OFFSET = 0x100000003
@@ -239,6 +239,18 @@ def test_price_only_and_moved_inputs(rocm, tapes):
     sums, v, _ = run_emulated(flat, rocm.options("fp64", adjoints=False, libm=1, mode=1), 200, inputs=x, rocm=rocm)
     assert np.array_equal(v, ov)
     assert np.all(sums[2:] == 0.0)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("name", ["no_draws", "input_out", "const_out", "draw_out"])
+def test_degenerate_tapes(rocm, nt, name, mode):
+    """No draws, an output that is an input, a zero derivative, an output that
+    is a draw: the oracle's values and derivatives bit for bit."""
+    flat = degenerate_tapes(nt)[name]
+    sums, v, g = run_emulated(flat, rocm.options("fp64", libm=1, mode=mode), 150, rocm=rocm)
+    ov, og = oracle.replay_paths(flat, 150, OFFSET, 42, threads=1)
+    assert np.array_equal(v, ov) and np.array_equal(g, og)
+    assert rel_err(sums, oracle.replay_sums(flat, 150, OFFSET, 42, threads=1), floor=1e-300) <= 1e-13
 
 
 @pytest.mark.parametrize("mode", [1, 2])
