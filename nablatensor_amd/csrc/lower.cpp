@@ -2939,7 +2939,7 @@ void Emitter::preamble() {
 // returns at once when the count is zero (the finishing pass then skips its
 // rows); otherwise each lane takes its bit (clearing the bitmap behind it),
 // visits its paths only if the bit is set, and a block with no such lane loads
-// no tables and writes a zero row of partials.
+// no tables and writes zero partials.
 void Emitter::kernel_head(bool slow) {
   const int nin = t_.n_in;
   const int M = p_.markets;
@@ -3275,8 +3275,8 @@ void Emitter::dump_rows(int m) {
 // its range, or the value or a derivative came out non-finite) is left out of
 // its sums and flagged in the bitmap. The exception kernel evaluates the
 // flagged paths again, one market at a time, with device libm and the
-// oracle's zero-adjoint rule, into a second set of partial rows. Kept apart,
-// the rare pass costs the replay kernel no registers.
+// oracle's zero-adjoint rule, into the second half of each channel's column
+// of partials. Kept apart, the rare pass costs the replay kernel no registers.
 void Emitter::kernel(bool slow) {
   const int nin = t_.n_in;
   const int M = p_.markets;

@@ -107,13 +107,18 @@ size_t flags_bytes_for(uint64_t lanes, int markets);
 // created, so that entry point itself never has to.
 int noalloc_prepare(int dev);
 
-// Partial rows a dispatch over `grid` blocks may write: the replay kernel's
-// and, when there is an exception kernel, as many again.
-int partial_rows(int grid, bool has_slow);
+// Length of each channel's column of partials in a dispatch over `grid`
+// blocks (the skeleton's nt_partial_column): the replay kernel's region of
+// 8 ceil(grid / 8) slots, then the exception kernel's. A dispatch of `nch`
+// channels needs nch such columns, channel-major.
+int partial_rows(int grid);
+
+// Offset of the exception kernel's region within each column.
+int partial_slow_offset(int grid);
 
 // Launches the replay kernel `fn` over `grid` blocks on `stream` and, when
-// `fn_slow` is set, the exception kernel after it, whose partial rows follow
-// the replay kernel's (rows grid .. 2 grid - 1 of `nch` doubles each).
+// `fn_slow` is set, the exception kernel after it, which writes the second
+// region of every channel's column (partial_slow_offset).
 // `between`, when set, is recorded after the replay kernel (it times that kernel alone).
 int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFunction_t fn_slow, const double* d_inputs,
                      double* d_partials, int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset,

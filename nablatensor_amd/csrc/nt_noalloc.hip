@@ -18,14 +18,14 @@
 // one device (on different streams, or from different threads) race on it.
 // The array is laid out as the flags (a count of the lanes that left paths to
 // the exception kernel, then their bitmap, one bit per lane of the grid) in a
-// region of their own of kFlagBytes at the start, then the partial rows and a
+// region of their own of kFlagBytes at the start, then the partials and a
 // reverse sweep's tape. The flags must be zero before a dispatch and every
 // dispatch leaves them zero (the finishing pass resets the count, the
 // exception kernel the bitmap words it read), so their region is never used
-// for anything else: one dispatch's rows can never be read as another's
+// for anything else: one dispatch's partials can never be read as another's
 // flags. noalloc_prepare clears it once per device when the first executable
-// on that device is created. Every block writes its own rows of partials, and
-// the finishing pass reads only the rows written.
+// on that device is created. Every block writes its own entry of each
+// channel's partials, and the finishing pass reads only the entries written.
 //
 // Compiled by hipcc (the array is device code); the rest of libnt_rocm.so is
 // host C++ built with g++.
@@ -97,7 +97,7 @@ extern "C" int nt_exec_replay_noalloc(nt_exec* x, const double* d_inputs, uint64
     return ntr::fail(NT_E_INVALID, "the dispatch's grid has more lanes than the allocation-free entry point's "
                                    "flags cover (2^22)");
   }
-  const int rows = ntr::partial_rows(grid, x->fn_slow != nullptr);
+  const int rows = ntr::partial_rows(grid);
   const size_t partial_bytes = round_up_256(sizeof(double) * static_cast<size_t>(rows) * static_cast<size_t>(nch));
   const size_t flag_bytes = kFlagBytes;
   const size_t tape_bytes = ntr::tape_bytes_per_lane(x) * static_cast<size_t>(lanes);

@@ -470,7 +470,9 @@ size_t flags_bytes_for(uint64_t lanes, int markets) {
   return (1 + static_cast<size_t>((lanes + 63) / 64) * static_cast<size_t>(std::max(1, markets))) * sizeof(uint64_t);
 }
 
-int partial_rows(int grid, bool has_slow) { return has_slow ? 2 * grid : grid; }
+int partial_rows(int grid) { return 16 * ((grid + 7) / 8); }
+
+int partial_slow_offset(int grid) { return 8 * ((grid + 7) / 8); }
 
 int launch_kernel_on(nt_exec* x, hipStream_t stream, hipFunction_t fn, hipFunction_t fn_slow, const double* d_inputs,
                      double* d_partials, int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset,
@@ -490,7 +492,7 @@ int launch_slow_on(nt_exec* x, hipStream_t stream, hipFunction_t fn_slow, const 
                    int nch, void* d_tape, uint64_t* d_flags, uint64_t paths, uint64_t offset, uint64_t seed,
                    double* out_v, double* out_g, int grid) {
   const int block = x->low.plan.block;
-  double* slow_rows = d_partials + static_cast<size_t>(grid) * static_cast<size_t>(nch);
+  double* slow_rows = d_partials + partial_slow_offset(grid);  // the exception kernel's region of each column
   void* sargs[] = {&d_inputs, &paths, &offset, &seed, &slow_rows, &d_tape, &out_v, &out_g, &d_flags};
   NT_HIP(hipModuleLaunchKernel(fn_slow, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(block), 1, 1, 0,
                                stream, sargs, nullptr),
@@ -605,7 +607,7 @@ int nt_exec_create(const nt_tape* tape, const nt_options* options, nt_exec** out
   const int nch = x->low.plan.n_channels;
   NT_HIP(hipMalloc(&x->d_inputs, sizeof(double) * std::max(1, x->low.ir.n_in)), "hipMalloc(inputs)");
   NT_HIP(hipMalloc(&x->d_partials,
-                   sizeof(double) * static_cast<size_t>(ntr::partial_rows(x->grid_cap, x->fn_slow != nullptr)) * nch),
+                   sizeof(double) * static_cast<size_t>(ntr::partial_rows(x->grid_cap)) * nch),
          "hipMalloc(partials)");
   NT_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_sums), sizeof(double) * nch, hipHostMallocDefault),
          "hipHostMalloc(sums)");
@@ -684,7 +686,7 @@ static int launch_replay(nt_exec* x, hipFunction_t fn, hipFunction_t fn_slow, ui
                        out_v, out_g, grid, between);
 }
 
-// Finishing pass over the partial rows of one dispatch on `grid` blocks: `nch`
+// Finishing pass over the partials of one dispatch on `grid` blocks: `nch`
 // sums written to host memory `out` (pinned, read after the stream drains).
 static int launch_finish(nt_exec* x, hipFunction_t fn, hipFunction_t fn_slow, double* d_partials, int grid, int nch,
                          double* out) {
@@ -771,7 +773,7 @@ static int market_variant(nt_exec* x, int markets, MarketVariant*& out) {
   if (e == hipSuccess) v.fn_slow = optional_function(v.mod, "nt_replay_slow");
   if (e == hipSuccess) e = hipMalloc(&v.d_inputs, sizeof(double) * std::max<size_t>(1, static_cast<size_t>(nin) * markets));
   if (e == hipSuccess) {
-    const size_t rows = static_cast<size_t>(ntr::partial_rows(x->grid_cap, v.fn_slow != nullptr));
+    const size_t rows = static_cast<size_t>(ntr::partial_rows(x->grid_cap));
     e = hipMalloc(&v.d_partials, sizeof(double) * rows * nch);
   }
   if (e != hipSuccess) {

@@ -10,8 +10,8 @@
 //     cosine leg for even k, sine leg for odd k. One block feeds both legs.
 //   * Box-Muller in fp64 (the reference formula) and fp32.
 //   * Deterministic reductions: wave64 butterfly, then LDS across the waves of
-//     a block, one row of per-block partials; a second kernel sums the rows in
-//     block order.
+//     a block, one per-block partial per channel (channel-major columns); a
+//     second kernel sums each column in block order.
 #pragma once
 
 #if !defined(__HIPCC_RTC__) && !defined(NT_HOST_EMU)
@@ -442,8 +442,24 @@ __device__ __forceinline__ bool nt_take_lane_flag(nt_u64* __restrict__ flags, nt
   return ((w >> (tid & 63)) & 1) != 0;
 }
 
-// Reduce NCH per-lane accumulators over the block and write one row of
-// partials[blockIdx.x * NCH + c]. `lds` holds NCH * (blockDim.x / 64) doubles.
+// Partials are channel-major, one column per channel, so the finishing pass
+// reads a channel with contiguous loads (64 entries per wave load); from a
+// row-major [block][channel] layout every wave load touched 64 cache lines,
+// and the pass, one block, was bound by its CU's address unit (40 us for 35
+// channels of 2,048 blocks). Within a column the entries are grouped by
+// b mod 8, the XCD the dispatcher deals block b to: block b sits at
+// nt_partial_slot(b, grid) = (b mod 8) G8 + b / 8, G8 = ceil(grid / 8), so
+// the entries of a 32-byte write granule come from one XCD's L2 (in block
+// order, four XCDs would each write back a part of every granule). A column
+// holds nt_partial_column(grid) = 16 G8 entries: the replay kernel's 8 G8
+// slots, then the exception kernel's (it runs on the same grid, with
+// `partials` advanced by 8 G8). The host allocates nch columns of that length.
+__device__ __forceinline__ nt_u32 nt_group8(nt_u32 grid) { return (grid + 7u) >> 3; }
+__device__ __forceinline__ nt_u64 nt_partial_column(nt_u32 grid) { return 16ull * nt_group8(grid); }
+__device__ __forceinline__ nt_u32 nt_partial_slot(nt_u32 b, nt_u32 grid) { return (b & 7u) * nt_group8(grid) + (b >> 3); }
+
+// Reduce NCH per-lane accumulators over the block and write the block's entry
+// of each channel's column. `lds` holds NCH * (blockDim.x / 64) doubles.
 template <int NCH>
 __device__ __forceinline__ void nt_block_store(const double (&acc)[NCH], double* __restrict__ partials,
                                                double* lds) {
@@ -459,21 +475,27 @@ __device__ __forceinline__ void nt_block_store(const double (&acc)[NCH], double*
   for (int c = threadIdx.x; c < NCH; c += blockDim.x) {
     double s = 0.0;
     for (int w = 0; w < waves; ++w) s += lds[c * waves + w];
-    partials[static_cast<nt_u64>(blockIdx.x) * NCH + c] = s;
+    partials[static_cast<nt_u64>(c) * nt_partial_column(gridDim.x) + nt_partial_slot(blockIdx.x, gridDim.x)] = s;
   }
 }
 
-// Second pass: out[c] = sum over blocks b of partials[b * nch + c], launched as
-// one block of 64 * min(nch, 16) threads. Wave w takes channels w, w + waves,
-// ...; lane l adds blocks l, l + 64, ... in order and the wave adds its 64 lane
-// sums by the fixed butterfly, with no block barrier. The order depends only on
-// the block count, so a channel's result is bitwise the same whatever nch is (a
-// market's sums do not change with the markets priced beside it) and run to
-// run. `out` is host memory the caller reads after the stream has drained.
-// The rows of an exception kernel (slow_blocks of them, after the replay
-// kernel's) are added only when `count`, the number of lanes that left paths
-// to it, is nonzero (an exception kernel that found it zero wrote no rows);
-// the pass then sets `count` back to zero for the next dispatch.
+// Second pass: out[c] = sum over blocks of channel c's entries, launched as
+// one block of 64 * min(nch, 16) threads; `blocks` is the dispatch's grid.
+// Wave w takes channels w, w + waves, ...; its lanes walk the column's slots
+// in a fixed order (region, then batches of 64 kBatch slots per class of
+// b mod 8, the eight classes side by side, each lane adding its slots in
+// order) and the wave adds its 64 lane sums by the fixed butterfly, with no
+// block barrier. All 8 kBatch loads of a batch are issued before its first
+// add, so a lane waits about one memory round trip per batch. The order
+// depends only on the grid, so a channel's result is bitwise the same whatever
+// nch is (a market's sums do not change with the markets priced beside it)
+// and run to run. `out` is host memory the caller reads after the stream has
+// drained.
+// The exception kernel's entries (its region of each column; `slow_blocks`
+// is the grid when there is such a kernel, else 0) are added only when
+// `count`, the number of lanes that left paths to it, is nonzero (an
+// exception kernel that found it zero wrote nothing); the pass then sets
+// `count` back to zero for the next dispatch.
 // With `deferred` set (host memory), the exception kernel has not run yet:
 // the pass writes whether it is needed (count nonzero) there and, if it is,
 // returns at once, changing nothing; the caller then runs the exception
@@ -489,13 +511,37 @@ extern "C" __global__ __launch_bounds__(1024) void nt_finish(const double* __res
     if (threadIdx.x == 0) deferred[0] = flagged ? 1u : 0u;
     if (flagged) return;
   }
-  if (count && count[0] != 0) blocks += slow_blocks;
+  const nt_u32 g8 = nt_group8(blocks);
+  const nt_u64 column = nt_partial_column(blocks);
+  const nt_u32 regions = (slow_blocks != 0 && count && count[0] != 0) ? 2u : 1u;
+  // slots of class x hold the blocks x, x + 8, ...: n[x] of them
+  nt_u32 n[8];
+#pragma unroll
+  for (nt_u32 x = 0; x < 8; ++x) n[x] = blocks > x ? (blocks - x + 7u) >> 3 : 0u;
+  constexpr nt_u32 kBatch = 4;
   for (nt_u32 c = threadIdx.x >> 6; c < nch; c += waves) {
     double s = 0.0;
-    // unrolled so the loads of several rows are in flight at once; the adds
-    // keep their order
-#pragma unroll 8
-    for (nt_u32 b = lane; b < blocks; b += 64) s += partials[static_cast<nt_u64>(b) * nch + c];
+    for (nt_u32 region = 0; region < regions; ++region) {
+      const double* col = partials + c * column + static_cast<nt_u64>(region) * 8u * g8;
+      for (nt_u32 jb = 0; jb < g8; jb += 64 * kBatch) {
+        double v[8][kBatch];
+#pragma unroll
+        for (nt_u32 x = 0; x < 8; ++x) {
+#pragma unroll
+          for (nt_u32 k = 0; k < kBatch; ++k) {
+            const nt_u32 j = jb + lane + 64 * k;
+            v[x][k] = j < n[x] ? col[static_cast<nt_u64>(x) * g8 + j] : 0.0;
+          }
+        }
+#pragma unroll
+        for (nt_u32 x = 0; x < 8; ++x) {
+#pragma unroll
+          for (nt_u32 k = 0; k < kBatch; ++k) {
+            if (jb + lane + 64 * k < n[x]) s += v[x][k];
+          }
+        }
+      }
+    }
     s = nt_wave_sum(s);
     if (lane == 0) out[c] = s;
   }
