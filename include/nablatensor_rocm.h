@@ -214,8 +214,8 @@ int nt_exec_replay_paths(nt_exec *exec, uint64_t paths, uint64_t offset, uint64_
  * for the executable's own stream. The call enqueues the replay and finishing
  * kernels and returns; the caller synchronizes before reading d_sums. Sums are
  * bit-identical to nt_exec_replay's for the same inputs, paths, offset and
- * seed. The per-block partials (grid x channels doubles, twice that when the
- * tape has an exception kernel), the bitmap of lanes that left paths to the
+ * seed. The per-block partials (channels x 16 ceil(grid / 8) doubles: room
+ * for the replay and exception kernels' entries), the bitmap of lanes that left paths to the
  * exception kernel (one bit per lane of the grid, in a fixed 512 KiB region of
  * its own, for grids of up to 2^22 lanes) and a reverse sweep's per-lane tape, if the
  * executable keeps one in device memory, live in a static array of
