@@ -641,7 +641,7 @@ int nt_exec_set_inputs(nt_exec* x, const double* inputs, int32_t n) {
 using ntr::grid_for;
 
 // Grows the flags to a dispatch on `grid` blocks pricing `markets` sets: a
-// size set by the grid (at most the resident cap), not by the paths, so it
+// size set by the grid (at most the executable's grid cap), not by the paths, so it
 // grows at most a few times per executable. The stream is drained first (the
 // old flags may still be in use) and the new ones are zeroed whole: every
 // dispatch leaves the count and the bitmap at zero after that.
