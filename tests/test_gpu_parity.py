@@ -591,6 +591,29 @@ def test_merton_jump_tape_several_markets(rocm, nt):
     assert rel_err(one, ref, floor=1e-300) <= 1e-10
 
 
+@pytest.mark.parametrize("mode", [2, 1])
+def test_exception_kernel_on_grids_off_the_xcd_multiple(rocm, nt, mode):
+    """The Merton tape, whose lanes leave paths to the exception kernel, on
+    grids of 1, 3, 12 and 14 blocks, and capped at 13 blocks over 100,000
+    paths: each channel's column groups the blocks by block mod 8 and puts
+    the exception kernel's entries in a second region, and the sums stay the
+    oracle's on grids that are not a multiple of 8."""
+    from conftest import merton_call_tape
+    flat = merton_call_tape(nt, MERTON, steps=32).flat()
+    with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+        assert "nt_replay_slow" in x.source()
+        for paths, blocks in ((1, 1), (700, 3), (3000, 12), (3329, 14)):
+            print(f"case merton32 mode={mode} paths={paths}", flush=True)
+            assert x.grid(paths)[0] == blocks
+            got, _ = x.replay(paths, OFFSET, 42)
+            assert rel_err(got, oracle.replay_sums(flat, paths, OFFSET, 42)) <= 1e-10, paths
+    print(f"case merton32 mode={mode} paths=100000 max_blocks=13", flush=True)
+    with rocm.Executable(flat, rocm.options("fp64", mode=mode, max_blocks=13)) as x:
+        assert x.grid(100_000)[0] == 13
+        got, _ = x.replay(100_000, OFFSET, 42)
+        assert rel_err(got, oracle.replay_sums(flat, 100_000, OFFSET, 42)) <= 1e-10
+
+
 def test_merton_jump_tape_converges_to_the_poisson_series(rocm, nt):
     """JumpModelsTest.mertonMonteCarloConvergesToThePoissonSeries at its own
     size (1,500,000 scenarios, seed 42, 128 steps): the device sums agree with
