@@ -305,6 +305,23 @@ def test_replay_many_with_a_non_finite_set(rocm, tapes, name):
     assert np.array_equal(np.isnan(many[1]), np.isnan(want)), (many[1], want)
 
 
+def test_dispatch_timing_is_ordered(rocm, tapes):
+    """The three timing figures of a dispatch: the replay kernel (first two
+    events), all its kernels (first to last event) and the host's wall time,
+    in that order and positive; the same for a dispatch of several sets."""
+    t = tapes["C2"]
+    print("case timing C2 and C1", flush=True)
+    for name, paths in (("C2", 2_000_000), ("C1", 1_000_000)):
+        with rocm.Executable(tapes[name], rocm.options("fp64")) as x:
+            for _ in range(3):
+                _, tm = x.replay(paths, 0, 42)
+                assert 0.0 < tm["replay_ms"] <= tm["kernel_ms"] <= tm["wall_ms"], (name, tm)
+    with rocm.Executable(t, rocm.options("fp64")) as x:
+        x0 = np.array(t["recorded_inputs"])
+        _, tm = x.replay_many(np.stack([x0, x0 * 1.01]), 200_000, 0, 42)
+        assert 0.0 < tm["kernel_ms"] <= tm["wall_ms"], tm
+
+
 @pytest.mark.parametrize("mode", [2, 1])
 def test_degenerate_tapes(rocm, nt, mode):
     """No draws, an output that is an input, a zero derivative, an output that
