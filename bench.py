@@ -560,7 +560,7 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (scenarios shard by path "
-              "range with one reduction of raw sums per GPU, see DESIGN.md)", file=sys.stderr)
+              "range, each GPU returning its raw sums for one fixed-order reduction)", file=sys.stderr)
         return 2
 
     import nablatensor_amd as nt

@@ -2,7 +2,7 @@
  * CPU oracle for the fused forward+adjoint Monte-Carlo tape replay.
  *
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's
- * scalar `cpu` engine, used as the checker for the HIP engine. Only tests/,
+ * scalar `cpu` engine, against which the tests hold the HIP engine. Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
  * product path (nablatensor_amd) never links, imports or calls anything here.
  *

@@ -2,8 +2,8 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
 this module. It restates the reference's scalar `cpu` engine (see nt_oracle.h
-for the file:line each function follows) and is the checker for the HIP engine,
-never a fallback for it.
+for the file:line each function follows); the tests hold the HIP engine to it,
+and it is never a fallback for it.
 """
 from __future__ import annotations
 

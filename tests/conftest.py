@@ -1,7 +1,7 @@
 """Shared fixtures: the five workload tapes, recorded by the host layer.
 
 Tests marked `gpu` need an MI355X (gfx950) and the in-tree libnt_rocm.so;
-everything else runs on the CPU. The oracle (oracle/oracle.py) is the checker.
+everything else runs on the CPU. Results are held to the oracle (oracle/oracle.py).
 """
 from __future__ import annotations
 

@@ -1,5 +1,5 @@
-"""The host layer's chunked replay on the CPU (SURVEY's "tiny chunk budget"
-failure-path check), under AddressSanitizer and UndefinedBehaviorSanitizer.
+"""The host layer's chunked replay on the CPU (a failure-path check with a
+tiny chunk budget), under AddressSanitizer and UndefinedBehaviorSanitizer.
 
 tests/host_chunks/driver.cpp drives AadExecutable::calibrate / replaySafe
 (nablatensor_amd/host/engine.cpp) with a stand-in executable that sums a
