@@ -415,6 +415,27 @@ def test_uniforms_and_named_streams_per_path(rocm, nt, mode):
     assert rel_err(sums, ref, floor=1e-300) <= 1e-10
 
 
+@pytest.mark.parametrize("seed", [301, 302, 303])
+def test_random_tapes_every_operation_on_device(rocm, nt, seed):
+    """Straight-line tapes of random shape using every operation, normals on
+    two streams and uniforms (conftest.random_tape), one output: per path and
+    summed against the oracle in both sweeps. At 250 steps (over 512 nodes)
+    the reverse sweep cuts the tape into checkpointed segments."""
+    from conftest import random_tape
+    for steps in (120, 250):
+        flat = random_tape(nt, seed, steps, outputs=1).flat()
+        for mode in (2, 1):
+            print(f"case random tape seed={seed} steps={steps} mode={mode}", flush=True)
+            with rocm.Executable(flat, rocm.options("fp64", mode=mode)) as x:
+                info = x.info()
+                assert info["scratch_bytes"] == 0 and info["mode"] == mode
+                assert (info["n_segments"] > 0) == (mode == 1 and steps == 250)
+                v, g = x.replay_paths(1024, OFFSET, 42)
+                sums, _ = x.replay(100_000, 0, 42)
+            check_per_path(v, g, flat, 1024, OFFSET, 42, max_above=0.0)
+            assert rel_err(sums, oracle.replay_sums(flat, 100_000, 0, 42), floor=1e-300) <= 1e-10
+
+
 def test_multi_output_per_path_and_sums(rocm, nt):
     from conftest import two_output_tape
     flat = two_output_tape(nt).flat()
