@@ -78,6 +78,56 @@ def test_other_workloads_print_one_line(patched, monkeypatch, capsys, workload):
     assert out["value"] > 0
 
 
+def test_measure_prices_the_roofline_from_the_replay_kernel_time(monkeypatch):
+    """bench.measure with a stand-in executable on the Asian call's default
+    plan: achieved = NT-FLOP per scenario x scenarios / the replay kernel's
+    mean event time, frac = achieved / the fp64 peak, algorithmic bytes = the
+    inputs plus one partial per channel and block, and traffic and executed
+    FLOPs from the committed counter summary of that kernel."""
+    import numpy as np
+
+    from nablatensor_amd import rocm
+
+    flat = bench.workload_tape("C2")
+
+    class FakeExecutable:
+        def __init__(self, flat, opts):
+            self.n = len(flat["input_node"])
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *exc):
+            return False
+
+        def info(self):
+            return {"vgprs": 84, "sgprs": 86, "scratch_bytes": 0, "lds_bytes": 18688, "loop_period": 6,
+                    "loop_iters": 252, "seg_len": 2, "n_segments": 126, "checkpoint": 0, "tape_slots": 0,
+                    "grid_cap": 10240, "mode": 2}
+
+        def grid(self, paths):
+            return 4096, 256
+
+        def source(self):
+            return "// nt-cost: forward=13656 reverse=16688 tangent=4586\n"
+
+        def replay(self, paths, offset, seed):
+            return np.zeros(2 + self.n), {"kernel_ms": 0.81, "wall_ms": 0.85, "replay_ms": 0.8}
+
+    monkeypatch.setattr(rocm, "Executable", FakeExecutable)
+    out = bench.measure(rocm, flat, "fp64", 2_000_000, 3, 1, 42, 0, 0, ramp=0.0, workload="C2")
+    r = out["roofline"]
+    assert out["replay_kernel_ms"] == pytest.approx(0.8) and out["kernel_ms"] == pytest.approx(0.81)
+    assert r["flops_per_scenario"] == 18_723 and r["peak"] == 78.6
+    assert r["achieved"] == pytest.approx(18_723 * 2e6 / 0.8e-3 / 1e12)
+    assert r["frac"] == pytest.approx(r["achieved"] / 78.6)
+    assert r["algorithmic_bytes"] == 8 * (5 + 4096 * 7)
+    assert r["traffic"] is not None and r["traffic_source"].endswith("nt_replay_asian252_fp64_counters.md")
+    assert r["executed_flops_per_scenario"] > 0
+    assert r["executed_frac"] == pytest.approx(r["executed_flops_per_scenario"] * 2e6 / 0.8e-3 / 1e12 / 78.6)
+    assert out["kernel"]["grid"] == 4096 and out["kernel"]["mode"] == "tangent"
+
+
 def test_risk_run_line(patched, monkeypatch, capsys):
     """--risk-run adds the raw sums of every launch (launch k over scenarios
     k x 10^6 onwards) and reports the time and the 10^10-scenario result."""
