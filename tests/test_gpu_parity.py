@@ -142,6 +142,27 @@ def test_dispatch_split_is_additive(rocm, tapes):
     assert rel_err(first + second, whole, floor=1e-300) <= 1e-12
 
 
+def test_one_dispatch_of_more_than_2_pow_32_paths(rocm, tapes):
+    """The European call over 5 x 10^9 paths in one dispatch (a path count
+    and path indices past 2^32, about 1,600 paths per lane on the capped grid)
+    equals two dispatches of half as many each to 1e-12, and its price is
+    Black-Scholes' within four standard errors."""
+    from scipy.stats import norm
+
+    n = 5_000_000_000
+    print(f"case C1 one dispatch of {n} paths", flush=True)
+    with rocm.Executable(tapes["C1"], rocm.options("fp64")) as x:
+        whole, _ = x.replay(n, 0, 42)
+        first, _ = x.replay(n // 2, 0, 42)
+        second, _ = x.replay(n // 2, n // 2, 42)
+    assert rel_err(first + second, whole, floor=1e-300) <= 1e-12
+    res = oracle.to_result(whole, n)
+    s0, k, vol, r, t = 100.0, 100.0, 0.2, 0.03, 1.0
+    d1 = (np.log(s0 / k) + (r + 0.5 * vol * vol) * t) / (vol * np.sqrt(t))
+    bs = s0 * norm.cdf(d1) - k * np.exp(-r * t) * norm.cdf(d1 - vol * np.sqrt(t))
+    assert abs(res["price"] - bs) <= 4 * res["stderr"], (res["price"], bs, res["stderr"])
+
+
 def test_worst_of_launches_past_2_pow_32_are_additive(rocm, tapes):
     """The worst-of risk run (launch k over scenarios [k 10^6, (k + 1) 10^6))
     reaches counter offsets past 2^32 from launch 4,295 on. Launches 4,294
