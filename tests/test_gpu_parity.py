@@ -134,6 +134,35 @@ def test_run_to_run_bit_identity(rocm, tapes):
     assert np.array_equal(a, b)
 
 
+def test_executables_on_two_threads(rocm, tapes):
+    """Two executables, each with its own stream and buffers, created and
+    replayed from two threads at once (the library call releases the
+    interpreter lock): each thread's sums equal the same replays made one
+    after another, bit for bit."""
+    import threading
+
+    jobs = {"C2": 200_000, "C3": 100_000}
+
+    def run(name, out):
+        with rocm.Executable(tapes[name], rocm.options("fp64")) as x:
+            out[name] = [x.replay(jobs[name], k * jobs[name], 42)[0] for k in range(5)]
+
+    print("case two threads C2 and C3", flush=True)
+    seq, par = {}, {}
+    for name in jobs:
+        run(name, seq)
+    threads = [threading.Thread(target=run, args=(name, par)) for name in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads)
+    for name in jobs:
+        assert name in par, name
+        for a, b in zip(seq[name], par[name]):
+            assert np.array_equal(a, b), name
+
+
 def test_dispatch_split_is_additive(rocm, tapes):
     with rocm.Executable(tapes["C2"], rocm.options("fp64")) as x:
         whole, _ = x.replay(100_000, 0, 7)
